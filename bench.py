@@ -1,0 +1,154 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen3 decoder token loop on one MI355X.
+
+Metric: decode tok/s at batch 1 + achieved fraction of the
+HBM roofline; prefill tok/s reported alongside.  Workload (default, configs[0]
+= C1): Qwen3-ASR-0.6B decoder, random-init bf16 weights N(0, 0.02) with
+all-ones norms (seed 0), 390 synthetic audio rows N(0,1) + 12 random prompt
+ids; prefill 401 rows, forward the last row, then greedy decode.  A "step" is
+one greedy decode forward (one token); K timed steps start at the C1
+positions (402 ..), fed back on the device (qwen_hip_decoder_generate).
+
+Roofline: the decode step is the unit launched per token; its algorithmic
+bytes (bf16 weights + LM head + fp32 norms + fp32 K/V read + K/V write, from
+qwen_hip_decoder_step_bytes) divided by the step's GPU time, measured with
+HIP events on the decoder's own stream around the timed steps.
+
+CPU baseline: the reference decoder compiled from its sources (oracle/_ref,
+-O3 -ffast-math, no BLAS) on a bounded sample of the same workload, timed on
+this host's cores.
+"""
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+WORKLOADS = {
+    "c1": dict(model_b=0, n_audio=390, n_ids=12,
+               desc="C1 Qwen3-ASR-0.6B decoder token loop: 390 audio rows + 12 ids, prefill 401, greedy decode"),
+    "c3": dict(model_b=1, n_audio=1500, n_ids=16,
+               desc="C3 Qwen3-ASR-1.7B decoder: 1500 audio rows + 16 ids, prefill 1515, greedy decode"),
+    "c4": dict(model_b=0, n_audio=8192, n_ids=0,
+               desc="C4 0.6B long context: prefill 8191 audio rows, greedy decode over up to 8.7k positions"),
+}
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(wl, rows, first_token, threads, decode_steps):
+    """Reference decoder (oracle/_ref) on this host: prefill of the same rows
+    and `decode_steps` greedy forwards from the same first token."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as P
+    if not P.ref_available():
+        return None
+    cfg = P.CFG_17B if wl["model_b"] else P.CFG_06B
+    t0 = time.time()
+    m = P.SynthModel(cfg, seed=0)
+    r = P.RefModel(m, threads=threads)
+    log(f"[cpu] weights generated in {time.time() - t0:.1f}s; prefill {rows.shape[0] - 1} rows on {threads} threads")
+    tp = r.time_prefill(rows[:-1])
+    tok, _, _ = r.forward(rows[-1])
+    toks, td = r.generate(first_token, decode_steps)
+    log(f"[cpu] prefill {tp:.1f}s, {decode_steps} decode steps {td:.2f}s (first token {tok})")
+    return {"value": round(decode_steps / td, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "prefill_tok_s": round((rows.shape[0] - 1) / tp, 2),
+            "sample": f"reference decoder (oracle/_ref, no BLAS) on the same weights/rows: prefill "
+                      f"{rows.shape[0] - 1} rows, then {decode_steps} greedy decode steps; decode tok/s over those steps",
+            "first_token_matches_gpu": bool(tok == first_token)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c1")
+    ap.add_argument("--engine", type=int, default=None, help="0 graph of fused kernels, 1 eager")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=48)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (one decoder context per GPU; "
+              "see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    qa = importlib.import_module("qwen-asr_amd")
+    wl = WORKLOADS[args.workload]
+    cfg = qa.preset(wl["model_b"])
+    n_rows = wl["n_audio"] + wl["n_ids"]
+    K, W = args.steps, args.warmup
+    d = qa.Decoder(cfg, 0, n_rows + K + W + 1024)
+    if args.engine is not None:
+        d.set_engine(args.engine)
+    t0 = time.time()
+    d.load_synthetic(0, 0.02, 0.0)
+    rows, ids, emb = qa.prompt_rows(cfg, wl["n_audio"], wl["n_ids"])
+    log(f"[gpu] {args.workload}: weights generated+uploaded in {time.time() - t0:.1f}s; {n_rows} input rows")
+    stream = torch.cuda.ExternalStream(d.stream())
+
+    # prefill (one untimed pass, then timed)
+    d.prefill(rows[:-1])
+    d.set_kv_len(0)
+    torch.cuda.synchronize()
+    tp0 = time.perf_counter()
+    d.prefill(rows[:-1])
+    prefill_s = time.perf_counter() - tp0
+    first = d.forward(rows[-1])
+    base = d.kv_len()
+    log(f"[gpu] prefill {n_rows - 1} rows in {prefill_s * 1e3:.2f} ms; first token {first}")
+
+    d.generate(first, W)
+    d.set_kv_len(base)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    tw0 = time.perf_counter()
+    toks = d.generate(first, K)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - tw0
+    gpu_ms = e0.elapsed_time(e1)
+    value = K / wall
+    step_bytes = [d.step_bytes(base + i) for i in range(K)]
+    avg_bytes = float(np.mean(step_bytes))
+    achieved = avg_bytes / (gpu_ms * 1e-3 / K) / 1e9
+    log(f"[gpu] decode {K} steps: wall {wall * 1e3:.2f} ms ({value:.1f} tok/s), events {gpu_ms:.2f} ms; "
+        f"{avg_bytes / 1e9:.4f} GB/step -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        cpu = cpu_baseline(wl, rows, first, threads, args.cpu_steps)
+
+    out = {
+        "metric": "decode tok/s at batch 1 (0.6B, 1.7B) + % of peak HBM GB/s; prefill tok/s",
+        "value": round(value, 3), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": wl["desc"], "batch": 1, "weights": "bf16 N(0,0.02) seed 0, norms 1.0",
+                   "activations": "fp32, fp32 accumulation", "kv_cache": "fp32",
+                   "prefill_rows": n_rows - 1, "decode_positions": [base, base + K - 1]},
+        "prefill_tok_s": round((n_rows - 1) / prefill_s, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode step (one token: all layers + LM head argmax)",
+                     "bytes_per_launch": round(avg_bytes), "launch_us": round(gpu_ms * 1e3 / K, 3)},
+        "cpu_baseline": cpu,
+        "tokens_head": [int(first)] + [int(t) for t in toks[:7]],
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

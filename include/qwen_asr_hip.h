@@ -1,0 +1,219 @@
+/*
+ * qwen_asr_hip.h - C ABI of the MI355X (gfx950) Qwen3 decoder token loop.
+ *
+ * This is the drop-in boundary for the reference's decoder hot path:
+ *   - the decoder-level entry points replace qwen_decoder_prefill /
+ *     qwen_decoder_forward (reference qwen_asr.h:313-317,
+ *     qwen_asr_decoder.c:262 and :388) and the KV-length bookkeeping the
+ *     callers do on ctx->kv_cache_len (qwen_asr.c:704, :1764);
+ *   - the op-level entry points replace the operators of qwen_asr_kernels.h
+ *     that the decoder calls, with the same argument meaning, but on DEVICE
+ *     pointers and with a HIP stream (NULL = the legacy default stream).
+ *
+ * Plain C: no C++ or torch types cross this boundary.  Every function that can
+ * fail returns 0 on success and a negative QWEN_HIP_E* code otherwise, except
+ * where noted; qwen_hip_last_error() gives the message of the last failure on
+ * the calling thread.  qwen_hip_decoder_forward keeps the reference
+ * convention of returning QWEN_TOKEN_IM_END (151645) when it cannot run
+ * (reference qwen_asr_decoder.c:417, :421).
+ *
+ * Numerics: bf16 weights (raw uint16 bit patterns, as the reference's
+ * uint16_t *W_bf16), fp32 activations, fp32 accumulation, fp32 KV cache.
+ */
+#ifndef QWEN_ASR_HIP_H
+#define QWEN_ASR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#include "qwen_synth.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------
+ * Constants (reference qwen_asr.h:23, :30-36)
+ * ------------------------------------------------------------------------ */
+#define QWEN_HIP_VOCAB_SIZE        151936
+#define QWEN_HIP_TOKEN_ENDOFTEXT   151643
+#define QWEN_HIP_TOKEN_IM_END      151645
+#define QWEN_HIP_MAX_LAYERS        28          /* QWEN_MAX_DEC_LAYERS, qwen_asr.h:27 */
+#define QWEN_HIP_HEAD_DIM          128         /* the only head size the kernels build for */
+
+#define QWEN_HIP_OK          0
+#define QWEN_HIP_EINVAL     -1    /* bad argument / shape the kernels do not support */
+#define QWEN_HIP_ENOMEM     -2    /* device or host allocation failed */
+#define QWEN_HIP_EDEVICE    -3    /* a HIP runtime call failed */
+#define QWEN_HIP_ESTATE     -4    /* call out of order (e.g. forward before weights) */
+
+/* ------------------------------------------------------------------------
+ * Model configuration: the decoder fields of qwen_config_t
+ * (reference qwen_asr.h:60-68; values set by detect_config, qwen_asr.c:135-191)
+ * ------------------------------------------------------------------------ */
+typedef struct {
+    int hidden;          /* dec_hidden: 1024 (0.6B) or 2048 (1.7B) */
+    int layers;          /* dec_layers: 28 */
+    int heads;           /* dec_heads: 16 */
+    int kv_heads;        /* dec_kv_heads: 8 */
+    int head_dim;        /* dec_head_dim: 128 */
+    int intermediate;    /* dec_intermediate: 3072 or 6144 */
+    int vocab;           /* vocab_size: 151936 */
+    float rms_eps;       /* dec_rms_norm_eps: 1e-6 */
+    float rope_theta;    /* dec_rope_theta: 1e6 */
+} qwen_hip_config;
+
+/* Fill cfg with the reference's 0.6B (model_b = 0) or 1.7B (model_b = 1)
+ * decoder shape (qwen_asr.c:153-186). */
+void qwen_hip_config_preset(qwen_hip_config *cfg, int model_b);
+
+/* Host-side weights of one decoder layer, as qwen_dec_layer_t holds them
+ * (reference qwen_asr.h:131-153): bf16 matrices row-major [out][in],
+ * fp32 norm vectors. */
+typedef struct {
+    const uint16_t *wq;              /* [heads*head_dim][hidden] */
+    const uint16_t *wk;              /* [kv_heads*head_dim][hidden] */
+    const uint16_t *wv;              /* [kv_heads*head_dim][hidden] */
+    const uint16_t *wo;              /* [hidden][heads*head_dim] */
+    const uint16_t *gate;            /* [intermediate][hidden] */
+    const uint16_t *up;              /* [intermediate][hidden] */
+    const uint16_t *down;            /* [hidden][intermediate] */
+    const float *q_norm;             /* [head_dim] */
+    const float *k_norm;             /* [head_dim] */
+    const float *input_norm;         /* [hidden] */
+    const float *post_attn_norm;     /* [hidden] */
+} qwen_hip_layer_weights;
+
+/* ------------------------------------------------------------------------
+ * Decoder-level ABI (the timed path)
+ * ------------------------------------------------------------------------ */
+typedef struct qwen_hip_decoder qwen_hip_decoder;
+
+/* Create a decoder context on HIP device `device` with room for
+ * `kv_capacity` cached positions (grown by doubling when exceeded, as
+ * kv_cache_grow does, qwen_asr_decoder.c:133-160).  Returns NULL on failure. */
+qwen_hip_decoder *qwen_hip_decoder_create(const qwen_hip_config *cfg, int device,
+                                          int kv_capacity);
+void qwen_hip_decoder_destroy(qwen_hip_decoder *dec);
+
+/* Upload weights (replaces qwen_decoder_load, qwen_asr_decoder.c:45-116:
+ * the gate/up rows are interleaved [g0,u0,g1,u1,...] as :95-107 does, and
+ * Wq|Wk|Wv are concatenated so one GEMV pass streams all three). */
+int qwen_hip_decoder_load_layer(qwen_hip_decoder *dec, int layer,
+                                const qwen_hip_layer_weights *w);
+int qwen_hip_decoder_load_embeddings(qwen_hip_decoder *dec,
+                                     const uint16_t *tok_embeddings, /* [vocab][hidden] */
+                                     const float *final_norm);       /* [hidden] */
+
+/* Generate the seeded synthetic model directly (host generation with
+ * qwen_synth_*, then upload).  norm_std = 0 gives the all-ones norms the
+ * benchmark configs prescribe; norm_std > 0 draws 1 + norm_std*N(0,1). */
+int qwen_hip_decoder_load_synthetic(qwen_hip_decoder *dec, uint64_t seed,
+                                    double weight_std, double norm_std);
+
+/* qwen_decoder_prefill (qwen_asr_decoder.c:262-359): run `seq_len` fp32 rows
+ * [seq_len][hidden] through all layers starting at position kv_len, append
+ * their K/V, advance kv_len.  `rows` is a HOST pointer; the _device variant
+ * takes a device pointer.  Produces no token. */
+int qwen_hip_decoder_prefill(qwen_hip_decoder *dec, const float *rows, int seq_len);
+int qwen_hip_decoder_prefill_device(qwen_hip_decoder *dec, const float *d_rows, int seq_len);
+
+/* qwen_decoder_forward (qwen_asr_decoder.c:388-476): one fp32 row (HOST
+ * pointer) at position kv_len; returns the greedy token (argmax of the tied
+ * LM head over the final-normed hidden state, lowest index on ties), or
+ * QWEN_HIP_TOKEN_IM_END on failure. */
+int qwen_hip_decoder_forward(qwen_hip_decoder *dec, const float *row);
+
+/* Same step with the input row gathered on the device from the embedding
+ * table (tok_embed_bf16_to_f32, qwen_asr.c:353-360, fused into the step). */
+int qwen_hip_decoder_forward_token(qwen_hip_decoder *dec, int token);
+
+/* The greedy loop of qwen_asr.c:729-759 kept on the device: starting from
+ * `first_token`, run n_steps forwards, each fed the previous step's argmax,
+ * with no host round trip per token.  Writes the n_steps produced tokens to
+ * out_tokens (host).  stop_on_eos != 0 truncates at the first
+ * <|endoftext|>/<|im_end|> (reference :733) and returns the count kept;
+ * otherwise returns n_steps.  Negative on error. */
+int qwen_hip_decoder_generate(qwen_hip_decoder *dec, int first_token, int n_steps,
+                              int *out_tokens, int stop_on_eos);
+
+/* KV bookkeeping: ctx->kv_cache_len.  set_kv_len accepts 0..kv_len and is
+ * the rollback used by streaming reuse (qwen_asr.c:1764). */
+int qwen_hip_decoder_kv_len(const qwen_hip_decoder *dec);
+int qwen_hip_decoder_set_kv_len(qwen_hip_decoder *dec, int kv_len);
+
+/* Validation taps.  read_hidden copies the final-normed hidden state of the
+ * last forward (the reference's ctx->dec_x after :474) to host [hidden].
+ * With keep_logits on, every forward also writes its full fp32 logits
+ * [vocab], readable with read_logits (costs one extra vocab-sized write). */
+int qwen_hip_decoder_set_keep_logits(qwen_hip_decoder *dec, int on);
+int qwen_hip_decoder_read_hidden(qwen_hip_decoder *dec, float *out);
+int qwen_hip_decoder_read_logits(qwen_hip_decoder *dec, float *out);
+
+/* Decode-step engine: 0 = one kernel per fused op, replayed from a HIP graph
+ * (default); 1 = same kernels launched eagerly (no graph). */
+int qwen_hip_decoder_set_engine(qwen_hip_decoder *dec, int engine);
+
+/* The stream the decoder launches on (for event timing by callers). */
+hipStream_t qwen_hip_decoder_stream(const qwen_hip_decoder *dec);
+
+/* Per-step algorithmic HBM bytes of one forward at cache length kv_len
+ * (weights + LM head + fp32 norms + K/V read + K/V write). */
+double qwen_hip_decoder_step_bytes(const qwen_hip_decoder *dec, int kv_len);
+
+const char *qwen_hip_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Op-level ABI: the qwen_asr_kernels.h operators on device pointers.
+ * Same argument order and meaning as the reference, plus a stream.
+ * ------------------------------------------------------------------------ */
+
+/* qwen_add_inplace (qwen_asr_kernels.h:18): a[i] += b[i] */
+int qwen_hip_add_inplace(float *a, const float *b, int n, hipStream_t s);
+
+/* qwen_rms_norm (qwen_asr_kernels.h:80): out = x * w / sqrt(mean(x^2)+eps);
+ * out may equal x. */
+int qwen_hip_rms_norm(float *out, const float *x, const float *w,
+                      int seq_len, int hidden, float eps, hipStream_t s);
+
+/* qwen_rms_norm_per_head (qwen_asr_kernels.h:86): in place per head_dim slice */
+int qwen_hip_rms_norm_per_head(float *x, const float *w, int seq_len, int n_heads,
+                               int head_dim, float eps, hipStream_t s);
+
+/* qwen_apply_rope_neox (qwen_asr_kernels.h:151): in place, cos/sin [seq][head_dim] */
+int qwen_hip_apply_rope_neox(float *x, const float *cos_vals, const float *sin_vals,
+                             int seq_len, int n_heads, int head_dim, hipStream_t s);
+
+/* qwen_swiglu_multiply (qwen_asr_kernels.h:97): out[s][j] = silu(gu[s][2j]) * gu[s][2j+1];
+ * out may equal gate_up. */
+int qwen_hip_swiglu_multiply(float *out, const float *gate_up, int seq_len,
+                             int intermediate, hipStream_t s);
+
+/* qwen_linear_nobias_bf16 (qwen_asr_kernels.h:41): y[seq][out] = x[seq][in] W^T.
+ * seq_len == 1 runs the bandwidth-bound GEMV; seq_len > 1 the MFMA GEMM. */
+int qwen_hip_linear_nobias_bf16(float *y, const float *x, const uint16_t *W_bf16,
+                                int seq_len, int in_dim, int out_dim, hipStream_t s);
+
+/* qwen_linear_nobias_bf16_qkv (qwen_asr_kernels.h:45): the three seq=1 matvecs */
+int qwen_hip_linear_nobias_bf16_qkv(float *q, float *k, float *v, const float *x,
+                                    const uint16_t *Wq_bf16, const uint16_t *Wk_bf16,
+                                    const uint16_t *Wv_bf16, int in_dim, int q_dim,
+                                    int kv_dim, hipStream_t s);
+
+/* qwen_causal_attention (qwen_asr_kernels.h:123): Q [seq_q][n_heads*hd],
+ * K/V [seq_k][n_kv_heads*hd] (the reference's row layout), out like Q. */
+int qwen_hip_causal_attention(float *out, const float *Q, const float *K, const float *V,
+                              int seq_q, int seq_k, int n_heads, int n_kv_heads,
+                              int head_dim, float scale, int q_offset, hipStream_t s);
+
+/* qwen_argmax_matvec_bf16 (qwen_asr_kernels.h:156): index of the largest
+ * W[o]·x, lowest index on exact ties.  Synchronous like the reference:
+ * returns the index (>= 0) or a negative error code. */
+int qwen_hip_argmax_matvec_bf16(const float *x, const uint16_t *W_bf16,
+                                int in_dim, int out_dim, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWEN_ASR_HIP_H */

@@ -1,0 +1,260 @@
+"""qwen-asr_amd: the Qwen3-ASR decoder token loop on MI355X (gfx950).
+
+The product is the C-ABI library ``libqwen_asr_hip.so`` (declared in
+``include/qwen_asr_hip.h``): hand-written HIP kernels plus C host code.  This
+module is only a thin ctypes view of that ABI for tests, ``bench.py`` and
+``__graft_entry__``; it has no compute of its own and no fallback: if the
+library is missing, loading fails loudly.
+
+The directory name is not a Python identifier, so import it with
+``importlib.import_module("qwen-asr_amd")``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqwen_asr_hip.so")
+
+QWEN_HIP_TOKEN_ENDOFTEXT = 151643
+QWEN_HIP_TOKEN_IM_END = 151645
+ERRORS = {0: "OK", -1: "EINVAL", -2: "ENOMEM", -3: "EDEVICE", -4: "ESTATE"}
+
+
+class HipConfig(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("layers", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("intermediate", C.c_int), ("vocab", C.c_int),
+                ("rms_eps", C.c_float), ("rope_theta", C.c_float)]
+
+
+class LayerWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down",
+                                          "q_norm", "k_norm", "input_norm", "post_attn_norm")]
+
+
+def build(jobs=8):
+    """Compile the library in-tree (hipcc for gfx950 + gcc)."""
+    subprocess.run(["make", "-s", "-C", HERE, f"-j{jobs}"], check=True)
+
+
+_lib = None
+
+# (name, restype, argtypes) of every exported entry point of include/qwen_asr_hip.h
+_vp, _i, _f, _d, _u64 = C.c_void_p, C.c_int, C.c_float, C.c_double, C.c_uint64
+SIGNATURES = [
+    ("qwen_hip_config_preset", None, [_vp, _i]),
+    ("qwen_hip_decoder_create", _vp, [_vp, _i, _i]),
+    ("qwen_hip_decoder_destroy", None, [_vp]),
+    ("qwen_hip_decoder_load_layer", _i, [_vp, _i, _vp]),
+    ("qwen_hip_decoder_load_embeddings", _i, [_vp, _vp, _vp]),
+    ("qwen_hip_decoder_load_synthetic", _i, [_vp, _u64, _d, _d]),
+    ("qwen_hip_decoder_prefill", _i, [_vp, _vp, _i]),
+    ("qwen_hip_decoder_prefill_device", _i, [_vp, _vp, _i]),
+    ("qwen_hip_decoder_forward", _i, [_vp, _vp]),
+    ("qwen_hip_decoder_forward_token", _i, [_vp, _i]),
+    ("qwen_hip_decoder_generate", _i, [_vp, _i, _i, _vp, _i]),
+    ("qwen_hip_decoder_kv_len", _i, [_vp]),
+    ("qwen_hip_decoder_set_kv_len", _i, [_vp, _i]),
+    ("qwen_hip_decoder_set_keep_logits", _i, [_vp, _i]),
+    ("qwen_hip_decoder_read_hidden", _i, [_vp, _vp]),
+    ("qwen_hip_decoder_read_logits", _i, [_vp, _vp]),
+    ("qwen_hip_decoder_set_engine", _i, [_vp, _i]),
+    ("qwen_hip_decoder_stream", _vp, [_vp]),
+    ("qwen_hip_decoder_step_bytes", _d, [_vp, _i]),
+    ("qwen_hip_last_error", C.c_char_p, []),
+    ("qwen_hip_add_inplace", _i, [_vp, _vp, _i, _vp]),
+    ("qwen_hip_rms_norm", _i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    ("qwen_hip_rms_norm_per_head", _i, [_vp, _vp, _i, _i, _i, _f, _vp]),
+    ("qwen_hip_apply_rope_neox", _i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    ("qwen_hip_swiglu_multiply", _i, [_vp, _vp, _i, _i, _vp]),
+    ("qwen_hip_linear_nobias_bf16", _i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    ("qwen_hip_linear_nobias_bf16_qkv", _i, [_vp] * 7 + [_i, _i, _i, _vp]),
+    ("qwen_hip_causal_attention", _i, [_vp] * 4 + [_i] * 5 + [_f, _i, _vp]),
+    ("qwen_hip_argmax_matvec_bf16", _i, [_vp, _vp, _i, _i, _vp]),
+    ("qwen_synth_key", _u64, [_u64, _u64]),
+    ("qwen_f32_to_bf16_rne", C.c_uint16, [_f]),
+    ("qwen_synth_normal_bf16", None, [_vp, C.c_size_t, _u64, _u64, _d, _d, _i]),
+    ("qwen_synth_normal_f32", None, [_vp, C.c_size_t, _u64, _u64, _d, _d, _i]),
+    ("qwen_synth_uniform_f32", None, [_vp, C.c_size_t, _u64, _u64, _d, _d, _i]),
+    ("qwen_synth_tokens", None, [_vp, C.c_size_t, _u64, _u64, _i]),
+    ("qwen_checksum_u16", _u64, [_vp, C.c_size_t]),
+]
+
+
+def lib():
+    """Load libqwen_asr_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() (no CPU fallback exists)")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error():
+    return lib().qwen_hip_last_error().decode(errors="replace")
+
+
+def check(rc, what=""):
+    if rc < 0:
+        raise RuntimeError(f"{what}: {ERRORS.get(rc, rc)}: {last_error()}")
+    return rc
+
+
+def preset(model_b=0):
+    c = HipConfig()
+    lib().qwen_hip_config_preset(C.byref(c), model_b)
+    return c
+
+
+def config_from(cfg):
+    """HipConfig from any object with hidden/layers/heads/kv_heads/head_dim/intermediate/vocab/eps/theta."""
+    return HipConfig(cfg.hidden, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.intermediate,
+                     cfg.vocab, cfg.eps, cfg.theta)
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------------------
+# seeded synthetic inputs (csrc/host/synth.c; tensor ids of include/qwen_synth.h)
+# ---------------------------------------------------------------------------
+SYNTH_EMBED = 1
+
+
+def synth_bf16(n, seed, tensor_id, std=0.02):
+    out = np.empty(n, np.uint16)
+    lib().qwen_synth_normal_bf16(_ptr(out), n, seed, tensor_id, 0.0, std, 0)
+    return out
+
+
+def synth_f32(n, seed, tensor_id, std=1.0, mean=0.0):
+    out = np.empty(n, np.float32)
+    lib().qwen_synth_normal_f32(_ptr(out), n, seed, tensor_id, mean, std, 0)
+    return out
+
+
+def synth_tokens(n, seed, tensor_id, n_ids=151643):
+    out = np.empty(n, np.int32)
+    lib().qwen_synth_tokens(_ptr(out), n, seed, tensor_id, n_ids)
+    return out
+
+
+def bf16_to_f32(a):
+    return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def prompt_rows(cfg, n_audio, n_ids, seed=0, audio_chunk=0, token_set=0, emb=None):
+    """The benchmark input rows: ids[:n/2] || n_audio rows N(0,1) || ids[n/2:]
+    (the prefix/audio/suffix template of the reference, qwen_asr.c:339-347,
+    with synthetic ids).  emb: the [vocab][hidden] bf16 table, regenerated
+    from the seed when not given."""
+    ids = synth_tokens(n_ids, seed, 600000 + token_set, min(151643, cfg.vocab))
+    if emb is None:
+        emb = synth_bf16(cfg.vocab * cfg.hidden, seed, SYNTH_EMBED).reshape(cfg.vocab, cfg.hidden)
+    audio = synth_f32(n_audio * cfg.hidden, seed, 500000 + audio_chunk).reshape(n_audio, cfg.hidden)
+    head = bf16_to_f32(emb[ids[: n_ids // 2]]).reshape(-1, cfg.hidden)
+    tail = bf16_to_f32(emb[ids[n_ids // 2:]]).reshape(-1, cfg.hidden)
+    return np.ascontiguousarray(np.concatenate([head, audio, tail]), np.float32), ids, emb
+
+
+class Decoder:
+    """One decoder context on one GPU (the decoder-level ABI)."""
+
+    def __init__(self, cfg: HipConfig, device=0, kv_capacity=1024):
+        self.cfg = cfg
+        self.h = lib().qwen_hip_decoder_create(C.byref(cfg), device, kv_capacity)
+        if not self.h:
+            raise RuntimeError(f"qwen_hip_decoder_create: {last_error()}")
+
+    # weights -------------------------------------------------------------
+    def load_synthetic(self, seed=0, weight_std=0.02, norm_std=0.0):
+        check(lib().qwen_hip_decoder_load_synthetic(self.h, seed, weight_std, norm_std), "load_synthetic")
+
+    def load_layer(self, l, wq, wk, wv, wo, gate, up, down, q_norm, k_norm, input_norm, post_attn_norm):
+        arrs = [np.ascontiguousarray(a) for a in (wq, wk, wv, wo, gate, up, down)]
+        arrs += [np.ascontiguousarray(a, np.float32) for a in (q_norm, k_norm, input_norm, post_attn_norm)]
+        w = LayerWeights(*[a.ctypes.data for a in arrs])
+        check(lib().qwen_hip_decoder_load_layer(self.h, l, C.byref(w)), f"load_layer {l}")
+
+    def load_embeddings(self, emb, final_norm):
+        emb = np.ascontiguousarray(emb, np.uint16)
+        fn = np.ascontiguousarray(final_norm, np.float32)
+        check(lib().qwen_hip_decoder_load_embeddings(self.h, _ptr(emb), _ptr(fn)), "load_embeddings")
+
+    def load_model(self, model):
+        """Upload a host model object exposing layer_args(l), emb, final_norm."""
+        for l in range(self.cfg.layers):
+            self.load_layer(l, *model.layer_args(l))
+        self.load_embeddings(model.emb, model.final_norm)
+
+    # token loop ----------------------------------------------------------
+    def prefill(self, rows):
+        rows = np.ascontiguousarray(rows, np.float32)
+        n = rows.size // self.cfg.hidden
+        check(lib().qwen_hip_decoder_prefill(self.h, _ptr(rows), n), "prefill")
+
+    def prefill_device(self, ptr, n):
+        check(lib().qwen_hip_decoder_prefill_device(self.h, C.c_void_p(ptr), n), "prefill_device")
+
+    def forward(self, row):
+        row = np.ascontiguousarray(row, np.float32)
+        return lib().qwen_hip_decoder_forward(self.h, _ptr(row))
+
+    def forward_token(self, token):
+        return lib().qwen_hip_decoder_forward_token(self.h, int(token))
+
+    def generate(self, first_token, n_steps, stop_on_eos=False):
+        out = np.empty(max(n_steps, 1), np.int32)
+        k = check(lib().qwen_hip_decoder_generate(self.h, int(first_token), int(n_steps), _ptr(out),
+                                                  1 if stop_on_eos else 0), "generate")
+        return out[:k]
+
+    def kv_len(self):
+        return lib().qwen_hip_decoder_kv_len(self.h)
+
+    def set_kv_len(self, n):
+        check(lib().qwen_hip_decoder_set_kv_len(self.h, int(n)), "set_kv_len")
+
+    def set_keep_logits(self, on):
+        check(lib().qwen_hip_decoder_set_keep_logits(self.h, 1 if on else 0), "set_keep_logits")
+
+    def set_engine(self, engine):
+        check(lib().qwen_hip_decoder_set_engine(self.h, int(engine)), "set_engine")
+
+    def read_hidden(self):
+        out = np.empty(self.cfg.hidden, np.float32)
+        check(lib().qwen_hip_decoder_read_hidden(self.h, _ptr(out)), "read_hidden")
+        return out
+
+    def read_logits(self):
+        out = np.empty(self.cfg.vocab, np.float32)
+        check(lib().qwen_hip_decoder_read_logits(self.h, _ptr(out)), "read_logits")
+        return out
+
+    def stream(self):
+        return lib().qwen_hip_decoder_stream(self.h)
+
+    def step_bytes(self, kv_len):
+        return lib().qwen_hip_decoder_step_bytes(self.h, int(kv_len))
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().qwen_hip_decoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,683 @@
+/*
+ * decoder.c - host side of the Qwen3 decoder token loop on one MI355X.
+ *
+ * Mirrors the reference decoder (qwen_asr_decoder.c) with every tensor
+ * resident in HBM:
+ *   weights     per layer Wqkv [q_dim+2*kv_dim][hidden] (Wq|Wk|Wv stacked so
+ *               one GEMV streams all three, as the fused-dispatch
+ *               qwen_linear_nobias_bf16_qkv does, qwen_asr_kernels.c:434-460),
+ *               Wo, Wgu [2*inter][hidden] with rows interleaved g0,u0,g1,u1
+ *               (qwen_asr_decoder.c:95-107), Wdown; tied embedding / LM head.
+ *   KV cache    fp32 like the reference (:122-131) but laid out
+ *               [layer][kv_head][position][128] so one head's keys stream
+ *               contiguously; grown by doubling (:133-160).
+ *   RoPE table  fp32 cos/sin [position][128] from the reference's formulas
+ *               (:207-256), computed on the host once per capacity.
+ * The decode step is a fixed kernel sequence whose only per-step state lives
+ * in device memory (position, input token), so it is captured once into a
+ * HIP graph and replayed; generate() replays it n times with no host round
+ * trip per token.
+ */
+#include "host_internal.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
+
+static __thread char g_err[512];
+
+void qk_set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+const char *qwen_hip_last_error(void) { return g_err; }
+
+void qwen_hip_config_preset(qwen_hip_config *c, int model_b) {
+    /* detect_config, qwen_asr.c:153-186 */
+    c->hidden = model_b ? 2048 : 1024;
+    c->layers = 28;
+    c->heads = 16;
+    c->kv_heads = 8;
+    c->head_dim = 128;
+    c->intermediate = model_b ? 6144 : 3072;
+    c->vocab = QWEN_HIP_VOCAB_SIZE;
+    c->rms_eps = 1e-6f;
+    c->rope_theta = 1e6f;
+}
+
+#define QK_NSPLIT 32          /* max position splits of decode attention */
+
+struct qwen_hip_decoder {
+    qwen_hip_config cfg;
+    int device;
+    hipStream_t stream;
+    int qd, kvd, qkv_rows;
+    float scale;
+
+    /* weights (one allocation) */
+    void *wbuf;
+    uint16_t *w_qkv[QWEN_HIP_MAX_LAYERS], *w_o[QWEN_HIP_MAX_LAYERS];
+    uint16_t *w_gu[QWEN_HIP_MAX_LAYERS], *w_down[QWEN_HIP_MAX_LAYERS];
+    float *n_in[QWEN_HIP_MAX_LAYERS], *n_post[QWEN_HIP_MAX_LAYERS];
+    float *n_q[QWEN_HIP_MAX_LAYERS], *n_k[QWEN_HIP_MAX_LAYERS];
+    uint16_t *emb;
+    float *fnorm;
+    unsigned char loaded[QWEN_HIP_MAX_LAYERS];
+    int emb_loaded;
+
+    /* KV cache + RoPE table, both sized kv_cap positions */
+    float *kc, *vc;
+    float *rope_cos, *rope_sin;
+    int kv_cap, kv_len;
+
+    /* decode buffers */
+    float *x, *qkv, *qrot, *attn_part, *attn_out, *h, *hidden, *logits, *cand_val;
+    int *cand_idx, n_cand;
+    int *d_tok, *d_pos, *d_counter, *d_log, log_cap;
+    float *h_row;             /* pinned staging */
+    int *h_int;
+
+    /* prefill buffers, sized pref_cap rows */
+    int pref_cap;
+    float *px, *pqkv, *pqrot;
+    uint16_t *pxh, *pxl, *pah, *pal, *phh, *phl;
+
+    hipGraph_t graph;
+    hipGraphExec_t gexec;
+    int graph_valid;
+    int engine, keep_logits;
+};
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+static int dev_alloc(void **p, size_t n) {
+    hipError_t e = hipMalloc(p, n ? n : 256);
+    if (e != hipSuccess) {
+        *p = NULL;
+        qk_set_err("hipMalloc(%zu): %s", n, hipGetErrorString(e));
+        return e == hipErrorOutOfMemory ? QWEN_HIP_ENOMEM : QWEN_HIP_EDEVICE;
+    }
+    return 0;
+}
+
+static void dev_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+static int use_device(const qwen_hip_decoder *d) {
+    QK_HIP(hipSetDevice(d->device));
+    return 0;
+}
+
+static void graph_drop(qwen_hip_decoder *d) {
+    if (d->gexec) (void)hipGraphExecDestroy(d->gexec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    d->gexec = NULL;
+    d->graph = NULL;
+    d->graph_valid = 0;
+}
+
+/* RoPE cos/sin table for positions [0, cap): ensure_rope_inv_freq and
+ * ensure_rope_cache, qwen_asr_decoder.c:207-256. */
+static int rope_build(qwen_hip_decoder *d, int cap) {
+    const int hd = d->cfg.head_dim, half = hd / 2;
+    size_t n = (size_t)cap * hd;
+    float *hc = (float *)malloc(n * sizeof(float)), *hs = (float *)malloc(n * sizeof(float));
+    float inv[QWEN_HIP_HEAD_DIM / 2];
+    if (!hc || !hs) { free(hc); free(hs); qk_set_err("host alloc for RoPE table"); return QWEN_HIP_ENOMEM; }
+    for (int i = 0; i < half; i++) inv[i] = 1.0f / powf(d->cfg.rope_theta, (float)(2 * i) / (float)hd);
+    for (int p = 0; p < cap; p++) {
+        float *c = hc + (size_t)p * hd, *s = hs + (size_t)p * hd;
+        for (int i = 0; i < half; i++) {
+            float a = (float)p * inv[i];
+            float cv = cosf(a), sv = sinf(a);
+            c[i] = cv; c[half + i] = cv;
+            s[i] = sv; s[half + i] = sv;
+        }
+    }
+    float *dc = NULL, *ds = NULL;
+    int rc = dev_alloc((void **)&dc, n * sizeof(float));
+    if (!rc) rc = dev_alloc((void **)&ds, n * sizeof(float));
+    if (!rc && hipMemcpy(dc, hc, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) rc = QWEN_HIP_EDEVICE;
+    if (!rc && hipMemcpy(ds, hs, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) rc = QWEN_HIP_EDEVICE;
+    free(hc);
+    free(hs);
+    if (rc) { dev_free(dc); dev_free(ds); if (rc == QWEN_HIP_EDEVICE) qk_set_err("RoPE table upload failed"); return rc; }
+    dev_free(d->rope_cos);
+    dev_free(d->rope_sin);
+    d->rope_cos = dc;
+    d->rope_sin = ds;
+    return 0;
+}
+
+/* kv_cache_grow (qwen_asr_decoder.c:133-160): double until >= required and
+ * copy the live positions [0, kv_len) of every (layer, kv head). */
+static int kv_reserve(qwen_hip_decoder *d, int required) {
+    if (required <= d->kv_cap) return 0;
+    int cap = d->kv_cap > 0 ? d->kv_cap : required;
+    while (cap < required) {
+        if (cap > (1 << 29)) { qk_set_err("KV capacity overflow"); return QWEN_HIP_EINVAL; }
+        cap *= 2;
+    }
+    const int hd = d->cfg.head_dim;
+    const size_t rows = (size_t)d->cfg.layers * d->cfg.kv_heads;
+    const size_t bytes = rows * (size_t)cap * hd * sizeof(float);
+    float *nk = NULL, *nv = NULL;
+    int rc = dev_alloc((void **)&nk, bytes);
+    if (!rc) rc = dev_alloc((void **)&nv, bytes);
+    if (rc) { dev_free(nk); dev_free(nv); return rc; }
+    QK_HIP(hipMemsetAsync(nk, 0, bytes, d->stream));
+    QK_HIP(hipMemsetAsync(nv, 0, bytes, d->stream));
+    if (d->kc && d->kv_len > 0) {
+        const size_t w = (size_t)d->kv_len * hd * sizeof(float);
+        const size_t sp = (size_t)d->kv_cap * hd * sizeof(float), dp = (size_t)cap * hd * sizeof(float);
+        QK_HIP(hipMemcpy2DAsync(nk, dp, d->kc, sp, w, rows, hipMemcpyDeviceToDevice, d->stream));
+        QK_HIP(hipMemcpy2DAsync(nv, dp, d->vc, sp, w, rows, hipMemcpyDeviceToDevice, d->stream));
+    }
+    QK_HIP(hipStreamSynchronize(d->stream));
+    if ((rc = rope_build(d, cap))) { dev_free(nk); dev_free(nv); return rc; }
+    dev_free(d->kc);
+    dev_free(d->vc);
+    d->kc = nk;
+    d->vc = nv;
+    d->kv_cap = cap;
+    graph_drop(d);
+    return 0;
+}
+
+static float *kc_layer(const qwen_hip_decoder *d, int l) {
+    return d->kc + (size_t)l * d->cfg.kv_heads * d->kv_cap * d->cfg.head_dim;
+}
+
+static float *vc_layer(const qwen_hip_decoder *d, int l) {
+    return d->vc + (size_t)l * d->cfg.kv_heads * d->kv_cap * d->cfg.head_dim;
+}
+
+static int set_dev_pos(qwen_hip_decoder *d) {
+    d->h_int[1] = d->kv_len;
+    QK_HIP(hipMemcpyAsync(d->d_pos, &d->h_int[1], sizeof(int), hipMemcpyHostToDevice, d->stream));
+    QK_HIP(hipStreamSynchronize(d->stream));
+    return 0;
+}
+
+static int check_cfg(const qwen_hip_config *c) {
+    if (!c) return 0;
+    if (c->head_dim != QWEN_HIP_HEAD_DIM) return 0;
+    if (c->layers <= 0 || c->layers > QWEN_HIP_MAX_LAYERS) return 0;
+    if (c->heads <= 0 || c->kv_heads <= 0 || c->heads % c->kv_heads) return 0;
+    int hpk = c->heads / c->kv_heads;
+    if (hpk != 1 && hpk != 2 && hpk != 4) return 0;
+    if (c->hidden <= 0 || c->hidden % 64 || c->hidden > 6144) return 0;
+    if (c->intermediate <= 0 || c->intermediate % 64 || c->intermediate > 6144) return 0;
+    if (c->heads * c->head_dim > 6144) return 0;
+    if (c->vocab <= 0) return 0;
+    return 1;
+}
+
+qwen_hip_decoder *qwen_hip_decoder_create(const qwen_hip_config *cfg, int device, int kv_capacity) {
+    if (!check_cfg(cfg)) {
+        qk_set_err("unsupported decoder configuration (head_dim must be 128; hidden, "
+                   "intermediate multiples of 64 and <= 6144; heads/kv_heads in {1,2,4})");
+        return NULL;
+    }
+    if (hipSetDevice(device) != hipSuccess) { qk_set_err("hipSetDevice(%d) failed", device); return NULL; }
+    qwen_hip_decoder *d = (qwen_hip_decoder *)calloc(1, sizeof(*d));
+    if (!d) { qk_set_err("host alloc"); return NULL; }
+    d->cfg = *cfg;
+    d->device = device;
+    d->qd = cfg->heads * cfg->head_dim;
+    d->kvd = cfg->kv_heads * cfg->head_dim;
+    d->qkv_rows = d->qd + 2 * d->kvd;
+    d->scale = 1.0f / sqrtf((float)cfg->head_dim);   /* qwen_asr_decoder.c:426 */
+    if (hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess) {
+        qk_set_err("hipStreamCreate failed");
+        free(d);
+        return NULL;
+    }
+
+    const size_t D = cfg->hidden, I = cfg->intermediate, L = cfg->layers;
+    size_t per_layer = align256((size_t)d->qkv_rows * D * 2) + align256((size_t)D * d->qd * 2) +
+                       align256(2 * I * D * 2) + align256(D * I * 2) + 2 * align256(D * 4) +
+                       2 * align256((size_t)cfg->head_dim * 4);
+    size_t total = L * per_layer + align256((size_t)cfg->vocab * D * 2) + align256(D * 4);
+    if (dev_alloc(&d->wbuf, total)) goto fail;
+    {
+        char *p = (char *)d->wbuf;
+        for (size_t l = 0; l < L; l++) {
+            d->w_qkv[l] = (uint16_t *)p; p += align256((size_t)d->qkv_rows * D * 2);
+            d->w_o[l] = (uint16_t *)p;   p += align256(D * d->qd * 2);
+            d->w_gu[l] = (uint16_t *)p;  p += align256(2 * I * D * 2);
+            d->w_down[l] = (uint16_t *)p; p += align256(D * I * 2);
+            d->n_in[l] = (float *)p;     p += align256(D * 4);
+            d->n_post[l] = (float *)p;   p += align256(D * 4);
+            d->n_q[l] = (float *)p;      p += align256((size_t)cfg->head_dim * 4);
+            d->n_k[l] = (float *)p;      p += align256((size_t)cfg->head_dim * 4);
+        }
+        d->emb = (uint16_t *)p; p += align256((size_t)cfg->vocab * D * 2);
+        d->fnorm = (float *)p;
+    }
+
+    d->n_cand = qk_gemv_blocks(cfg->vocab, cfg->hidden, QK_EPI_ARGMAX);
+    d->log_cap = 4096;
+    if (dev_alloc((void **)&d->x, D * 4) || dev_alloc((void **)&d->qkv, (size_t)d->qkv_rows * 4) ||
+        dev_alloc((void **)&d->qrot, (size_t)d->qd * 4) ||
+        dev_alloc((void **)&d->attn_part, (size_t)cfg->heads * QK_NSPLIT * (cfg->head_dim + 2) * 4) ||
+        dev_alloc((void **)&d->attn_out, (size_t)d->qd * 4) || dev_alloc((void **)&d->h, I * 4) ||
+        dev_alloc((void **)&d->hidden, D * 4) || dev_alloc((void **)&d->logits, (size_t)cfg->vocab * 4) ||
+        dev_alloc((void **)&d->cand_val, (size_t)d->n_cand * 4) ||
+        dev_alloc((void **)&d->cand_idx, (size_t)d->n_cand * 4) ||
+        dev_alloc((void **)&d->d_tok, 256) || dev_alloc((void **)&d->d_pos, 256) ||
+        dev_alloc((void **)&d->d_counter, 256) || dev_alloc((void **)&d->d_log, (size_t)d->log_cap * 4))
+        goto fail;
+    if (hipHostMalloc((void **)&d->h_row, D * 4, hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void **)&d->h_int, 64, hipHostMallocDefault) != hipSuccess) {
+        qk_set_err("hipHostMalloc failed");
+        goto fail;
+    }
+    if (hipMemset(d->hidden, 0, D * 4) != hipSuccess || hipMemset(d->d_counter, 0, 256) != hipSuccess ||
+        hipMemset(d->d_pos, 0, 256) != hipSuccess) {
+        qk_set_err("hipMemset failed");
+        goto fail;
+    }
+    if (kv_reserve(d, kv_capacity > 0 ? kv_capacity : 1024)) goto fail;
+    return d;
+fail:
+    qwen_hip_decoder_destroy(d);
+    return NULL;
+}
+
+static void prefill_free(qwen_hip_decoder *d) {
+    dev_free(d->px); dev_free(d->pqkv); dev_free(d->pqrot);
+    dev_free(d->pxh); dev_free(d->pxl); dev_free(d->pah); dev_free(d->pal);
+    dev_free(d->phh); dev_free(d->phl);
+    d->px = d->pqkv = d->pqrot = NULL;
+    d->pxh = d->pxl = d->pah = d->pal = d->phh = d->phl = NULL;
+    d->pref_cap = 0;
+}
+
+void qwen_hip_decoder_destroy(qwen_hip_decoder *d) {
+    if (!d) return;
+    (void)hipSetDevice(d->device);
+    if (d->stream) (void)hipStreamSynchronize(d->stream);
+    graph_drop(d);
+    dev_free(d->wbuf);
+    dev_free(d->kc); dev_free(d->vc); dev_free(d->rope_cos); dev_free(d->rope_sin);
+    dev_free(d->x); dev_free(d->qkv); dev_free(d->qrot); dev_free(d->attn_part);
+    dev_free(d->attn_out); dev_free(d->h); dev_free(d->hidden); dev_free(d->logits);
+    dev_free(d->cand_val); dev_free(d->cand_idx); dev_free(d->d_tok); dev_free(d->d_pos);
+    dev_free(d->d_counter); dev_free(d->d_log);
+    prefill_free(d);
+    if (d->h_row) (void)hipHostFree(d->h_row);
+    if (d->h_int) (void)hipHostFree(d->h_int);
+    if (d->stream) (void)hipStreamDestroy(d->stream);
+    free(d);
+}
+
+/* ------------------------------------------------------------------------ */
+/* weights                                                                   */
+/* ------------------------------------------------------------------------ */
+int qwen_hip_decoder_load_layer(qwen_hip_decoder *d, int l, const qwen_hip_layer_weights *w) {
+    if (!d || !w || l < 0 || l >= d->cfg.layers) { qk_set_err("load_layer: bad argument"); return QWEN_HIP_EINVAL; }
+    if (!w->wq || !w->wk || !w->wv || !w->wo || !w->gate || !w->up || !w->down || !w->q_norm ||
+        !w->k_norm || !w->input_norm || !w->post_attn_norm) {
+        qk_set_err("load_layer %d: missing tensor", l);
+        return QWEN_HIP_EINVAL;
+    }
+    QK_TRY(use_device(d));
+    const size_t D = d->cfg.hidden, I = d->cfg.intermediate, hd = d->cfg.head_dim;
+    QK_HIP(hipMemcpy(d->w_qkv[l], w->wq, (size_t)d->qd * D * 2, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->w_qkv[l] + (size_t)d->qd * D, w->wk, (size_t)d->kvd * D * 2, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->w_qkv[l] + (size_t)(d->qd + d->kvd) * D, w->wv, (size_t)d->kvd * D * 2,
+                     hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->w_o[l], w->wo, D * d->qd * 2, hipMemcpyHostToDevice));
+    /* interleave gate/up rows: row 2r = gate[r], row 2r+1 = up[r] */
+    QK_HIP(hipMemcpy2D(d->w_gu[l], 2 * D * 2, w->gate, D * 2, D * 2, I, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy2D(d->w_gu[l] + D, 2 * D * 2, w->up, D * 2, D * 2, I, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->w_down[l], w->down, D * I * 2, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->n_in[l], w->input_norm, D * 4, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->n_post[l], w->post_attn_norm, D * 4, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->n_q[l], w->q_norm, hd * 4, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->n_k[l], w->k_norm, hd * 4, hipMemcpyHostToDevice));
+    d->loaded[l] = 1;
+    return 0;
+}
+
+int qwen_hip_decoder_load_embeddings(qwen_hip_decoder *d, const uint16_t *emb, const float *fnorm) {
+    if (!d || !emb || !fnorm) { qk_set_err("load_embeddings: bad argument"); return QWEN_HIP_EINVAL; }
+    QK_TRY(use_device(d));
+    QK_HIP(hipMemcpy(d->emb, emb, (size_t)d->cfg.vocab * d->cfg.hidden * 2, hipMemcpyHostToDevice));
+    QK_HIP(hipMemcpy(d->fnorm, fnorm, (size_t)d->cfg.hidden * 4, hipMemcpyHostToDevice));
+    d->emb_loaded = 1;
+    return 0;
+}
+
+static void norm_vec(float *out, size_t n, uint64_t seed, uint64_t tid, double norm_std) {
+    if (norm_std == 0.0) {
+        for (size_t i = 0; i < n; i++) out[i] = 1.0f;
+    } else {
+        qwen_synth_normal_f32(out, n, seed, tid, 1.0, norm_std, 0);
+    }
+}
+
+int qwen_hip_decoder_load_synthetic(qwen_hip_decoder *d, uint64_t seed, double wstd, double norm_std) {
+    if (!d) return QWEN_HIP_EINVAL;
+    const qwen_hip_config *c = &d->cfg;
+    const size_t D = c->hidden, I = c->intermediate, hd = c->head_dim;
+    const size_t qd = d->qd, kvd = d->kvd;
+    size_t big = (size_t)c->vocab * D;
+    size_t need = qd * D + 2 * kvd * D + D * qd + 3 * I * D;
+    uint16_t *buf = (uint16_t *)malloc((need > big ? need : big) * 2);
+    float *nb = (float *)malloc((2 * D + 2 * hd) * 4);
+    if (!buf || !nb) { free(buf); free(nb); qk_set_err("host alloc for synthetic weights"); return QWEN_HIP_ENOMEM; }
+    int rc = 0;
+    for (int l = 0; l < c->layers && !rc; l++) {
+        qwen_hip_layer_weights w;
+        uint16_t *p = buf;
+        w.wq = p;   qwen_synth_normal_bf16(p, qd * D, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_WQ), 0, wstd, 0); p += qd * D;
+        w.wk = p;   qwen_synth_normal_bf16(p, kvd * D, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_WK), 0, wstd, 0); p += kvd * D;
+        w.wv = p;   qwen_synth_normal_bf16(p, kvd * D, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_WV), 0, wstd, 0); p += kvd * D;
+        w.wo = p;   qwen_synth_normal_bf16(p, D * qd, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_WO), 0, wstd, 0); p += D * qd;
+        w.gate = p; qwen_synth_normal_bf16(p, I * D, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_GATE), 0, wstd, 0); p += I * D;
+        w.up = p;   qwen_synth_normal_bf16(p, I * D, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_UP), 0, wstd, 0); p += I * D;
+        w.down = p; qwen_synth_normal_bf16(p, D * I, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_DOWN), 0, wstd, 0);
+        float *n = nb;
+        w.q_norm = n;         norm_vec(n, hd, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_QNORM), norm_std); n += hd;
+        w.k_norm = n;         norm_vec(n, hd, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_KNORM), norm_std); n += hd;
+        w.input_norm = n;     norm_vec(n, D, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_INNORM), norm_std); n += D;
+        w.post_attn_norm = n; norm_vec(n, D, seed, QWEN_SYNTH_LAYER(l, QWEN_SYNTH_POSTNORM), norm_std);
+        rc = qwen_hip_decoder_load_layer(d, l, &w);
+    }
+    if (!rc) {
+        qwen_synth_normal_bf16(buf, big, seed, QWEN_SYNTH_EMBED, 0, wstd, 0);
+        norm_vec(nb, D, seed, QWEN_SYNTH_FINAL_NORM, norm_std);
+        rc = qwen_hip_decoder_load_embeddings(d, buf, nb);
+    }
+    free(buf);
+    free(nb);
+    return rc;
+}
+
+static int ready(qwen_hip_decoder *d) {
+    if (!d) { qk_set_err("NULL decoder"); return QWEN_HIP_EINVAL; }
+    if (!d->emb_loaded) { qk_set_err("embeddings not loaded"); return QWEN_HIP_ESTATE; }
+    for (int l = 0; l < d->cfg.layers; l++)
+        if (!d->loaded[l]) { qk_set_err("layer %d not loaded", l); return QWEN_HIP_ESTATE; }
+    return use_device(d);
+}
+
+/* ------------------------------------------------------------------------ */
+/* prefill: qwen_decoder_prefill, qwen_asr_decoder.c:262-359                */
+/* ------------------------------------------------------------------------ */
+static int prefill_reserve(qwen_hip_decoder *d, int S) {
+    if (S <= d->pref_cap) return 0;
+    int cap = d->pref_cap > 0 ? d->pref_cap : 64;       /* ensure_prefill_buffers :181-182 */
+    while (cap < S) cap *= 2;
+    prefill_free(d);
+    const size_t D = d->cfg.hidden, I = d->cfg.intermediate;
+    int rc = dev_alloc((void **)&d->px, (size_t)cap * D * 4);
+    if (!rc) rc = dev_alloc((void **)&d->pqkv, (size_t)cap * d->qkv_rows * 4);
+    if (!rc) rc = dev_alloc((void **)&d->pqrot, (size_t)cap * d->qd * 4);
+    if (!rc) rc = dev_alloc((void **)&d->pxh, (size_t)cap * D * 2);
+    if (!rc) rc = dev_alloc((void **)&d->pxl, (size_t)cap * D * 2);
+    if (!rc) rc = dev_alloc((void **)&d->pah, (size_t)cap * d->qd * 2);
+    if (!rc) rc = dev_alloc((void **)&d->pal, (size_t)cap * d->qd * 2);
+    if (!rc) rc = dev_alloc((void **)&d->phh, (size_t)cap * I * 2);
+    if (!rc) rc = dev_alloc((void **)&d->phl, (size_t)cap * I * 2);
+    if (rc) { prefill_free(d); return rc; }
+    d->pref_cap = cap;
+    return 0;
+}
+
+static int prefill_layers(qwen_hip_decoder *d, int S) {
+    const qwen_hip_config *c = &d->cfg;
+    const int D = c->hidden, I = c->intermediate, hd = c->head_dim, start = d->kv_len;
+    hipStream_t s = d->stream;
+    for (int l = 0; l < c->layers; l++) {
+        QK_TRY(qk_rmsnorm_split_launch(d->px, d->n_in[l], S, D, c->rms_eps, d->pxh, d->pxl, s));
+        QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_qkv[l], S, d->qkv_rows, D, QK_GEMM_STORE, d->pqkv, NULL, NULL, s));
+        qk_rope_append_args ra = {
+            .qkv = d->pqkv, .q_norm = d->n_q[l], .k_norm = d->n_k[l], .eps = c->rms_eps,
+            .rope_cos = d->rope_cos, .rope_sin = d->rope_sin, .k_cache = kc_layer(d, l),
+            .v_cache = vc_layer(d, l), .cap = d->kv_cap, .pos_dev = NULL, .start = start, .S = S,
+            .heads = c->heads, .kv_heads = c->kv_heads, .q_out = d->pqrot};
+        QK_TRY(qk_rope_append_launch(&ra, s));
+        qk_attn_args aa = {
+            .q = d->pqrot, .k = kc_layer(d, l), .v = vc_layer(d, l), .pos_stride = hd,
+            .head_stride = (long)d->kv_cap * hd, .pos_dev = NULL, .seq_k = start + S, .seq_q = S,
+            .q_offset = start, .heads = c->heads, .kv_heads = c->kv_heads, .scale = d->scale,
+            .out = NULL, .out_hi = d->pah, .out_lo = d->pal};
+        QK_TRY(qk_attn_prefill_launch(&aa, s));
+        QK_TRY(qk_gemm_launch(d->pah, d->pal, d->w_o[l], S, D, d->qd, QK_GEMM_ADD, d->px, NULL, NULL, s));
+        QK_TRY(qk_rmsnorm_split_launch(d->px, d->n_post[l], S, D, c->rms_eps, d->pxh, d->pxl, s));
+        QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_gu[l], S, 2 * I, D, QK_GEMM_SWIGLU, NULL, d->phh, d->phl, s));
+        QK_TRY(qk_gemm_launch(d->phh, d->phl, d->w_down[l], S, D, I, QK_GEMM_ADD, d->px, NULL, NULL, s));
+    }
+    return 0;
+}
+
+static int prefill_common(qwen_hip_decoder *d, const float *rows, int S, hipMemcpyKind kind) {
+    int rc = ready(d);
+    if (rc) return rc;
+    if (S < 0 || (S > 0 && !rows)) { qk_set_err("prefill: bad rows"); return QWEN_HIP_EINVAL; }
+    if (S == 0) return 0;
+    if (d->kv_len + S > d->kv_cap) QK_TRY(kv_reserve(d, d->kv_len + S + 1024));   /* :278-279 */
+    QK_TRY(prefill_reserve(d, S));
+    QK_HIP(hipMemcpyAsync(d->px, rows, (size_t)S * d->cfg.hidden * 4, kind, d->stream));
+    QK_TRY(prefill_layers(d, S));
+    QK_HIP(hipStreamSynchronize(d->stream));
+    d->kv_len += S;
+    return set_dev_pos(d);
+}
+
+int qwen_hip_decoder_prefill(qwen_hip_decoder *d, const float *rows, int S) {
+    return prefill_common(d, rows, S, hipMemcpyHostToDevice);
+}
+
+int qwen_hip_decoder_prefill_device(qwen_hip_decoder *d, const float *d_rows, int S) {
+    return prefill_common(d, d_rows, S, hipMemcpyDeviceToDevice);
+}
+
+/* ------------------------------------------------------------------------ */
+/* decode step: qwen_decoder_forward, qwen_asr_decoder.c:388-476            */
+/* ------------------------------------------------------------------------ */
+static int enqueue_step(qwen_hip_decoder *d) {
+    const qwen_hip_config *c = &d->cfg;
+    const int D = c->hidden, I = c->intermediate, hd = c->head_dim;
+    hipStream_t s = d->stream;
+    for (int l = 0; l < c->layers; l++) {
+        /* input RMSNorm + Q|K|V; layer 0 also gathers the token embedding */
+        qk_gemv_args g = {.W = d->w_qkv[l], .rows = d->qkv_rows, .K = D, .x = d->x, .norm_w = d->n_in[l],
+                          .eps = c->rms_eps, .y = d->qkv, .epi = QK_EPI_STORE};
+        if (l == 0) { g.tok = d->d_tok; g.emb = d->emb; g.x_store = d->x; }
+        QK_TRY(qk_gemv_launch(&g, s));
+        qk_rope_append_args ra = {
+            .qkv = d->qkv, .q_norm = d->n_q[l], .k_norm = d->n_k[l], .eps = c->rms_eps,
+            .rope_cos = d->rope_cos, .rope_sin = d->rope_sin, .k_cache = kc_layer(d, l),
+            .v_cache = vc_layer(d, l), .cap = d->kv_cap, .pos_dev = d->d_pos, .S = 1,
+            .heads = c->heads, .kv_heads = c->kv_heads, .q_out = d->qrot};
+        QK_TRY(qk_rope_append_launch(&ra, s));
+        qk_attn_args aa = {
+            .q = d->qrot, .k = kc_layer(d, l), .v = vc_layer(d, l), .pos_stride = hd,
+            .head_stride = (long)d->kv_cap * hd, .pos_dev = d->d_pos, .seq_q = 1, .heads = c->heads,
+            .kv_heads = c->kv_heads, .scale = d->scale, .part = d->attn_part, .nsplit = QK_NSPLIT,
+            .out = d->attn_out};
+        QK_TRY(qk_attn_decode_launch(&aa, s));
+        qk_gemv_args go = {.W = d->w_o[l], .rows = D, .K = d->qd, .x = d->attn_out, .y = d->x, .epi = QK_EPI_ADD};
+        QK_TRY(qk_gemv_launch(&go, s));
+        qk_gemv_args gu = {.W = d->w_gu[l], .rows = 2 * I, .K = D, .x = d->x, .norm_w = d->n_post[l],
+                           .eps = c->rms_eps, .y = d->h, .epi = QK_EPI_SWIGLU};
+        QK_TRY(qk_gemv_launch(&gu, s));
+        qk_gemv_args gd = {.W = d->w_down[l], .rows = D, .K = I, .x = d->h, .y = d->x, .epi = QK_EPI_ADD};
+        QK_TRY(qk_gemv_launch(&gd, s));
+    }
+    /* final RMSNorm (in place in the reference, :474) + tied LM head argmax */
+    qk_gemv_args gl = {.W = d->emb, .rows = c->vocab, .K = D, .x = d->x, .norm_w = d->fnorm, .eps = c->rms_eps,
+                       .normed_store = d->hidden, .logits = d->keep_logits ? d->logits : NULL,
+                       .cand_val = d->cand_val, .cand_idx = d->cand_idx, .epi = QK_EPI_ARGMAX};
+    QK_TRY(qk_gemv_launch(&gl, s));
+    QK_TRY(qk_argmax_finish_launch(d->cand_val, d->cand_idx, d->n_cand, d->d_tok, d->d_log, d->d_counter,
+                                   d->d_pos, s));
+    return 0;
+}
+
+static int graph_ensure(qwen_hip_decoder *d) {
+    if (d->graph_valid) return 0;
+    graph_drop(d);
+    QK_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(d);
+    hipGraph_t g = NULL;
+    hipError_t e = hipStreamEndCapture(d->stream, &g);
+    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+    if (e != hipSuccess) { qk_set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return QWEN_HIP_EDEVICE; }
+    d->graph = g;
+    QK_HIP(hipGraphInstantiate(&d->gexec, g, NULL, NULL, 0));
+    d->graph_valid = 1;
+    return 0;
+}
+
+static int launch_steps(qwen_hip_decoder *d, int n) {
+    if (d->engine == 0) {
+        QK_TRY(graph_ensure(d));
+        for (int i = 0; i < n; i++) QK_HIP(hipGraphLaunch(d->gexec, d->stream));
+    } else {
+        for (int i = 0; i < n; i++) QK_TRY(enqueue_step(d));
+    }
+    return 0;
+}
+
+static int log_reserve(qwen_hip_decoder *d, int n) {
+    if (n <= d->log_cap) return 0;
+    int cap = d->log_cap;
+    while (cap < n) cap *= 2;
+    int *p = NULL;
+    QK_TRY(dev_alloc((void **)&p, (size_t)cap * 4));
+    dev_free(d->d_log);
+    d->d_log = p;
+    d->log_cap = cap;
+    graph_drop(d);
+    return 0;
+}
+
+/* one forward whose input is already staged (x or d_tok set by the caller) */
+static int forward_staged(qwen_hip_decoder *d) {
+    d->h_int[2] = 0;
+    QK_HIP(hipMemcpyAsync(d->d_counter, &d->h_int[2], sizeof(int), hipMemcpyHostToDevice, d->stream));
+    QK_TRY(launch_steps(d, 1));
+    QK_HIP(hipMemcpyAsync(&d->h_int[3], d->d_tok, sizeof(int), hipMemcpyDeviceToHost, d->stream));
+    QK_HIP(hipStreamSynchronize(d->stream));
+    d->kv_len += 1;
+    return d->h_int[3];
+}
+
+static int forward_prepare(qwen_hip_decoder *d, int steps) {
+    int rc = ready(d);
+    if (rc) return rc;
+    if (d->kv_len + steps > d->kv_cap) QK_TRY(kv_reserve(d, d->kv_len + steps + 1024));   /* :416-418 */
+    QK_TRY(log_reserve(d, steps));
+    return 0;
+}
+
+int qwen_hip_decoder_forward(qwen_hip_decoder *d, const float *row) {
+    if (!row || forward_prepare(d, 1)) return QWEN_HIP_TOKEN_IM_END;
+    memcpy(d->h_row, row, (size_t)d->cfg.hidden * 4);
+    d->h_int[0] = -1;
+    if (hipMemcpyAsync(d->x, d->h_row, (size_t)d->cfg.hidden * 4, hipMemcpyHostToDevice, d->stream) != hipSuccess ||
+        hipMemcpyAsync(d->d_tok, &d->h_int[0], sizeof(int), hipMemcpyHostToDevice, d->stream) != hipSuccess) {
+        qk_set_err("forward: staging copy failed");
+        return QWEN_HIP_TOKEN_IM_END;
+    }
+    int t = forward_staged(d);
+    return t < 0 ? QWEN_HIP_TOKEN_IM_END : t;
+}
+
+int qwen_hip_decoder_forward_token(qwen_hip_decoder *d, int token) {
+    if (!d || token < 0 || token >= d->cfg.vocab) { qk_set_err("forward_token: bad token"); return QWEN_HIP_TOKEN_IM_END; }
+    if (forward_prepare(d, 1)) return QWEN_HIP_TOKEN_IM_END;
+    d->h_int[0] = token;
+    if (hipMemcpyAsync(d->d_tok, &d->h_int[0], sizeof(int), hipMemcpyHostToDevice, d->stream) != hipSuccess) {
+        qk_set_err("forward_token: staging copy failed");
+        return QWEN_HIP_TOKEN_IM_END;
+    }
+    int t = forward_staged(d);
+    return t < 0 ? QWEN_HIP_TOKEN_IM_END : t;
+}
+
+int qwen_hip_decoder_generate(qwen_hip_decoder *d, int first, int n, int *out, int stop_on_eos) {
+    if (!d || n < 0 || (n > 0 && !out) || first < 0 || first >= d->cfg.vocab) {
+        qk_set_err("generate: bad argument");
+        return QWEN_HIP_EINVAL;
+    }
+    if (n == 0) return 0;
+    QK_TRY(forward_prepare(d, n));
+    const int start = d->kv_len;
+    d->h_int[0] = first;
+    d->h_int[2] = 0;
+    QK_HIP(hipMemcpyAsync(d->d_tok, &d->h_int[0], sizeof(int), hipMemcpyHostToDevice, d->stream));
+    QK_HIP(hipMemcpyAsync(d->d_counter, &d->h_int[2], sizeof(int), hipMemcpyHostToDevice, d->stream));
+    QK_TRY(launch_steps(d, n));
+    QK_HIP(hipMemcpyAsync(out, d->d_log, (size_t)n * 4, hipMemcpyDeviceToHost, d->stream));
+    QK_HIP(hipStreamSynchronize(d->stream));
+    int kept = n;
+    if (stop_on_eos) {
+        for (int i = 0; i < n; i++)
+            if (out[i] == QWEN_HIP_TOKEN_ENDOFTEXT || out[i] == QWEN_HIP_TOKEN_IM_END) { kept = i + 1; break; }
+    }
+    d->kv_len = start + kept;
+    QK_TRY(set_dev_pos(d));
+    return kept;
+}
+
+int qwen_hip_decoder_kv_len(const qwen_hip_decoder *d) { return d ? d->kv_len : QWEN_HIP_EINVAL; }
+
+int qwen_hip_decoder_set_kv_len(qwen_hip_decoder *d, int n) {
+    if (!d || n < 0 || n > d->kv_len) { qk_set_err("set_kv_len: %d outside [0, kv_len]", n); return QWEN_HIP_EINVAL; }
+    QK_TRY(use_device(d));
+    d->kv_len = n;
+    return set_dev_pos(d);
+}
+
+int qwen_hip_decoder_set_keep_logits(qwen_hip_decoder *d, int on) {
+    if (!d) return QWEN_HIP_EINVAL;
+    if ((on != 0) != d->keep_logits) { d->keep_logits = on != 0; graph_drop(d); }
+    return 0;
+}
+
+int qwen_hip_decoder_set_engine(qwen_hip_decoder *d, int engine) {
+    if (!d || engine < 0 || engine > 1) return QWEN_HIP_EINVAL;
+    d->engine = engine;
+    return 0;
+}
+
+int qwen_hip_decoder_read_hidden(qwen_hip_decoder *d, float *out) {
+    if (!d || !out) return QWEN_HIP_EINVAL;
+    QK_TRY(use_device(d));
+    QK_HIP(hipMemcpyAsync(out, d->hidden, (size_t)d->cfg.hidden * 4, hipMemcpyDeviceToHost, d->stream));
+    QK_HIP(hipStreamSynchronize(d->stream));
+    return 0;
+}
+
+int qwen_hip_decoder_read_logits(qwen_hip_decoder *d, float *out) {
+    if (!d || !out) return QWEN_HIP_EINVAL;
+    if (!d->keep_logits) { qk_set_err("read_logits needs set_keep_logits(1) before the forward"); return QWEN_HIP_ESTATE; }
+    QK_TRY(use_device(d));
+    QK_HIP(hipMemcpyAsync(out, d->logits, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, d->stream));
+    QK_HIP(hipStreamSynchronize(d->stream));
+    return 0;
+}
+
+hipStream_t qwen_hip_decoder_stream(const qwen_hip_decoder *d) { return d ? d->stream : NULL; }
+
+double qwen_hip_decoder_step_bytes(const qwen_hip_decoder *d, int kv_len) {
+    if (!d) return 0.0;
+    const qwen_hip_config *c = &d->cfg;
+    const double D = c->hidden, I = c->intermediate, L = c->layers;
+    double w = L * 2.0 * (D * d->qkv_rows + (double)d->qd * D + 2.0 * I * D + I * D);
+    double lm = 2.0 * c->vocab * D;
+    double norms = 4.0 * (L * (2.0 * D + 2.0 * c->head_dim) + D);
+    double kv_row = L * d->kvd * 4.0 * 2.0;         /* K and V, fp32, all layers */
+    return w + lm + norms + kv_row * (kv_len + 1) + kv_row;
+}

@@ -1,0 +1,610 @@
+// decode.hip - bandwidth-bound kernels of the per-token step (gfx950, wave64).
+//
+//  gemv_kernel        y = W x with bf16 W streamed once from HBM, fp32 x held
+//                     in registers, fp32 accumulation (reference
+//                     qwen_bf16_matvec_fused_avx, qwen_asr_kernels_avx.c:25-155),
+//                     with fused prologues (RMSNorm qwen_asr_kernels.c:750-809;
+//                     embedding gather qwen_asr.c:353-360) and epilogues
+//                     (residual add :159-161; SwiGLU on interleaved rows
+//                     :902-959; LM-head argmax :518-543).
+//  argmax_finish      second pass of the argmax over the per-block winners.
+//  rope_append        per-head q/k RMSNorm (:811-873) + NeoX RoPE
+//                     (:1182-1247) + K/V append (qwen_asr_decoder.c:446-447).
+//  attn_decode_split  one query row against the fp32 KV cache, split over
+//  attn_combine       positions (qwen_causal_attention, :1050-1141).
+//  attn_prefill       many query rows, causal, K/V tiles staged in LDS.
+#include "common.h"
+#include "qk_kernels.h"
+#include "qwen_asr_hip.h"
+
+#include <math.h>
+
+// ---------------------------------------------------------------------------
+// GEMV.  A wave owns ROWS consecutive rows; lane l covers columns
+// [c*512 + 8l, c*512 + 8l + 8) for chunk c < NC, so one 16-byte load per lane
+// per row per chunk streams the row at full coalescing.  The ROWS partial
+// sums per lane are reduced with a transposing butterfly: each exchange
+// halves the values a lane carries, so the whole reduction costs
+// log2(ROWS) + 6 - log2(ROWS) + (ROWS - 1) shuffles instead of 6 * ROWS.
+// ---------------------------------------------------------------------------
+template <int N>
+__device__ __forceinline__ void transpose_step(float (&v)[N], int n, int m, int lane) {
+    const bool up = (lane & m) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 2; i++) {
+        if (i < n / 2) {
+            float keep = up ? v[i + n / 2] : v[i];
+            float send = up ? v[i] : v[i + n / 2];
+            v[i] = keep + __shfl_xor(send, m, QK_WAVE);
+        }
+    }
+}
+
+// Reduce ROWS per-lane partials to KEEP values per lane (KEEP = 1 or 2).
+// Afterwards every lane of the aligned group of 64*KEEP/ROWS lanes holds the
+// totals of rows [KEEP*(lane / (64*KEEP/ROWS)), +KEEP).
+template <int ROWS, int KEEP>
+__device__ __forceinline__ void reduce_rows(float (&v)[ROWS], int lane) {
+    int n = ROWS, m = 32;
+#pragma unroll
+    for (; n > KEEP; n >>= 1, m >>= 1) transpose_step<ROWS>(v, n, m, lane);
+#pragma unroll
+    for (; m >= 1; m >>= 1) {
+#pragma unroll
+        for (int i = 0; i < KEEP; i++) v[i] += __shfl_xor(v[i], m, QK_WAVE);
+    }
+}
+
+template <int NC, int ROWS>
+__device__ __forceinline__ void gemv_load(uint4 (&w)[ROWS][NC], const uint16_t *W, int R, int K,
+                                          int rbase, int lane) {
+#pragma unroll
+    for (int j = 0; j < ROWS; j++) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int col = c * 512 + lane * 8;
+            const int r = rbase + j;
+            if (r < R && col < K) w[j][c] = ld_stream16(W + (size_t)r * K + col);
+            else w[j][c] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+}
+
+template <int NC, int ROWS, int EPI>
+__global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int K = a.K, R = a.rows;
+
+    // ---- prologue: the input row, optionally gathered and RMS-normed ----
+    float xr[NC][8];
+    int tok = -1;
+    if (a.tok) tok = *a.tok;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int col = c * 512 + lane * 8;
+        if (col < K) {
+            if (tok >= 0) {
+                uint4 e = *reinterpret_cast<const uint4 *>(a.emb + (size_t)tok * K + col);
+                xr[c][0] = bf16_lo(e.x); xr[c][1] = bf16_hi(e.x);
+                xr[c][2] = bf16_lo(e.y); xr[c][3] = bf16_hi(e.y);
+                xr[c][4] = bf16_lo(e.z); xr[c][5] = bf16_hi(e.z);
+                xr[c][6] = bf16_lo(e.w); xr[c][7] = bf16_hi(e.w);
+            } else {
+                float4 p0 = *reinterpret_cast<const float4 *>(a.x + col);
+                float4 p1 = *reinterpret_cast<const float4 *>(a.x + col + 4);
+                xr[c][0] = p0.x; xr[c][1] = p0.y; xr[c][2] = p0.z; xr[c][3] = p0.w;
+                xr[c][4] = p1.x; xr[c][5] = p1.y; xr[c][6] = p1.z; xr[c][7] = p1.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) xr[c][j] = 0.0f;
+        }
+    }
+    if (tok >= 0 && a.x_store && blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int col = c * 512 + lane * 8;
+            if (col < K)
+#pragma unroll
+                for (int j = 0; j < 8; j++) a.x_store[col + j] = xr[c][j];
+        }
+    }
+    if (a.norm_w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) ss = fmaf(xr[c][j], xr[c][j], ss);
+        ss = wave_sum(ss);
+        const float rinv = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int col = c * 512 + lane * 8;
+            if (col < K)
+#pragma unroll
+                for (int j = 0; j < 8; j++) xr[c][j] = (xr[c][j] * a.norm_w[col + j]) * rinv;
+        }
+    }
+    if (a.normed_store && blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int col = c * 512 + lane * 8;
+            if (col < K)
+#pragma unroll
+                for (int j = 0; j < 8; j++) a.normed_store[col + j] = xr[c][j];
+        }
+    }
+
+    // ---- rows ----
+    const int rows_per_block = 4 * ROWS * iters;
+    float best_v = -1e30f;
+    int best_i = 0x7fffffff;
+    uint4 w[ROWS][NC];
+    int rbase = blockIdx.x * rows_per_block + wave * ROWS;
+    if (rbase < R) gemv_load<NC, ROWS>(w, a.W, R, K, rbase, lane);
+    for (int it = 0; it < iters; it++) {
+        if (rbase >= R) break;
+        const int rnext = rbase + 4 * ROWS;
+        const bool more = (it + 1 < iters) && (rnext < R);
+        uint4 wn[ROWS][NC];
+        if (more) gemv_load<NC, ROWS>(wn, a.W, R, K, rnext, lane);
+
+        float acc[ROWS];
+#pragma unroll
+        for (int j = 0; j < ROWS; j++) {
+            acc[j] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; c++) acc[j] = dot8_bf16(w[j][c], xr[c], acc[j]);
+        }
+
+        if (EPI == QK_EPI_SWIGLU) {
+            reduce_rows<ROWS, 2>(acc, lane);
+            const int span = 128 / ROWS;                 // lanes per (g,u) pair
+            const int r = rbase + 2 * (lane / span);
+            if ((lane % span) == 0 && r + 1 < R + 1 && r < R)
+                a.y[r >> 1] = swiglu1(acc[0], acc[1]);
+        } else {
+            reduce_rows<ROWS, 1>(acc, lane);
+            const int span = 64 / ROWS;
+            const int r = rbase + lane / span;
+            if ((lane % span) == 0 && r < R) {
+                if (EPI == QK_EPI_STORE) a.y[r] = acc[0];
+                else if (EPI == QK_EPI_ADD) a.y[r] += acc[0];
+                else {
+                    if (a.logits) a.logits[r] = acc[0];
+                    if (argmax_better(acc[0], r, best_v, best_i)) { best_v = acc[0]; best_i = r; }
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < ROWS; j++)
+#pragma unroll
+                for (int c = 0; c < NC; c++) w[j][c] = wn[j][c];
+        }
+        rbase = rnext;
+    }
+
+    if (EPI == QK_EPI_ARGMAX) {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            float ov = __shfl_xor(best_v, m, QK_WAVE);
+            int oi = __shfl_xor(best_i, m, QK_WAVE);
+            if (argmax_better(ov, oi, best_v, best_i)) { best_v = ov; best_i = oi; }
+        }
+        __shared__ float sv[4];
+        __shared__ int si[4];
+        if (lane == 0) { sv[wave] = best_v; si[wave] = best_i; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float bv = sv[0];
+            int bi = si[0];
+            for (int i = 1; i < 4; i++)
+                if (argmax_better(sv[i], si[i], bv, bi)) { bv = sv[i]; bi = si[i]; }
+            a.cand_val[blockIdx.x] = bv;
+            a.cand_idx[blockIdx.x] = bi;
+        }
+    }
+}
+
+static int gemv_pick_rows(int R, int epi) {
+    if (epi == QK_EPI_ARGMAX) return 4;
+    if (R / 16 >= 256) return 4;
+    if (R / 8 >= 256 || epi == QK_EPI_SWIGLU) return 2;
+    return 1;
+}
+
+static int gemv_pick_iters(int K, int epi) {
+    if (epi != QK_EPI_ARGMAX) return 1;
+    return K <= 1024 ? 8 : 4;
+}
+
+extern "C" int qk_gemv_blocks(int rows, int K, int epi) {
+    const int per = 4 * gemv_pick_rows(rows, epi) * gemv_pick_iters(K, epi);
+    return (rows + per - 1) / per;
+}
+
+template <int NC, int ROWS>
+static void gemv_dispatch_epi(const qk_gemv_args *a, int iters, int blocks, hipStream_t s) {
+    switch (a->epi) {
+    case QK_EPI_STORE: gemv_kernel<NC, ROWS, QK_EPI_STORE><<<blocks, 256, 0, s>>>(*a, iters); break;
+    case QK_EPI_ADD: gemv_kernel<NC, ROWS, QK_EPI_ADD><<<blocks, 256, 0, s>>>(*a, iters); break;
+    case QK_EPI_SWIGLU:
+        if (ROWS >= 2) gemv_kernel<NC, (ROWS >= 2 ? ROWS : 2), QK_EPI_SWIGLU><<<blocks, 256, 0, s>>>(*a, iters);
+        break;
+    default:
+        if (ROWS == 4) gemv_kernel<NC, 4, QK_EPI_ARGMAX><<<blocks, 256, 0, s>>>(*a, iters);
+        break;
+    }
+}
+
+template <int NC>
+static void gemv_dispatch_rows(const qk_gemv_args *a, int rows_pw, int iters, int blocks, hipStream_t s) {
+    if (rows_pw == 4) gemv_dispatch_epi<NC, 4>(a, iters, blocks, s);
+    else if (rows_pw == 2) gemv_dispatch_epi<NC, 2>(a, iters, blocks, s);
+    else gemv_dispatch_epi<NC, 1>(a, iters, blocks, s);
+}
+
+extern "C" int qk_gemv_launch(const qk_gemv_args *a, hipStream_t s) {
+    if (!a || !a->W || a->rows <= 0 || a->K <= 0 || (a->K & 7) || a->K > 12 * 512) return QWEN_HIP_EINVAL;
+    if (a->epi == QK_EPI_SWIGLU && (a->rows & 1)) return QWEN_HIP_EINVAL;
+    if (a->epi == QK_EPI_ARGMAX && (!a->cand_val || !a->cand_idx)) return QWEN_HIP_EINVAL;
+    if (a->epi != QK_EPI_ARGMAX && !a->y) return QWEN_HIP_EINVAL;
+    if (!a->x && !a->tok) return QWEN_HIP_EINVAL;
+    if (a->tok && !a->emb) return QWEN_HIP_EINVAL;
+    const int rows_pw = gemv_pick_rows(a->rows, a->epi);
+    const int iters = gemv_pick_iters(a->K, a->epi);
+    const int blocks = qk_gemv_blocks(a->rows, a->K, a->epi);
+    const int nc = (a->K + 511) / 512;
+    switch (nc) {
+    case 1: gemv_dispatch_rows<1>(a, rows_pw, iters, blocks, s); break;
+    case 2: gemv_dispatch_rows<2>(a, rows_pw, iters, blocks, s); break;
+    case 3:
+    case 4: gemv_dispatch_rows<4>(a, rows_pw, iters, blocks, s); break;
+    case 5:
+    case 6: gemv_dispatch_rows<6>(a, rows_pw, iters, blocks, s); break;
+    case 7:
+    case 8: gemv_dispatch_rows<8>(a, rows_pw, iters, blocks, s); break;
+    default: gemv_dispatch_rows<12>(a, rows_pw, iters, blocks, s); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// ---------------------------------------------------------------------------
+// Argmax, second pass: one block reduces the per-block winners.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void argmax_finish(const float *cv, const int *ci, int n, int *tok_out,
+                                                     int *log, int *counter, int *pos) {
+    float bv = -1e30f;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 256)
+        if (argmax_better(cv[i], ci[i], bv, bi)) { bv = cv[i]; bi = ci[i]; }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        float ov = __shfl_xor(bv, m, QK_WAVE);
+        int oi = __shfl_xor(bi, m, QK_WAVE);
+        if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < 4; i++)
+            if (argmax_better(sv[i], si[i], sv[0], si[0])) { sv[0] = sv[i]; si[0] = si[i]; }
+        // nothing above the reference's -1e30 floor: it returns its start row
+        const int t = si[0] == 0x7fffffff ? 0 : si[0];
+        if (tok_out) *tok_out = t;
+        if (log) {
+            const int c = *counter;
+            log[c] = t;
+            *counter = c + 1;
+        }
+        if (pos) *pos = *pos + 1;
+    }
+}
+
+extern "C" int qk_argmax_finish_launch(const float *cand_val, const int *cand_idx, int n, int *tok_out,
+                                       int *log, int *counter, int *pos, hipStream_t s) {
+    if (n <= 0 || !cand_val || !cand_idx || (log && !counter)) return QWEN_HIP_EINVAL;
+    argmax_finish<<<1, 256, 0, s>>>(cand_val, cand_idx, n, tok_out, log, counter, pos);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// ---------------------------------------------------------------------------
+// q/k RMSNorm + NeoX RoPE + K/V append.  One wave per (head, row); lane l
+// owns the RoPE pair (l, l+64) of the 128-wide head.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void rope_append(qk_rope_append_args a) {
+    const int hd = QWEN_HIP_HEAD_DIM, half = hd / 2;
+    const int lane = threadIdx.x;
+    const int head = blockIdx.x;                // [0, heads) q, [heads, heads+kv_heads) k/v
+    const int srow = blockIdx.y;
+    const int start = a.pos_dev ? *a.pos_dev : a.start;
+    const int p = start + srow;
+    const int qd = a.heads * hd, kvd = a.kv_heads * hd;
+    const float *row = a.qkv + (size_t)srow * (qd + 2 * kvd);
+    const bool is_q = head < a.heads;
+    const int kvh = head - a.heads;
+    const float *src = is_q ? row + head * hd : row + qd + kvh * hd;
+    const float *nw = is_q ? a.q_norm : a.k_norm;
+    float x1 = src[lane], x2 = src[lane + half];
+    float ss = fmaf(x1, x1, x2 * x2);
+    ss = wave_sum(ss);
+    const float rinv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+    x1 = (x1 * nw[lane]) * rinv;
+    x2 = (x2 * nw[lane + half]) * rinv;
+    const float c = a.rope_cos[(size_t)p * hd + lane];
+    const float sn = a.rope_sin[(size_t)p * hd + lane];
+    const float r1 = fmaf(x1, c, -(x2 * sn));
+    const float r2 = fmaf(x2, c, x1 * sn);
+    if (is_q) {
+        float *dst = a.q_out + (size_t)srow * qd + head * hd;
+        dst[lane] = r1;
+        dst[lane + half] = r2;
+    } else {
+        const size_t off = ((size_t)kvh * a.cap + p) * hd;
+        a.k_cache[off + lane] = r1;
+        a.k_cache[off + lane + half] = r2;
+        const float *vs = row + qd + kvd + kvh * hd;
+        a.v_cache[off + lane] = vs[lane];
+        a.v_cache[off + lane + half] = vs[lane + half];
+    }
+}
+
+extern "C" int qk_rope_append_launch(const qk_rope_append_args *a, hipStream_t s) {
+    if (!a || a->S <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads) return QWEN_HIP_EINVAL;
+    dim3 grid(a->heads + a->kv_heads, a->S);
+    rope_append<<<grid, 64, 0, s>>>(*a);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention.  Block (kv head, split) covers a contiguous range of
+// positions for the HPK query heads sharing that kv head, so each K/V row is
+// read once for all of them.  Sixteen lanes own one position (8 dims each);
+// a wave advances four positions per step and the four waves interleave.
+// Online softmax runs per 16-lane group; groups and waves merge in LDS, and
+// the splits merge in attn_combine.  Partials: [head][split][m, l, o[128]].
+// ---------------------------------------------------------------------------
+#define QK_ATTN_MIN_CHUNK 32
+
+__device__ __host__ __forceinline__ int attn_chunk(int seq_k, int nsplit) {
+    int c = (seq_k + nsplit - 1) / nsplit;
+    return c < QK_ATTN_MIN_CHUNK ? QK_ATTN_MIN_CHUNK : c;
+}
+
+template <int HPK>
+__global__ __launch_bounds__(256) void attn_decode_split(qk_attn_args a) {
+    const int hd = QWEN_HIP_HEAD_DIM;
+    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, gl = lane & 15;
+    const int seq_k = a.pos_dev ? *a.pos_dev + 1 : a.seq_k;
+    const int chunk = attn_chunk(seq_k, a.nsplit);
+    const int nsplit = (seq_k + chunk - 1) / chunk;
+    if (split >= nsplit) return;
+    const int s0 = split * chunk;
+    const int s1 = min(s0 + chunk, seq_k);
+
+    float q[HPK][8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        const float *qp = a.q + (size_t)(kvh * HPK + h) * hd + gl * 8;
+        float4 q0 = *reinterpret_cast<const float4 *>(qp);
+        float4 q1 = *reinterpret_cast<const float4 *>(qp + 4);
+        q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
+        q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
+    }
+    float m[HPK], l[HPK], o[HPK][8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[h][j] = 0.0f;
+    }
+    const float *kb = a.k + (size_t)kvh * a.head_stride + gl * 8;
+    const float *vb = a.v + (size_t)kvh * a.head_stride + gl * 8;
+    for (int p = s0 + wave * 4 + g; p < s1; p += 16) {
+        const float *kp = kb + (size_t)p * a.pos_stride;
+        const float *vp = vb + (size_t)p * a.pos_stride;
+        float4 k0 = *reinterpret_cast<const float4 *>(kp);
+        float4 k1 = *reinterpret_cast<const float4 *>(kp + 4);
+        float4 v0 = *reinterpret_cast<const float4 *>(vp);
+        float4 v1 = *reinterpret_cast<const float4 *>(vp + 4);
+        const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int h = 0; h < HPK; h++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) d = fmaf(q[h][j], kv[j], d);
+            d = group_sum<16>(d);
+            const float sc = d * a.scale;
+            const float mn = fmaxf(m[h], sc);
+            const float corr = __expf(m[h] - mn);
+            const float pw = __expf(sc - mn);
+            l[h] = fmaf(l[h], corr, pw);
+#pragma unroll
+            for (int j = 0; j < 8; j++) o[h][j] = fmaf(o[h][j], corr, pw * vv[j]);
+            m[h] = mn;
+        }
+    }
+
+    __shared__ float sm_m[16][HPK], sm_l[16][HPK];
+    __shared__ float sm_o[16][HPK][128];
+    const int grp = wave * 4 + g;
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        if (gl == 0) { sm_m[grp][h] = m[h]; sm_l[grp][h] = l[h]; }
+#pragma unroll
+        for (int j = 0; j < 8; j++) sm_o[grp][h][gl * 8 + j] = o[h][j];
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < HPK * hd; t += 256) {
+        const int h = t / hd, d = t % hd;
+        float M = -INFINITY;
+        for (int i = 0; i < 16; i++) M = fmaxf(M, sm_m[i][h]);
+        float L = 0.0f, acc = 0.0f;
+        for (int i = 0; i < 16; i++) {
+            const float mi = sm_m[i][h];
+            const float e = (mi == -INFINITY) ? 0.0f : __expf(mi - M);
+            L = fmaf(sm_l[i][h], e, L);
+            acc = fmaf(sm_o[i][h][d], e, acc);
+        }
+        float *pp = a.part + ((size_t)(kvh * HPK + h) * a.nsplit + split) * (hd + 2);
+        if (d == 0) { pp[0] = M; pp[1] = L; }
+        pp[2 + d] = acc;
+    }
+}
+
+__global__ __launch_bounds__(128) void attn_combine(qk_attn_args a) {
+    const int hd = QWEN_HIP_HEAD_DIM;
+    const int h = blockIdx.x, d = threadIdx.x;
+    const int seq_k = a.pos_dev ? *a.pos_dev + 1 : a.seq_k;
+    const int chunk = attn_chunk(seq_k, a.nsplit);
+    const int nsplit = (seq_k + chunk - 1) / chunk;
+    const float *pp = a.part + (size_t)h * a.nsplit * (hd + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, pp[(size_t)s * (hd + 2)]);
+    float L = 0.0f, acc = 0.0f;
+    for (int s = 0; s < nsplit; s++) {
+        const float *q = pp + (size_t)s * (hd + 2);
+        const float e = (q[0] == -INFINITY) ? 0.0f : __expf(q[0] - M);
+        L = fmaf(q[1], e, L);
+        acc = fmaf(q[2 + d], e, acc);
+    }
+    // the reference normalises by multiplying with 1/sum (qwen_asr_kernels.c:1091-1094)
+    a.out[(size_t)h * hd + d] = acc * (1.0f / L);
+}
+
+extern "C" int qk_attn_decode_launch(const qk_attn_args *a, hipStream_t s) {
+    if (!a || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads || a->nsplit <= 0 || !a->part)
+        return QWEN_HIP_EINVAL;
+    if (!a->pos_dev && a->seq_k <= 0) return QWEN_HIP_EINVAL;
+    const int hpk = a->heads / a->kv_heads;
+    dim3 grid(a->kv_heads, a->nsplit);
+    switch (hpk) {
+    case 1: attn_decode_split<1><<<grid, 256, 0, s>>>(*a); break;
+    case 2: attn_decode_split<2><<<grid, 256, 0, s>>>(*a); break;
+    case 4: attn_decode_split<4><<<grid, 256, 0, s>>>(*a); break;
+    default: return QWEN_HIP_EINVAL;
+    }
+    attn_combine<<<a->heads, 128, 0, s>>>(*a);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill attention (causal).  Block = 64 query rows of one head; four lanes
+// per query row, each owning 32 of the 128 dims.  K/V tiles of 32 positions
+// are staged in LDS and shared by all 64 rows.
+// ---------------------------------------------------------------------------
+#define QK_PA_ROWS 64
+#define QK_PA_TILE 32
+
+__global__ __launch_bounds__(256) void attn_prefill(qk_attn_args a) {
+    const int hd = QWEN_HIP_HEAD_DIM;
+    __shared__ float4 sk[QK_PA_TILE][hd / 4];
+    __shared__ float4 sv[QK_PA_TILE][hd / 4];
+    const int h = blockIdx.y;
+    const int kvh = h / (a.heads / a.kv_heads);
+    const int qi = blockIdx.x * QK_PA_ROWS + (threadIdx.x >> 2);
+    const int quarter = threadIdx.x & 3;
+    const int qstride = a.heads * hd;
+    const bool valid = qi < a.seq_q;
+
+    float4 q[8], o[8];
+    if (valid) {
+        const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)qi * qstride + h * hd + quarter * 32);
+#pragma unroll
+        for (int j = 0; j < 8; j++) q[j] = qp[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) q[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    float m = -INFINITY, l = 0.0f;
+
+    const int last_q = min(a.seq_q, (int)(blockIdx.x + 1) * QK_PA_ROWS) - 1;
+    const int kend_block = min(a.seq_k, a.q_offset + last_q + 1);
+    const int my_kend = valid ? min(a.seq_k, a.q_offset + qi + 1) : 0;
+    const float *kb = a.k + (size_t)kvh * a.head_stride;
+    const float *vb = a.v + (size_t)kvh * a.head_stride;
+
+    for (int t0 = 0; t0 < kend_block; t0 += QK_PA_TILE) {
+        const int nk = min(QK_PA_TILE, kend_block - t0);
+        __syncthreads();
+        for (int e = threadIdx.x; e < QK_PA_TILE * hd / 4; e += 256) {
+            const int r = e / (hd / 4), c = e % (hd / 4);
+            if (r < nk) {
+                sk[r][c] = *reinterpret_cast<const float4 *>(kb + (size_t)(t0 + r) * a.pos_stride + c * 4);
+                sv[r][c] = *reinterpret_cast<const float4 *>(vb + (size_t)(t0 + r) * a.pos_stride + c * 4);
+            }
+        }
+        __syncthreads();
+        const int jmax = min(nk, my_kend - t0);
+        for (int j = 0; j < nk; j++) {
+            // lanes of one query row agree on (j < jmax); rows in a wave may not
+            float d = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const float4 kk = sk[j][quarter * 8 + c];
+                d = fmaf(q[c].x, kk.x, d);
+                d = fmaf(q[c].y, kk.y, d);
+                d = fmaf(q[c].z, kk.z, d);
+                d = fmaf(q[c].w, kk.w, d);
+            }
+            d = group_sum<4>(d);
+            if (j < jmax) {
+                const float sc = d * a.scale;
+                const float mn = fmaxf(m, sc);
+                const float corr = __expf(m - mn);
+                const float pw = __expf(sc - mn);
+                l = fmaf(l, corr, pw);
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const float4 vv = sv[j][quarter * 8 + c];
+                    o[c].x = fmaf(o[c].x, corr, pw * vv.x);
+                    o[c].y = fmaf(o[c].y, corr, pw * vv.y);
+                    o[c].z = fmaf(o[c].z, corr, pw * vv.z);
+                    o[c].w = fmaf(o[c].w, corr, pw * vv.w);
+                }
+                m = mn;
+            }
+        }
+    }
+    if (!valid) return;
+    const float inv = (l > 0.0f) ? 1.0f / l : 0.0f;
+    const size_t base = (size_t)qi * qstride + h * hd + quarter * 32;
+    if (a.out) {
+        float4 *op = reinterpret_cast<float4 *>(a.out + base);
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            op[c] = make_float4(o[c].x * inv, o[c].y * inv, o[c].z * inv, o[c].w * inv);
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float vals[4] = {o[c].x * inv, o[c].y * inv, o[c].z * inv, o[c].w * inv};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint16_t hi = f32_to_bf16_rne(vals[e]);
+                const uint16_t lo = f32_to_bf16_rne(vals[e] - bf16_to_f32(hi));
+                a.out_hi[base + c * 4 + e] = hi;
+                a.out_lo[base + c * 4 + e] = lo;
+            }
+        }
+    }
+}
+
+extern "C" int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s) {
+    if (!a || a->seq_q <= 0 || a->seq_k <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads)
+        return QWEN_HIP_EINVAL;
+    if (!a->out && (!a->out_hi || !a->out_lo)) return QWEN_HIP_EINVAL;
+    dim3 grid((a->seq_q + QK_PA_ROWS - 1) / QK_PA_ROWS, a->heads);
+    attn_prefill<<<grid, 256, 0, s>>>(*a);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}

@@ -1,0 +1,111 @@
+/*
+ * qk_kernels.h - internal launcher interface between the C host code
+ * (csrc/host, C) and the HIP kernels (csrc/kernels, .hip files).  Plain C structs
+ * and functions; every launcher returns 0 or a negative QWEN_HIP_E* code and
+ * only launches (never synchronises).
+ */
+#ifndef QK_KERNELS_H
+#define QK_KERNELS_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- bandwidth-bound GEMV (decode) ---------------------------------- */
+enum { QK_EPI_STORE = 0, QK_EPI_ADD = 1, QK_EPI_SWIGLU = 2, QK_EPI_ARGMAX = 3 };
+
+typedef struct {
+    const uint16_t *W;        /* [rows][K] bf16 */
+    int rows, K;
+    const float *x;           /* [K] input row (unless gathered via tok) */
+    const float *norm_w;      /* non-NULL: input is rms_norm(x) * norm_w */
+    float eps;
+    const int *tok;           /* non-NULL and *tok >= 0: x = emb[*tok] widened */
+    const uint16_t *emb;      /* [vocab][K] bf16 for the gather */
+    float *x_store;           /* gather mode: block 0 writes the gathered row */
+    float *normed_store;      /* non-NULL: block 0 writes the (normed) input */
+    float *y;                 /* STORE/ADD: [rows]; SWIGLU: [rows/2] */
+    float *logits;            /* ARGMAX: optional [rows] */
+    float *cand_val;          /* ARGMAX: per-block winners */
+    int *cand_idx;
+    int epi;
+} qk_gemv_args;
+
+int qk_gemv_launch(const qk_gemv_args *a, hipStream_t s);
+/* number of blocks qk_gemv_launch uses (= candidates for ARGMAX) */
+int qk_gemv_blocks(int rows, int K, int epi);
+
+/* Reduce ARGMAX candidates: token = best; *tok_out = token (if non-NULL),
+ * log[*counter] = token and ++*counter (if log non-NULL), ++*pos (if
+ * non-NULL). */
+int qk_argmax_finish_launch(const float *cand_val, const int *cand_idx, int n,
+                            int *tok_out, int *log, int *counter, int *pos,
+                            hipStream_t s);
+
+/* ---- q/k RMSNorm + NeoX RoPE + KV append ---------------------------- */
+typedef struct {
+    const float *qkv;         /* [S][q_dim + 2*kv_dim] raw projections */
+    const float *q_norm, *k_norm;
+    float eps;
+    const float *rope_cos, *rope_sin;   /* [cap][head_dim], indexed by position */
+    float *k_cache, *v_cache; /* layer base, layout [kv_heads][cap][head_dim] */
+    int cap;
+    const int *pos_dev;       /* non-NULL: start position = *pos_dev */
+    int start;                /* start position when pos_dev is NULL */
+    int S, heads, kv_heads;
+    float *q_out;             /* [S][q_dim] normed + rotated queries */
+} qk_rope_append_args;
+
+int qk_rope_append_launch(const qk_rope_append_args *a, hipStream_t s);
+
+/* ---- causal GQA attention -------------------------------------------- */
+typedef struct {
+    const float *q;           /* [seq_q][heads*head_dim] */
+    const float *k, *v;       /* element (pos, kvh, d) at base + pos*pos_stride + kvh*head_stride + d */
+    long pos_stride, head_stride;
+    const int *pos_dev;       /* decode: seq_k = *pos_dev + 1 */
+    int seq_k;                /* decode without pos_dev / prefill: keys [0, seq_k) */
+    int seq_q, q_offset;      /* prefill: query i sees keys j <= q_offset + i */
+    int heads, kv_heads;
+    float scale;
+    float *part;              /* decode split partials [heads][nsplit][head_dim+2] */
+    int nsplit;
+    float *out;               /* fp32 [seq_q][heads*head_dim] */
+    uint16_t *out_hi, *out_lo;/* prefill alternative: bf16 hi/lo split of out */
+} qk_attn_args;
+
+int qk_attn_decode_launch(const qk_attn_args *a, hipStream_t s);
+int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s);
+
+/* ---- prefill (MFMA) ---------------------------------------------------- */
+/* hi/lo = bf16 split of rms_norm(x)*w (w NULL: of x itself): hi = bf16(v),
+ * lo = bf16(v - hi), so hi + lo carries v to ~2^-17 relative. */
+int qk_rmsnorm_split_launch(const float *x, const float *w, int S, int D, float eps,
+                            uint16_t *hi, uint16_t *lo, hipStream_t s);
+
+enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2 };
+/* Y[M][N] (=, +=) (A_hi + A_lo)[M][K] . W[N][K]^T on bf16 MFMA with fp32
+ * accumulation; SWIGLU writes silu(Y[:,2j]) * Y[:,2j+1] as a bf16 hi/lo
+ * split [M][N/2] into out_hi/out_lo. */
+int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W,
+                   int M, int N, int K, int epi, float *y,
+                   uint16_t *out_hi, uint16_t *out_lo, hipStream_t s);
+
+/* ---- elementwise (op-level ABI) --------------------------------------- */
+int qk_add_launch(float *a, const float *b, long n, hipStream_t s);
+int qk_rms_norm_launch(float *out, const float *x, const float *w, int S, int D,
+                       float eps, hipStream_t s);
+int qk_rms_norm_per_head_launch(float *x, const float *w, int S, int nh, int hd,
+                                float eps, hipStream_t s);
+int qk_rope_launch(float *x, const float *cos_v, const float *sin_v, int S, int nh,
+                   int hd, hipStream_t s);
+int qk_swiglu_launch(float *out, const float *gate_up, int S, int inter, hipStream_t s);
+int qk_split_bf16_launch(const float *x, long n, uint16_t *hi, uint16_t *lo, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,144 @@
+"""Op-level parity: each qwen_asr_kernels.h operator of the HIP library,
+called through the C ABI on device memory, against the CPU oracle on the same
+seeded inputs.  Tolerances are stated per test; fp32 accumulation order
+differs between the GPU and CPU, so GEMV checks use the rounding bound
+4*K*2^-24*sum|w*x| (and the bf16 hi/lo GEMM adds 2^-16*sum|w*x|)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def ptr(t):
+    return t.data_ptr()
+
+
+# the GEMV sweep (rows x cols), plus the true 1.7B 2048x2048
+SWEEP = [(2048, 1024), (1024, 2048), (6144, 1024), (1024, 3072), (151936, 1024), (4096, 2048),
+         (2048, 4096), (12288, 2048), (2048, 6144), (151936, 2048), (2048, 2048)]
+
+
+@pytest.mark.parametrize("rows,cols", SWEEP)
+def test_gemv_sweep(P, qa, gpu, rows, cols):
+    W = P.synth_bf16(rows * cols, 0, 9000 + rows + cols).reshape(rows, cols)
+    x = P.synth_uniform(cols, 0, 9100 + cols)
+    dW, dx = dev(gpu, W.view(np.int16)), dev(gpu, x)
+    dy = gpu.empty(rows, dtype=gpu.float32, device="cuda")
+    qa.check(qa.lib().qwen_hip_linear_nobias_bf16(ptr(dy), ptr(dx), ptr(dW), 1, cols, rows, None), "gemv")
+    gpu.cuda.synchronize()
+    y = host(dy)
+    yo = np.empty(rows, np.float32)
+    P.orc_lib().orc_linear_bf16(yo, x, W, 1, cols, rows)
+    Wf = P.bf16_to_f32(W)
+    absum = np.abs(Wf) @ np.abs(x)
+    bound = 8 * cols * 2.0 ** -24 * absum + 1e-12
+    assert np.all(np.abs(y - yo) <= bound), float(np.max(np.abs(y - yo) / bound))
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 64, 256), (31, 4096, 1024), (64, 1024, 2048), (401, 6144, 1024),
+                                   (130, 2048, 6144), (7, 100, 200)])
+def test_gemm_hilo(P, qa, gpu, M, N, K):
+    W = P.synth_bf16(N * K, 1, 9200 + N).reshape(N, K)
+    x = P.synth_f32(M * K, 1, 9300 + M).reshape(M, K)
+    dW, dx = dev(gpu, W.view(np.int16)), dev(gpu, x)
+    dy = gpu.empty((M, N), dtype=gpu.float32, device="cuda")
+    qa.check(qa.lib().qwen_hip_linear_nobias_bf16(ptr(dy), ptr(dx), ptr(dW), M, K, N, None), "gemm")
+    gpu.cuda.synchronize()
+    y = host(dy)
+    yo = np.empty((M, N), np.float32)
+    P.orc_lib().orc_linear_bf16(yo, x, W, M, K, N)
+    absum = np.abs(x) @ np.abs(P.bf16_to_f32(W)).T
+    bound = (2.0 ** -16 + 8 * K * 2.0 ** -24) * absum + 1e-12
+    assert np.all(np.abs(y - yo) <= bound), float(np.max(np.abs(y - yo) / bound))
+
+
+def test_elementwise_ops(P, qa, gpu):
+    lib, orc = qa.lib(), P.orc_lib()
+    r = np.random.default_rng(0)
+    S, D, nh, hd = 5, 1024, 16, 128
+    x = r.standard_normal((S, D)).astype(np.float32) * 2
+    w = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    # rms_norm, out-of-place and in place
+    dx, dw = dev(gpu, x), dev(gpu, w)
+    do = gpu.empty_like(dx)
+    qa.check(lib.qwen_hip_rms_norm(ptr(do), ptr(dx), ptr(dw), S, D, 1e-6, None))
+    qa.check(lib.qwen_hip_rms_norm(ptr(dx), ptr(dx), ptr(dw), S, D, 1e-6, None))
+    exp = np.empty_like(x)
+    orc.orc_rms_norm(exp, x, w, S, D, 1e-6)
+    gpu.cuda.synchronize()
+    np.testing.assert_allclose(host(do), exp, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(host(dx), exp, rtol=1e-5, atol=1e-6)
+    # per-head norm + rope
+    q = r.standard_normal((S, nh * hd)).astype(np.float32)
+    wh = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+    c = np.empty((9000, hd), np.float32)
+    s = np.empty((9000, hd), np.float32)
+    orc.orc_rope_table(c, s, 9000, hd, 1e6)
+    pos = np.array([0, 5, 400, 4000, 8999])
+    cs, ss = np.ascontiguousarray(c[pos]), np.ascontiguousarray(s[pos])
+    dq = dev(gpu, q)
+    qa.check(lib.qwen_hip_rms_norm_per_head(ptr(dq), ptr(dev(gpu, wh)), S, nh, hd, 1e-6, None))
+    qa.check(lib.qwen_hip_apply_rope_neox(ptr(dq), ptr(dev(gpu, cs)), ptr(dev(gpu, ss)), S, nh, hd, None))
+    e = q.copy()
+    orc.orc_rms_norm_per_head(e, wh, S, nh, hd, 1e-6)
+    orc.orc_apply_rope(e, cs, ss, S, nh, hd)
+    gpu.cuda.synchronize()
+    np.testing.assert_allclose(host(dq), e, rtol=1e-5, atol=2e-6)
+    # swiglu, out-of-place and in place; add
+    gu = r.standard_normal((3, 2 * 3072)).astype(np.float32) * 3
+    dgu = dev(gpu, gu)
+    dout = gpu.empty((3, 3072), dtype=gpu.float32, device="cuda")
+    qa.check(lib.qwen_hip_swiglu_multiply(ptr(dout), ptr(dgu), 3, 3072, None))
+    qa.check(lib.qwen_hip_swiglu_multiply(ptr(dgu), ptr(dgu), 3, 3072, None))
+    eo = np.empty((3, 3072), np.float32)
+    orc.orc_swiglu(eo, gu, 3, 3072)
+    gpu.cuda.synchronize()
+    np.testing.assert_allclose(host(dout), eo, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(host(dgu).reshape(-1)[:3 * 3072].reshape(3, 3072), eo, rtol=1e-5, atol=1e-6)
+    a, b = r.standard_normal(1000).astype(np.float32), r.standard_normal(1000).astype(np.float32)
+    da = dev(gpu, a)
+    qa.check(lib.qwen_hip_add_inplace(ptr(da), ptr(dev(gpu, b)), 1000, None))
+    gpu.cuda.synchronize()
+    assert np.array_equal(host(da), a + b)
+
+
+@pytest.mark.parametrize("sq,sk,q_off", [(1, 1, 0), (1, 529, 528), (1, 3000, 2999), (1, 100, 40),
+                                         (7, 7, 0), (64, 100, 36), (130, 130, 0), (33, 300, 200)])
+def test_causal_attention(P, qa, gpu, sq, sk, q_off):
+    nh, nkv, hd = 16, 8, 128
+    r = np.random.default_rng(sq * 1000 + sk)
+    Q = r.standard_normal((sq, nh * hd)).astype(np.float32)
+    K = r.standard_normal((sk, nkv * hd)).astype(np.float32)
+    V = r.standard_normal((sk, nkv * hd)).astype(np.float32)
+    scale = 1.0 / np.sqrt(128.0)
+    dout = gpu.empty((sq, nh * hd), dtype=gpu.float32, device="cuda")
+    qa.check(qa.lib().qwen_hip_causal_attention(ptr(dout), ptr(dev(gpu, Q)), ptr(dev(gpu, K)), ptr(dev(gpu, V)),
+                                                sq, sk, nh, nkv, hd, scale, q_off, None), "attention")
+    gpu.cuda.synchronize()
+    exp = np.empty((sq, nh * hd), np.float32)
+    P.orc_lib().orc_causal_attention(exp, Q, K, V, sq, sk, nh, nkv, hd, scale, q_off)
+    np.testing.assert_allclose(host(dout), exp, atol=3e-5, rtol=1e-4)
+
+
+def test_argmax_matvec(P, qa, gpu):
+    K, N = 1024, 151936
+    W = P.synth_bf16(N * K, 4, 1).reshape(N, K)
+    x = P.synth_uniform(K, 4, 2)
+    dW = dev(gpu, W.view(np.int16))
+    got = qa.check(qa.lib().qwen_hip_argmax_matvec_bf16(ptr(dev(gpu, x)), ptr(dW), K, N, None))
+    exp = P.orc_lib().orc_argmax_matvec_bf16(x, W, K, N, None)
+    assert got == exp
+    # exact ties resolve to the lowest row, across blocks
+    W2 = W.copy()
+    W2[3] = W[exp]
+    W2[N - 1] = W[exp]
+    got2 = qa.lib().qwen_hip_argmax_matvec_bf16(ptr(dev(gpu, x)), ptr(dev(gpu, W2.view(np.int16))), K, N, None)
+    assert got2 == 3
