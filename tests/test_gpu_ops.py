@@ -84,9 +84,11 @@ def test_elementwise_ops(P, qa, gpu):
     orc.orc_rope_table(c, s, 9000, hd, 1e6)
     pos = np.array([0, 5, 400, 4000, 8999])
     cs, ss = np.ascontiguousarray(c[pos]), np.ascontiguousarray(s[pos])
-    dq = dev(gpu, q)
-    qa.check(lib.qwen_hip_rms_norm_per_head(ptr(dq), ptr(dev(gpu, wh)), S, nh, hd, 1e-6, None))
-    qa.check(lib.qwen_hip_apply_rope_neox(ptr(dq), ptr(dev(gpu, cs)), ptr(dev(gpu, ss)), S, nh, hd, None))
+    # keep every device tensor referenced until the kernels ran: a temporary
+    # freed after data_ptr() lets the caching allocator hand its block out again
+    dq, dwh, dcs, dss = dev(gpu, q), dev(gpu, wh), dev(gpu, cs), dev(gpu, ss)
+    qa.check(lib.qwen_hip_rms_norm_per_head(ptr(dq), ptr(dwh), S, nh, hd, 1e-6, None))
+    qa.check(lib.qwen_hip_apply_rope_neox(ptr(dq), ptr(dcs), ptr(dss), S, nh, hd, None))
     e = q.copy()
     orc.orc_rms_norm_per_head(e, wh, S, nh, hd, 1e-6)
     orc.orc_apply_rope(e, cs, ss, S, nh, hd)
@@ -104,8 +106,8 @@ def test_elementwise_ops(P, qa, gpu):
     np.testing.assert_allclose(host(dout), eo, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(host(dgu).reshape(-1)[:3 * 3072].reshape(3, 3072), eo, rtol=1e-5, atol=1e-6)
     a, b = r.standard_normal(1000).astype(np.float32), r.standard_normal(1000).astype(np.float32)
-    da = dev(gpu, a)
-    qa.check(lib.qwen_hip_add_inplace(ptr(da), ptr(dev(gpu, b)), 1000, None))
+    da, db = dev(gpu, a), dev(gpu, b)
+    qa.check(lib.qwen_hip_add_inplace(ptr(da), ptr(db), 1000, None))
     gpu.cuda.synchronize()
     assert np.array_equal(host(da), a + b)
 
@@ -120,7 +122,8 @@ def test_causal_attention(P, qa, gpu, sq, sk, q_off):
     V = r.standard_normal((sk, nkv * hd)).astype(np.float32)
     scale = 1.0 / np.sqrt(128.0)
     dout = gpu.empty((sq, nh * hd), dtype=gpu.float32, device="cuda")
-    qa.check(qa.lib().qwen_hip_causal_attention(ptr(dout), ptr(dev(gpu, Q)), ptr(dev(gpu, K)), ptr(dev(gpu, V)),
+    dQ, dK, dV = dev(gpu, Q), dev(gpu, K), dev(gpu, V)
+    qa.check(qa.lib().qwen_hip_causal_attention(ptr(dout), ptr(dQ), ptr(dK), ptr(dV),
                                                 sq, sk, nh, nkv, hd, scale, q_off, None), "attention")
     gpu.cuda.synchronize()
     exp = np.empty((sq, nh * hd), np.float32)
@@ -132,13 +135,14 @@ def test_argmax_matvec(P, qa, gpu):
     K, N = 1024, 151936
     W = P.synth_bf16(N * K, 4, 1).reshape(N, K)
     x = P.synth_uniform(K, 4, 2)
-    dW = dev(gpu, W.view(np.int16))
-    got = qa.check(qa.lib().qwen_hip_argmax_matvec_bf16(ptr(dev(gpu, x)), ptr(dW), K, N, None))
+    dW, dx = dev(gpu, W.view(np.int16)), dev(gpu, x)
+    got = qa.check(qa.lib().qwen_hip_argmax_matvec_bf16(ptr(dx), ptr(dW), K, N, None))
     exp = P.orc_lib().orc_argmax_matvec_bf16(x, W, K, N, None)
     assert got == exp
     # exact ties resolve to the lowest row, across blocks
     W2 = W.copy()
     W2[3] = W[exp]
     W2[N - 1] = W[exp]
-    got2 = qa.lib().qwen_hip_argmax_matvec_bf16(ptr(dev(gpu, x)), ptr(dev(gpu, W2.view(np.int16))), K, N, None)
+    dW2 = dev(gpu, W2.view(np.int16))
+    got2 = qa.lib().qwen_hip_argmax_matvec_bf16(ptr(dx), ptr(dW2), K, N, None)
     assert got2 == 3
