@@ -19,10 +19,15 @@ CPU baseline: the reference decoder compiled from its sources (oracle/_ref,
 this host's cores.
 """
 import argparse
+import csv
+import glob
 import importlib
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -41,6 +46,45 @@ HBM_PEAK_GBS = 8000.0
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+DECODE_KERNELS = ("gemv_kernel", "attn_decode_fused", "attn_merge", "argmax_finish")
+
+
+def pmc_pass(counter, workload, timeout=150):
+    """One child run of this script under rocprofv3 --pmc <counter>: a short
+    decode (plus a 256 MiB calibration copy kernel).  Returns (KiB per decode
+    step summed over the step's kernels, calibration factor), or None."""
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        return None
+    out = tempfile.mkdtemp(prefix="qk_pmc_")
+    cmd = [exe, "--pmc", counter, "-d", out, "-o", "run", "--output-format", "csv", "--",
+           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--steps", "16", "--warmup", "2",
+           "--calib-copy-mb", "256", "--workload", workload]
+    env = dict(os.environ, TMPDIR="/tmp")
+    try:
+        subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                       timeout=timeout, check=False)
+        files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            return None
+        total, steps, cal = 0.0, 0, None
+        for r in csv.DictReader(open(files[0])):
+            name, v = r["Kernel_Name"], float(r["Counter_Value"])
+            if "AUnaryFunctor" in name:
+                cal = v
+            elif any(k in name for k in DECODE_KERNELS):
+                total += v
+                steps += "argmax_finish" in name
+        if not steps or not cal:
+            return None
+        factor = 256 * 1024 / cal
+        return total / steps * factor, factor
+    except (subprocess.SubprocessError, OSError, KeyError, ValueError):
+        return None
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
 
 
 def cpu_baseline(wl, rows, first_token, threads, decode_steps):
@@ -74,7 +118,11 @@ def main():
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c1")
     ap.add_argument("--engine", type=int, default=None, help="0 graph of fused kernels, 1 eager")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc child runs")
     ap.add_argument("--cpu-steps", type=int, default=48)
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="before timing, run one copy kernel (torch.mul by 1) over this many MiB: a "
+                         "known-size kernel that calibrates rocprofv3 read/write byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one decoder context per GPU; "
@@ -96,6 +144,16 @@ def main():
     rows, ids, emb = qa.prompt_rows(cfg, wl["n_audio"], wl["n_ids"])
     log(f"[gpu] {args.workload}: weights generated+uploaded in {time.time() - t0:.1f}s; {n_rows} input rows")
     stream = torch.cuda.ExternalStream(d.stream())
+    if args.calib_copy_mb:
+        # source written first, then 1 GiB of other writes so the source is no
+        # longer in the 256 MB last-level cache when the copy reads it
+        src = torch.ones(args.calib_copy_mb << 18, dtype=torch.float32, device="cuda")
+        evict = torch.full((1 << 28,), 2.0, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.mul(src, 1.0, out=dst)   # an elementwise kernel: reads and writes exactly N MiB
+        torch.cuda.synchronize()
+        del src, dst, evict
 
     # prefill (one untimed pass, then timed)
     d.prefill(rows[:-1])
@@ -126,6 +184,19 @@ def main():
     log(f"[gpu] decode {K} steps: wall {wall * 1e3:.2f} ms ({value:.1f} tok/s), events {gpu_ms:.2f} ms; "
         f"{avg_bytes / 1e9:.4f} GB/step -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
 
+    traffic = None
+    traffic_note = None
+    if not args.no_traffic:
+        fr = pmc_pass("FETCH_SIZE", args.workload)
+        wr = pmc_pass("WRITE_SIZE", args.workload)
+        if fr and wr:
+            traffic = round((fr[0] + wr[0]) * 1024)
+            traffic_note = (f"per decode step at positions {n_rows}-{n_rows + 17}: FETCH_SIZE x {fr[1]:.4f} + "
+                            f"WRITE_SIZE x {wr[1]:.4f} (factors from a 256 MiB copy kernel)")
+            log(f"[gpu] traffic per step {traffic / 1e6:.1f} MB ({traffic / avg_bytes:.3f} x algorithmic)")
+        else:
+            log("[gpu] rocprofv3 traffic passes unavailable: traffic null")
+
     cpu = None
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)
@@ -141,7 +212,7 @@ def main():
                    "prefill_rows": n_rows - 1, "decode_positions": [base, base + K - 1]},
         "prefill_tok_s": round((n_rows - 1) / prefill_s, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "kernel": "decode step (one token: all layers + LM head argmax)",
                      "bytes_per_launch": round(avg_bytes), "launch_us": round(gpu_ms * 1e3 / K, 3)},
         "cpu_baseline": cpu,

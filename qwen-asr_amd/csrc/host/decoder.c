@@ -49,7 +49,17 @@ void qwen_hip_config_preset(qwen_hip_config *c, int model_b) {
     c->rope_theta = 1e6f;
 }
 
-#define QK_NSPLIT 32          /* max position splits of decode attention */
+/* Decode attention split budgets.  Up to QK_SHORT_MAX cached positions the
+ * step uses at most QK_MERGE_MAX_SPLIT splits and the O-projection merges
+ * them in its prologue (graph variant 0); beyond that it uses up to
+ * QK_ATTN_MAX_SPLIT splits and a separate merge kernel (variant 1).  The
+ * host knows every step's position, so it picks the variant per step. */
+#define QK_SHORT_MAX 2048
+enum { STEP_SHORT = 0, STEP_LONG = 1, STEP_VARIANTS = 2 };
+
+/* Control block (one device allocation): the input token of the next step,
+ * its position (= kv_len) and the generate log cursor. */
+enum { CTL_TOK = 0, CTL_POS = 1, CTL_COUNTER = 2, CTL_INTS = 64 };
 
 struct qwen_hip_decoder {
     qwen_hip_config cfg;
@@ -75,8 +85,10 @@ struct qwen_hip_decoder {
     int kv_cap, kv_len;
 
     /* decode buffers */
-    float *x, *qkv, *qrot, *attn_part, *attn_out, *h, *hidden, *logits, *cand_val;
+    float *x, *qkv, *attn_out, *h, *hidden, *logits, *cand_val;
+    float *part_o, *part_m, *part_l; /* attention split partials */
     int *cand_idx, n_cand;
+    int *ctl;                 /* control block, see CTL_* */
     int *d_tok, *d_pos, *d_counter, *d_log, log_cap;
     float *h_row;             /* pinned staging */
     int *h_int;
@@ -86,9 +98,8 @@ struct qwen_hip_decoder {
     float *px, *pqkv, *pqrot;
     uint16_t *pxh, *pxl, *pah, *pal, *phh, *phl;
 
-    hipGraph_t graph;
-    hipGraphExec_t gexec;
-    int graph_valid;
+    hipGraph_t graph[STEP_VARIANTS];
+    hipGraphExec_t gexec[STEP_VARIANTS];
     int engine, keep_logits;
 };
 
@@ -114,11 +125,12 @@ static int use_device(const qwen_hip_decoder *d) {
 }
 
 static void graph_drop(qwen_hip_decoder *d) {
-    if (d->gexec) (void)hipGraphExecDestroy(d->gexec);
-    if (d->graph) (void)hipGraphDestroy(d->graph);
-    d->gexec = NULL;
-    d->graph = NULL;
-    d->graph_valid = 0;
+    for (int v = 0; v < STEP_VARIANTS; v++) {
+        if (d->gexec[v]) (void)hipGraphExecDestroy(d->gexec[v]);
+        if (d->graph[v]) (void)hipGraphDestroy(d->graph[v]);
+        d->gexec[v] = NULL;
+        d->graph[v] = NULL;
+    }
 }
 
 /* RoPE cos/sin table for positions [0, cap): ensure_rope_inv_freq and
@@ -264,24 +276,30 @@ qwen_hip_decoder *qwen_hip_decoder_create(const qwen_hip_config *cfg, int device
     d->n_cand = qk_gemv_blocks(cfg->vocab, cfg->hidden, QK_EPI_ARGMAX);
     d->log_cap = 4096;
     if (dev_alloc((void **)&d->x, D * 4) || dev_alloc((void **)&d->qkv, (size_t)d->qkv_rows * 4) ||
-        dev_alloc((void **)&d->qrot, (size_t)d->qd * 4) ||
-        dev_alloc((void **)&d->attn_part, (size_t)cfg->heads * QK_NSPLIT * (cfg->head_dim + 2) * 4) ||
+        dev_alloc((void **)&d->part_o, (size_t)cfg->heads * QK_ATTN_MAX_SPLIT * cfg->head_dim * 4) ||
+        dev_alloc((void **)&d->part_m, (size_t)cfg->heads * QK_ATTN_MAX_SPLIT * 4) ||
+        dev_alloc((void **)&d->part_l, (size_t)cfg->heads * QK_ATTN_MAX_SPLIT * 4) ||
         dev_alloc((void **)&d->attn_out, (size_t)d->qd * 4) || dev_alloc((void **)&d->h, I * 4) ||
         dev_alloc((void **)&d->hidden, D * 4) || dev_alloc((void **)&d->logits, (size_t)cfg->vocab * 4) ||
         dev_alloc((void **)&d->cand_val, (size_t)d->n_cand * 4) ||
         dev_alloc((void **)&d->cand_idx, (size_t)d->n_cand * 4) ||
-        dev_alloc((void **)&d->d_tok, 256) || dev_alloc((void **)&d->d_pos, 256) ||
-        dev_alloc((void **)&d->d_counter, 256) || dev_alloc((void **)&d->d_log, (size_t)d->log_cap * 4))
+        dev_alloc((void **)&d->ctl, CTL_INTS * 4) || dev_alloc((void **)&d->d_log, (size_t)d->log_cap * 4))
         goto fail;
+    d->d_tok = d->ctl + CTL_TOK;
+    d->d_pos = d->ctl + CTL_POS;
+    d->d_counter = d->ctl + CTL_COUNTER;
     if (hipHostMalloc((void **)&d->h_row, D * 4, hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc((void **)&d->h_int, 64, hipHostMallocDefault) != hipSuccess) {
+        hipHostMalloc((void **)&d->h_int, 256, hipHostMallocDefault) != hipSuccess) {
         qk_set_err("hipHostMalloc failed");
         goto fail;
     }
-    if (hipMemset(d->hidden, 0, D * 4) != hipSuccess || hipMemset(d->d_counter, 0, 256) != hipSuccess ||
-        hipMemset(d->d_pos, 0, 256) != hipSuccess) {
-        qk_set_err("hipMemset failed");
-        goto fail;
+    {
+        int init[CTL_INTS] = {0};
+        if (hipMemset(d->hidden, 0, D * 4) != hipSuccess ||
+            hipMemcpy(d->ctl, init, sizeof init, hipMemcpyHostToDevice) != hipSuccess) {
+            qk_set_err("control block init failed");
+            goto fail;
+        }
     }
     if (kv_reserve(d, kv_capacity > 0 ? kv_capacity : 1024)) goto fail;
     return d;
@@ -306,10 +324,9 @@ void qwen_hip_decoder_destroy(qwen_hip_decoder *d) {
     graph_drop(d);
     dev_free(d->wbuf);
     dev_free(d->kc); dev_free(d->vc); dev_free(d->rope_cos); dev_free(d->rope_sin);
-    dev_free(d->x); dev_free(d->qkv); dev_free(d->qrot); dev_free(d->attn_part);
+    dev_free(d->x); dev_free(d->qkv); dev_free(d->part_o); dev_free(d->part_m); dev_free(d->part_l);
     dev_free(d->attn_out); dev_free(d->h); dev_free(d->hidden); dev_free(d->logits);
-    dev_free(d->cand_val); dev_free(d->cand_idx); dev_free(d->d_tok); dev_free(d->d_pos);
-    dev_free(d->d_counter); dev_free(d->d_log);
+    dev_free(d->cand_val); dev_free(d->cand_idx); dev_free(d->ctl); dev_free(d->d_log);
     prefill_free(d);
     if (d->h_row) (void)hipHostFree(d->h_row);
     if (d->h_int) (void)hipHostFree(d->h_int);
@@ -484,9 +501,9 @@ int qwen_hip_decoder_prefill_device(qwen_hip_decoder *d, const float *d_rows, in
 /* ------------------------------------------------------------------------ */
 /* decode step: qwen_decoder_forward, qwen_asr_decoder.c:388-476            */
 /* ------------------------------------------------------------------------ */
-static int enqueue_step(qwen_hip_decoder *d) {
+static int enqueue_step(qwen_hip_decoder *d, int variant) {
     const qwen_hip_config *c = &d->cfg;
-    const int D = c->hidden, I = c->intermediate, hd = c->head_dim;
+    const int D = c->hidden, I = c->intermediate;
     hipStream_t s = d->stream;
     for (int l = 0; l < c->layers; l++) {
         /* input RMSNorm + Q|K|V; layer 0 also gathers the token embedding */
@@ -494,20 +511,29 @@ static int enqueue_step(qwen_hip_decoder *d) {
                           .eps = c->rms_eps, .y = d->qkv, .epi = QK_EPI_STORE};
         if (l == 0) { g.tok = d->d_tok; g.emb = d->emb; g.x_store = d->x; }
         QK_TRY(qk_gemv_launch(&g, s));
-        qk_rope_append_args ra = {
+        /* q/k norm + RoPE + K/V append + split attention (qwen_asr_decoder.c:439-455) */
+        qk_attn_fused_args aa = {
             .qkv = d->qkv, .q_norm = d->n_q[l], .k_norm = d->n_k[l], .eps = c->rms_eps,
             .rope_cos = d->rope_cos, .rope_sin = d->rope_sin, .k_cache = kc_layer(d, l),
-            .v_cache = vc_layer(d, l), .cap = d->kv_cap, .pos_dev = d->d_pos, .S = 1,
-            .heads = c->heads, .kv_heads = c->kv_heads, .q_out = d->qrot};
-        QK_TRY(qk_rope_append_launch(&ra, s));
-        qk_attn_args aa = {
-            .q = d->qrot, .k = kc_layer(d, l), .v = vc_layer(d, l), .pos_stride = hd,
-            .head_stride = (long)d->kv_cap * hd, .pos_dev = d->d_pos, .seq_q = 1, .heads = c->heads,
-            .kv_heads = c->kv_heads, .scale = d->scale, .part = d->attn_part, .nsplit = QK_NSPLIT,
-            .out = d->attn_out};
-        QK_TRY(qk_attn_decode_launch(&aa, s));
-        qk_gemv_args go = {.W = d->w_o[l], .rows = D, .K = d->qd, .x = d->attn_out, .y = d->x, .epi = QK_EPI_ADD};
+            .v_cache = vc_layer(d, l), .cap = d->kv_cap, .pos_dev = d->d_pos, .heads = c->heads,
+            .kv_heads = c->kv_heads, .scale = d->scale, .part_o = d->part_o, .part_m = d->part_m,
+            .part_l = d->part_l};
+        /* O projection + residual (:457-458), merging the attention splits */
+        qk_gemv_args go = {.W = d->w_o[l], .rows = D, .K = d->qd, .y = d->x, .epi = QK_EPI_ADD};
+        if (variant == STEP_SHORT) {
+            aa.nsplit = QK_MERGE_MAX_SPLIT;
+            QK_TRY(qk_attn_fused_launch(&aa, s));
+            go.merge_o = d->part_o; go.merge_m = d->part_m; go.merge_l = d->part_l;
+            go.merge_pos = d->d_pos; go.merge_nsplit = QK_MERGE_MAX_SPLIT;
+        } else {
+            aa.nsplit = QK_ATTN_MAX_SPLIT;
+            aa.out = d->attn_out;
+            QK_TRY(qk_attn_fused_launch(&aa, s));
+            QK_TRY(qk_attn_merge_launch(&aa, s));
+            go.x = d->attn_out;
+        }
         QK_TRY(qk_gemv_launch(&go, s));
+        /* post-attention RMSNorm + gate|up + SwiGLU (:460-466), down + residual (:467-468) */
         qk_gemv_args gu = {.W = d->w_gu[l], .rows = 2 * I, .K = D, .x = d->x, .norm_w = d->n_post[l],
                            .eps = c->rms_eps, .y = d->h, .epi = QK_EPI_SWIGLU};
         QK_TRY(qk_gemv_launch(&gu, s));
@@ -520,31 +546,33 @@ static int enqueue_step(qwen_hip_decoder *d) {
                        .cand_val = d->cand_val, .cand_idx = d->cand_idx, .epi = QK_EPI_ARGMAX};
     QK_TRY(qk_gemv_launch(&gl, s));
     QK_TRY(qk_argmax_finish_launch(d->cand_val, d->cand_idx, d->n_cand, d->d_tok, d->d_log, d->d_counter,
-                                   d->d_pos, s));
+                                   d->d_pos, NULL, s));
     return 0;
 }
 
-static int graph_ensure(qwen_hip_decoder *d) {
-    if (d->graph_valid) return 0;
-    graph_drop(d);
+static int graph_ensure(qwen_hip_decoder *d, int v) {
+    if (d->gexec[v]) return 0;
     QK_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(d);
+    int rc = enqueue_step(d, v);
     hipGraph_t g = NULL;
     hipError_t e = hipStreamEndCapture(d->stream, &g);
     if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
     if (e != hipSuccess) { qk_set_err("hipStreamEndCapture: %s", hipGetErrorString(e)); return QWEN_HIP_EDEVICE; }
-    d->graph = g;
-    QK_HIP(hipGraphInstantiate(&d->gexec, g, NULL, NULL, 0));
-    d->graph_valid = 1;
+    d->graph[v] = g;
+    QK_HIP(hipGraphInstantiate(&d->gexec[v], g, NULL, NULL, 0));
     return 0;
 }
 
+/* n steps starting at position kv_len: step i attends over kv_len + i + 1 keys */
 static int launch_steps(qwen_hip_decoder *d, int n) {
-    if (d->engine == 0) {
-        QK_TRY(graph_ensure(d));
-        for (int i = 0; i < n; i++) QK_HIP(hipGraphLaunch(d->gexec, d->stream));
-    } else {
-        for (int i = 0; i < n; i++) QK_TRY(enqueue_step(d));
+    for (int i = 0; i < n; i++) {
+        const int v = (d->kv_len + i + 1 <= QK_SHORT_MAX) ? STEP_SHORT : STEP_LONG;
+        if (d->engine == 0) {
+            QK_TRY(graph_ensure(d, v));
+            QK_HIP(hipGraphLaunch(d->gexec[v], d->stream));
+        } else {
+            QK_TRY(enqueue_step(d, v));
+        }
     }
     return 0;
 }
@@ -567,10 +595,10 @@ static int forward_staged(qwen_hip_decoder *d) {
     d->h_int[2] = 0;
     QK_HIP(hipMemcpyAsync(d->d_counter, &d->h_int[2], sizeof(int), hipMemcpyHostToDevice, d->stream));
     QK_TRY(launch_steps(d, 1));
-    QK_HIP(hipMemcpyAsync(&d->h_int[3], d->d_tok, sizeof(int), hipMemcpyDeviceToHost, d->stream));
+    QK_HIP(hipMemcpyAsync(&d->h_int[8], d->ctl, 4 * sizeof(int), hipMemcpyDeviceToHost, d->stream));
     QK_HIP(hipStreamSynchronize(d->stream));
     d->kv_len += 1;
-    return d->h_int[3];
+    return d->h_int[8 + CTL_TOK];
 }
 
 static int forward_prepare(qwen_hip_decoder *d, int steps) {

@@ -136,7 +136,7 @@ int qwen_hip_argmax_matvec_bf16(const float *x, const uint16_t *W, int in_dim, i
         qk_gemv_args g = {.W = W, .rows = out_dim, .K = in_dim, .x = x, .cand_val = cv, .cand_idx = ci,
                           .epi = QK_EPI_ARGMAX};
         rc = qk_gemv_launch(&g, s);
-        if (!rc) rc = qk_argmax_finish_launch(cv, ci, nb, tok, NULL, NULL, NULL, s);
+        if (!rc) rc = qk_argmax_finish_launch(cv, ci, nb, tok, NULL, NULL, NULL, NULL, s);
         if (!rc && hipMemcpyAsync(&result, tok, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess)
             rc = QWEN_HIP_EDEVICE;
         if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = QWEN_HIP_EDEVICE;

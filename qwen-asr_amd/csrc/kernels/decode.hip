@@ -11,7 +11,10 @@
 //  rope_append        per-head q/k RMSNorm (:811-873) + NeoX RoPE
 //                     (:1182-1247) + K/V append (qwen_asr_decoder.c:446-447).
 //  attn_decode_split  one query row against the fp32 KV cache, split over
-//  attn_combine       positions (qwen_causal_attention, :1050-1141).
+//  attn_combine       positions (qwen_causal_attention, :1050-1141); used by
+//                     the op-level ABI.
+//  attn_decode_fused  the decoder's per-layer attention: q/k norm + RoPE + K/V
+//                     append + split attention + in-kernel combine.
 //  attn_prefill       many query rows, causal, K/V tiles staged in LDS.
 #include "common.h"
 #include "qk_kernels.h"
@@ -76,10 +79,66 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
     const int wave = threadIdx.x >> 6;
     const int K = a.K, R = a.rows;
 
+    // The first rows' weights do not depend on the input row: issue their
+    // loads before the prologue so HBM latency overlaps the gather / norm.
+    const int rows_per_block = 4 * ROWS * iters;
+    uint4 w[ROWS][NC];
+    int rbase = blockIdx.x * rows_per_block + wave * ROWS;
+    if (rbase < R) gemv_load<NC, ROWS>(w, a.W, R, K, rbase, lane);
+
     // ---- prologue: the input row, optionally gathered and RMS-normed ----
     float xr[NC][8];
     int tok = -1;
     if (a.tok) tok = *a.tok;
+    if (a.merge_o) {
+        // The input is the attention output, merged here from its position
+        // splits (m, l, o): x = (sum_s o_s e^(m_s - M)) * (1 / sum_s l_s e^(m_s - M)).
+        // Thread t merges columns [8t, 8t + 8) into LDS for the whole block.
+        __shared__ __attribute__((aligned(16))) float xs[QK_MERGE_MAX_K];
+        const int seq_k = *a.merge_pos + 1;
+        const int ck = qk_attn_chunk(seq_k, a.merge_nsplit);
+        const int ns = (seq_k + ck - 1) / ck;
+        for (int t = threadIdx.x; t * 8 < K; t += 256) {
+            const int col = t * 8, h = col >> 7, d = col & 127;
+            const float *pm = a.merge_m + (size_t)h * a.merge_nsplit;
+            const float *pl = a.merge_l + (size_t)h * a.merge_nsplit;
+            const float *po = a.merge_o + (size_t)h * a.merge_nsplit * 128 + d;
+            float mv[QK_MERGE_MAX_SPLIT], lv[QK_MERGE_MAX_SPLIT];
+            float4 oa[QK_MERGE_MAX_SPLIT], ob[QK_MERGE_MAX_SPLIT];
+#pragma unroll
+            for (int s = 0; s < QK_MERGE_MAX_SPLIT; s++)
+                if (s < ns) {
+                    mv[s] = pm[s];
+                    lv[s] = pl[s];
+                    oa[s] = *reinterpret_cast<const float4 *>(po + (size_t)s * 128);
+                    ob[s] = *reinterpret_cast<const float4 *>(po + (size_t)s * 128 + 4);
+                }
+            float M = -INFINITY;
+#pragma unroll
+            for (int s = 0; s < QK_MERGE_MAX_SPLIT; s++) if (s < ns) M = fmaxf(M, mv[s]);
+            float L = 0.0f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < QK_MERGE_MAX_SPLIT; s++)
+                if (s < ns) {
+                    const float e = (mv[s] == -INFINITY) ? 0.0f : __expf(mv[s] - M);
+                    L = fmaf(lv[s], e, L);
+                    acc[0] = fmaf(oa[s].x, e, acc[0]); acc[1] = fmaf(oa[s].y, e, acc[1]);
+                    acc[2] = fmaf(oa[s].z, e, acc[2]); acc[3] = fmaf(oa[s].w, e, acc[3]);
+                    acc[4] = fmaf(ob[s].x, e, acc[4]); acc[5] = fmaf(ob[s].y, e, acc[5]);
+                    acc[6] = fmaf(ob[s].z, e, acc[6]); acc[7] = fmaf(ob[s].w, e, acc[7]);
+                }
+            const float inv = 1.0f / L;        // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
+#pragma unroll
+            for (int j = 0; j < 8; j++) xs[col + j] = acc[j] * inv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int col = c * 512 + lane * 8;
+#pragma unroll
+            for (int j = 0; j < 8; j++) xr[c][j] = (col < K) ? xs[col + j] : 0.0f;
+        }
+    } else
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         const int col = c * 512 + lane * 8;
@@ -137,12 +196,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
     }
 
     // ---- rows ----
-    const int rows_per_block = 4 * ROWS * iters;
     float best_v = -1e30f;
     int best_i = 0x7fffffff;
-    uint4 w[ROWS][NC];
-    int rbase = blockIdx.x * rows_per_block + wave * ROWS;
-    if (rbase < R) gemv_load<NC, ROWS>(w, a.W, R, K, rbase, lane);
     for (int it = 0; it < iters; it++) {
         if (rbase >= R) break;
         const int rnext = rbase + 4 * ROWS;
@@ -162,7 +217,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
             reduce_rows<ROWS, 2>(acc, lane);
             const int span = 128 / ROWS;                 // lanes per (g,u) pair
             const int r = rbase + 2 * (lane / span);
-            if ((lane % span) == 0 && r + 1 < R + 1 && r < R)
+            if ((lane % span) == 0 && r < R)
                 a.y[r >> 1] = swiglu1(acc[0], acc[1]);
         } else {
             reduce_rows<ROWS, 1>(acc, lane);
@@ -251,7 +306,10 @@ extern "C" int qk_gemv_launch(const qk_gemv_args *a, hipStream_t s) {
     if (a->epi == QK_EPI_SWIGLU && (a->rows & 1)) return QWEN_HIP_EINVAL;
     if (a->epi == QK_EPI_ARGMAX && (!a->cand_val || !a->cand_idx)) return QWEN_HIP_EINVAL;
     if (a->epi != QK_EPI_ARGMAX && !a->y) return QWEN_HIP_EINVAL;
-    if (!a->x && !a->tok) return QWEN_HIP_EINVAL;
+    if (!a->x && !a->tok && !a->merge_o) return QWEN_HIP_EINVAL;
+    if (a->merge_o && (!a->merge_m || !a->merge_l || !a->merge_pos || a->merge_nsplit <= 0 ||
+                       a->merge_nsplit > QK_MERGE_MAX_SPLIT || a->K > QK_MERGE_MAX_K || (a->K & 127) || a->tok))
+        return QWEN_HIP_EINVAL;
     if (a->tok && !a->emb) return QWEN_HIP_EINVAL;
     const int rows_pw = gemv_pick_rows(a->rows, a->epi);
     const int iters = gemv_pick_iters(a->K, a->epi);
@@ -275,7 +333,7 @@ extern "C" int qk_gemv_launch(const qk_gemv_args *a, hipStream_t s) {
 // Argmax, second pass: one block reduces the per-block winners.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void argmax_finish(const float *cv, const int *ci, int n, int *tok_out,
-                                                     int *log, int *counter, int *pos) {
+                                                     int *log, int *counter, int *pos, unsigned *epoch) {
     float bv = -1e30f;
     int bi = 0x7fffffff;
     for (int i = threadIdx.x; i < n; i += 256)
@@ -303,13 +361,14 @@ __global__ __launch_bounds__(256) void argmax_finish(const float *cv, const int 
             *counter = c + 1;
         }
         if (pos) *pos = *pos + 1;
+        if (epoch) *epoch = *epoch + 1;
     }
 }
 
 extern "C" int qk_argmax_finish_launch(const float *cand_val, const int *cand_idx, int n, int *tok_out,
-                                       int *log, int *counter, int *pos, hipStream_t s) {
+                                       int *log, int *counter, int *pos, unsigned *epoch, hipStream_t s) {
     if (n <= 0 || !cand_val || !cand_idx || (log && !counter)) return QWEN_HIP_EINVAL;
-    argmax_finish<<<1, 256, 0, s>>>(cand_val, cand_idx, n, tok_out, log, counter, pos);
+    argmax_finish<<<1, 256, 0, s>>>(cand_val, cand_idx, n, tok_out, log, counter, pos, epoch);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 
@@ -369,11 +428,11 @@ extern "C" int qk_rope_append_launch(const qk_rope_append_args *a, hipStream_t s
 // Online softmax runs per 16-lane group; groups and waves merge in LDS, and
 // the splits merge in attn_combine.  Partials: [head][split][m, l, o[128]].
 // ---------------------------------------------------------------------------
-#define QK_ATTN_MIN_CHUNK 32
+#define QK_OPATTN_MIN_CHUNK 32
 
 __device__ __host__ __forceinline__ int attn_chunk(int seq_k, int nsplit) {
     int c = (seq_k + nsplit - 1) / nsplit;
-    return c < QK_ATTN_MIN_CHUNK ? QK_ATTN_MIN_CHUNK : c;
+    return c < QK_OPATTN_MIN_CHUNK ? QK_OPATTN_MIN_CHUNK : c;
 }
 
 template <int HPK>
@@ -606,5 +665,222 @@ extern "C" int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s) {
     if (!a->out && (!a->out_hi || !a->out_lo)) return QWEN_HIP_EINVAL;
     dim3 grid((a->seq_q + QK_PA_ROWS - 1) / QK_PA_ROWS, a->heads);
     attn_prefill<<<grid, 256, 0, s>>>(*a);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// ---------------------------------------------------------------------------
+// Fused decode attention: one launch per layer does what the reference does
+// in qwen_asr_decoder.c:439-455 -- q/k RMSNorm, NeoX RoPE, K/V append at
+// `pos`, causal GQA attention over [0, pos] -- split over positions.  Each
+// 16-lane group owns every 16th position of its split and prefetches the
+// K/V rows of its next QK_AB positions into registers while it folds the
+// current ones into its online softmax, so the position loop streams instead
+// of paying one memory latency per position.  Splits write unnormalised
+// partials (m, l, o[128]) with plain stores; the merge runs in the next
+// kernel (the O-projection prologue for <= 8 splits, attn_merge otherwise).
+// ---------------------------------------------------------------------------
+#define QK_AB 4
+
+// one lane pair (l, l+64) of a 128-wide head: RMSNorm with weight, then RoPE
+__device__ __forceinline__ void norm_rope_pair(float &x1, float &x2, const float *nw, float eps, float c, float sn,
+                                               int lane) {
+    float ss = wave_sum(fmaf(x1, x1, x2 * x2));
+    const float rinv = 1.0f / sqrtf(ss / 128.0f + eps);
+    const float a = (x1 * nw[lane]) * rinv, b = (x2 * nw[lane + 64]) * rinv;
+    x1 = fmaf(a, c, -(b * sn));
+    x2 = fmaf(b, c, a * sn);
+}
+
+template <int HPK>
+__device__ __forceinline__ void attn_fold(const float (&q)[HPK][8], float4 k0, float4 k1, float4 v0, float4 v1,
+                                          float scale, float (&m)[HPK], float (&l)[HPK], float (&o)[HPK][8]) {
+    const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) d = fmaf(q[h][j], kv[j], d);
+        d = group_sum<16>(d);
+        const float sc = d * scale;
+        const float mn = fmaxf(m[h], sc);
+        const float corr = __expf(m[h] - mn), pw = __expf(sc - mn);
+        l[h] = fmaf(l[h], corr, pw);
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[h][j] = fmaf(o[h][j], corr, pw * vv[j]);
+        m[h] = mn;
+    }
+}
+
+template <int HPK>
+__global__ __launch_bounds__(256) void attn_decode_fused(qk_attn_fused_args a) {
+    const int hd = QWEN_HIP_HEAD_DIM;
+    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, gl = lane & 15;
+    const int pos = *a.pos_dev, seq_k = pos + 1;
+    const int chunk = qk_attn_chunk(seq_k, a.nsplit);
+    const int nsplit = (seq_k + chunk - 1) / chunk;
+    if (split >= nsplit) return;
+    const int s0 = split * chunk, s1 = min(s0 + chunk, seq_k);
+    const bool last_split = (s1 == seq_k);
+    const int cached_end = last_split ? pos : s1;        // position pos itself comes from LDS
+    const int qd = a.heads * hd, kvd = a.kv_heads * hd;
+
+    // prefetch the first batch of cached K/V rows (independent of this step's q)
+    const float *kb = a.k_cache + (size_t)kvh * a.cap * hd + gl * 8;
+    const float *vb = a.v_cache + (size_t)kvh * a.cap * hd + gl * 8;
+    const int p0 = s0 + wave * 4 + g;
+    float4 ck[QK_AB][2], cv[QK_AB][2];
+#pragma unroll
+    for (int j = 0; j < QK_AB; j++) {
+        const int p = p0 + 16 * j;
+        if (p < cached_end) {
+            ck[j][0] = *reinterpret_cast<const float4 *>(kb + (size_t)p * hd);
+            ck[j][1] = *reinterpret_cast<const float4 *>(kb + (size_t)p * hd + 4);
+            cv[j][0] = *reinterpret_cast<const float4 *>(vb + (size_t)p * hd);
+            cv[j][1] = *reinterpret_cast<const float4 *>(vb + (size_t)p * hd + 4);
+        }
+    }
+
+    __shared__ __attribute__((aligned(16))) float qs[HPK][128];
+    __shared__ __attribute__((aligned(16))) float knew[128];
+    __shared__ __attribute__((aligned(16))) float vnew[128];
+    __shared__ float sm_m[16][HPK], sm_l[16][HPK];
+    __shared__ float sm_o[16][HPK][128];
+
+    const float c = a.rope_cos[(size_t)pos * hd + lane], sn = a.rope_sin[(size_t)pos * hd + lane];
+    if (wave < HPK) {                       // query heads of this group
+        const float *src = a.qkv + (size_t)(kvh * HPK + wave) * hd;
+        float x1 = src[lane], x2 = src[lane + 64];
+        norm_rope_pair(x1, x2, a.q_norm, a.eps, c, sn, lane);
+        qs[wave][lane] = x1;
+        qs[wave][lane + 64] = x2;
+    }
+    if (last_split && wave == (HPK < 4 ? HPK : 0)) {    // this step's key and value
+        const float *ks = a.qkv + qd + (size_t)kvh * hd;
+        const float *vs = a.qkv + qd + kvd + (size_t)kvh * hd;
+        float x1 = ks[lane], x2 = ks[lane + 64];
+        norm_rope_pair(x1, x2, a.k_norm, a.eps, c, sn, lane);
+        const float v1 = vs[lane], v2 = vs[lane + 64];
+        knew[lane] = x1; knew[lane + 64] = x2;
+        vnew[lane] = v1; vnew[lane + 64] = v2;
+        const size_t off = ((size_t)kvh * a.cap + pos) * hd;
+        a.k_cache[off + lane] = x1; a.k_cache[off + lane + 64] = x2;
+        a.v_cache[off + lane] = v1; a.v_cache[off + lane + 64] = v2;
+    }
+    __syncthreads();
+
+    float q[HPK][8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) q[h][j] = qs[h][gl * 8 + j];
+    float m[HPK], l[HPK], o[HPK][8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[h][j] = 0.0f;
+    }
+    for (int pb = p0; pb < cached_end; pb += 16 * QK_AB) {
+        float4 nk[QK_AB][2], nv[QK_AB][2];
+        const int pn = pb + 16 * QK_AB;
+#pragma unroll
+        for (int j = 0; j < QK_AB; j++) {
+            const int p = pn + 16 * j;
+            if (p < cached_end) {
+                nk[j][0] = *reinterpret_cast<const float4 *>(kb + (size_t)p * hd);
+                nk[j][1] = *reinterpret_cast<const float4 *>(kb + (size_t)p * hd + 4);
+                nv[j][0] = *reinterpret_cast<const float4 *>(vb + (size_t)p * hd);
+                nv[j][1] = *reinterpret_cast<const float4 *>(vb + (size_t)p * hd + 4);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < QK_AB; j++)
+            if (pb + 16 * j < cached_end) attn_fold<HPK>(q, ck[j][0], ck[j][1], cv[j][0], cv[j][1], a.scale, m, l, o);
+#pragma unroll
+        for (int j = 0; j < QK_AB; j++) {
+            ck[j][0] = nk[j][0]; ck[j][1] = nk[j][1];
+            cv[j][0] = nv[j][0]; cv[j][1] = nv[j][1];
+        }
+    }
+    if (last_split && wave == 0 && g == 0) {
+        const float4 *kn = reinterpret_cast<const float4 *>(&knew[gl * 8]);
+        const float4 *vn = reinterpret_cast<const float4 *>(&vnew[gl * 8]);
+        attn_fold<HPK>(q, kn[0], kn[1], vn[0], vn[1], a.scale, m, l, o);
+    }
+
+    const int grp = wave * 4 + g;
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        if (gl == 0) { sm_m[grp][h] = m[h]; sm_l[grp][h] = l[h]; }
+#pragma unroll
+        for (int j = 0; j < 8; j++) sm_o[grp][h][gl * 8 + j] = o[h][j];
+    }
+    __syncthreads();
+    // merge the 16 groups; thread t -> (head t / 128, dim t % 128)
+    for (int t = threadIdx.x; t < HPK * hd; t += 256) {
+        const int h = t / hd, d = t % hd;
+        float M = -INFINITY;
+        for (int i = 0; i < 16; i++) M = fmaxf(M, sm_m[i][h]);
+        float L = 0.0f, acc = 0.0f;
+        for (int i = 0; i < 16; i++) {
+            const float mi = sm_m[i][h];
+            const float e = (mi == -INFINITY) ? 0.0f : __expf(mi - M);
+            L = fmaf(sm_l[i][h], e, L);
+            acc = fmaf(sm_o[i][h][d], e, acc);
+        }
+        const int hq = kvh * HPK + h;
+        if (nsplit == 1 && a.out) {
+            a.out[(size_t)hq * hd + d] = acc * (1.0f / L);
+        } else {
+            a.part_o[((size_t)hq * a.nsplit + split) * hd + d] = acc;
+            if (d == 0) {
+                a.part_m[(size_t)hq * a.nsplit + split] = M;
+                a.part_l[(size_t)hq * a.nsplit + split] = L;
+            }
+        }
+    }
+}
+
+extern "C" int qk_attn_fused_launch(const qk_attn_fused_args *a, hipStream_t s) {
+    if (!a || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads || a->nsplit <= 0 ||
+        a->nsplit > QK_ATTN_MAX_SPLIT || !a->part_o || !a->part_m || !a->part_l || !a->pos_dev)
+        return QWEN_HIP_EINVAL;
+    dim3 grid(a->kv_heads, a->nsplit);
+    switch (a->heads / a->kv_heads) {
+    case 1: attn_decode_fused<1><<<grid, 256, 0, s>>>(*a); break;
+    case 2: attn_decode_fused<2><<<grid, 256, 0, s>>>(*a); break;
+    case 4: attn_decode_fused<4><<<grid, 256, 0, s>>>(*a); break;
+    default: return QWEN_HIP_EINVAL;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// Merge of the split partials into out[head][128] (long contexts).
+__global__ __launch_bounds__(128) void attn_merge(const float *part_o, const float *part_m, const float *part_l,
+                                                   int nsplit_max, const int *pos_dev, float *out) {
+    const int hd = QWEN_HIP_HEAD_DIM, h = blockIdx.x, d = threadIdx.x;
+    const int seq_k = *pos_dev + 1;
+    const int chunk = qk_attn_chunk(seq_k, nsplit_max);
+    const int ns = (seq_k + chunk - 1) / chunk;
+    const float *pm = part_m + (size_t)h * nsplit_max, *pl = part_l + (size_t)h * nsplit_max;
+    const float *po = part_o + (size_t)h * nsplit_max * hd + d;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; s++) M = fmaxf(M, pm[s]);
+    float L = 0.0f, acc = 0.0f;
+    for (int s = 0; s < ns; s++) {
+        const float e = (pm[s] == -INFINITY) ? 0.0f : __expf(pm[s] - M);
+        L = fmaf(pl[s], e, L);
+        acc = fmaf(po[(size_t)s * hd], e, acc);
+    }
+    out[(size_t)h * hd + d] = acc * (1.0f / L);
+}
+
+extern "C" int qk_attn_merge_launch(const qk_attn_fused_args *a, hipStream_t s) {
+    if (!a || !a->out || !a->pos_dev) return QWEN_HIP_EINVAL;
+    attn_merge<<<a->heads, 128, 0, s>>>(a->part_o, a->part_m, a->part_l, a->nsplit, a->pos_dev, a->out);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }

@@ -32,18 +32,26 @@ typedef struct {
     float *cand_val;          /* ARGMAX: per-block winners */
     int *cand_idx;
     int epi;
+    /* merge prologue: the input row is the attention output merged from
+     * split partials (K = heads*128); replaces x */
+    const float *merge_o, *merge_m, *merge_l;
+    const int *merge_pos;     /* seq_k = *merge_pos + 1 */
+    int merge_nsplit;         /* split budget the partials were written with */
 } qk_gemv_args;
+
+#define QK_MERGE_MAX_SPLIT 8      /* merge prologue: at most this many splits */
+#define QK_MERGE_MAX_K 2048       /* ... over an input row of at most this length */
 
 int qk_gemv_launch(const qk_gemv_args *a, hipStream_t s);
 /* number of blocks qk_gemv_launch uses (= candidates for ARGMAX) */
 int qk_gemv_blocks(int rows, int K, int epi);
 
 /* Reduce ARGMAX candidates: token = best; *tok_out = token (if non-NULL),
- * log[*counter] = token and ++*counter (if log non-NULL), ++*pos (if
- * non-NULL). */
+ * log[*counter] = token and ++*counter (if log non-NULL), ++*pos and
+ * ++*epoch (each if non-NULL). */
 int qk_argmax_finish_launch(const float *cand_val, const int *cand_idx, int n,
                             int *tok_out, int *log, int *counter, int *pos,
-                            hipStream_t s);
+                            unsigned *epoch, hipStream_t s);
 
 /* ---- q/k RMSNorm + NeoX RoPE + KV append ---------------------------- */
 typedef struct {
@@ -79,6 +87,42 @@ typedef struct {
 
 int qk_attn_decode_launch(const qk_attn_args *a, hipStream_t s);
 int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s);
+
+/* ---- fused decode attention (one kernel per layer) -------------------- */
+/* q/k RMSNorm + RoPE + K/V append + split attention.  Positions [0, pos]
+ * are cut into nsplit' = ceil((pos+1)/chunk) splits of
+ * chunk = max(QK_ATTN_MIN_CHUNK, ceil((pos+1)/nsplit)); each split writes the
+ * unnormalised partials (m, l, o[head_dim]) of its query heads.  With a
+ * single split the result goes straight to `out`.  The merge is
+ * qk_attn_merge_launch or the O-projection GEMV prologue (QK_PRO_MERGE). */
+#define QK_ATTN_MIN_CHUNK 64
+#define QK_ATTN_MAX_SPLIT 32
+#ifdef __cplusplus
+__host__ __device__
+#endif
+static inline int qk_attn_chunk(int seq_k, int nsplit) {
+    int c = (seq_k + nsplit - 1) / nsplit;
+    return c < QK_ATTN_MIN_CHUNK ? QK_ATTN_MIN_CHUNK : c;
+}
+
+typedef struct {
+    const float *qkv;                  /* raw [q_dim + 2*kv_dim] */
+    const float *q_norm, *k_norm;
+    float eps;
+    const float *rope_cos, *rope_sin;  /* [cap][head_dim] */
+    float *k_cache, *v_cache;          /* layer base [kv_heads][cap][head_dim] */
+    int cap;
+    const int *pos_dev;                /* position of this step (= kv_len) */
+    int heads, kv_heads;
+    float scale;
+    float *part_o;                     /* [heads][nsplit][head_dim] */
+    float *part_m, *part_l;            /* [heads][nsplit] */
+    int nsplit;                        /* split budget (<= QK_ATTN_MAX_SPLIT) */
+    float *out;                        /* [heads*head_dim] (single split / merge) */
+} qk_attn_fused_args;
+
+int qk_attn_fused_launch(const qk_attn_fused_args *a, hipStream_t s);
+int qk_attn_merge_launch(const qk_attn_fused_args *a, hipStream_t s);
 
 /* ---- prefill (MFMA) ---------------------------------------------------- */
 /* hi/lo = bf16 split of rms_norm(x)*w (w NULL: of x itself): hi = bf16(v),

@@ -118,6 +118,39 @@ def test_tiny_against_oracle_free_run(P, qa, tiny):
             break
 
 
+def test_tiny_long_context_crosses_step_variants(P, qa, tiny):
+    """Decode attention switches from <= 8 splits merged in the O-projection
+    (<= 2048 keys) to up to 32 splits + a merge kernel: logits on both sides
+    of the switch and a free run across it must match the oracle."""
+    rows, _ = P.prompt_rows(tiny, 2036, 6, seed=21)
+    o = P.Oracle(tiny)
+    d = make_decoder(qa, P, tiny, kv_capacity=4096)
+    d.set_keep_logits(True)
+    o.prefill(rows[:-1])
+    d.prefill(rows[:-1])
+    teach = P.synth_tokens(24, 21, P.synth_tokens_id(3), tiny.cfg.vocab)
+    inp = [None] + list(teach)
+    for i, t in enumerate(inp):          # keys 2042 .. 2065: both variants
+        if t is None:
+            td, (to, lo, _) = d.forward(rows[-1]), o.forward(rows[-1], True)
+        else:
+            td, (to, lo, _) = d.forward_token(int(t)), o.forward(o.embed(int(t)), True)
+        lg = d.read_logits()
+        assert np.abs(lg - lo).max() < 1e-3, (i, d.kv_len(), float(np.abs(lg - lo).max()))
+        assert td == to or np.sort(lo)[-1] - np.sort(lo)[-2] < TIE
+    # free run across the boundary from a rollback point below it
+    d.set_kv_len(2040)
+    o.set_kv_len(2040)
+    gen = d.generate(int(teach[0]), 20)
+    t = int(teach[0])
+    for i in range(20):
+        t, lo, _ = o.forward(o.embed(t), True)
+        if gen[i] != t:
+            s = np.sort(lo)
+            assert s[-1] - s[-2] < TIE, f"step {i}"
+            break
+
+
 def test_error_conventions(qa, gpu):
     c = qa.preset(0)
     d = qa.Decoder(c, 0, 64)
