@@ -296,6 +296,8 @@ qwen_hip_decoder *qwen_hip_decoder_create(const qwen_hip_config *cfg, int device
     {
         int init[CTL_INTS] = {0};
         if (hipMemset(d->hidden, 0, D * 4) != hipSuccess ||
+            hipMemset(d->part_o, 0, (size_t)cfg->heads * QK_ATTN_MAX_SPLIT * cfg->head_dim * 4) != hipSuccess ||
+            hipMemset(d->part_l, 0, (size_t)cfg->heads * QK_ATTN_MAX_SPLIT * 4) != hipSuccess ||
             hipMemcpy(d->ctl, init, sizeof init, hipMemcpyHostToDevice) != hipSuccess) {
             qk_set_err("control block init failed");
             goto fail;
@@ -503,9 +505,9 @@ int qwen_hip_decoder_prefill_device(qwen_hip_decoder *d, const float *d_rows, in
 /* ------------------------------------------------------------------------ */
 static int enqueue_step(qwen_hip_decoder *d, int variant) {
     const qwen_hip_config *c = &d->cfg;
-    const int D = c->hidden, I = c->intermediate;
+    const int D = c->hidden, I = c->intermediate, L = c->layers;
     hipStream_t s = d->stream;
-    for (int l = 0; l < c->layers; l++) {
+    for (int l = 0; l < L; l++) {
         /* input RMSNorm + Q|K|V; layer 0 also gathers the token embedding */
         qk_gemv_args g = {.W = d->w_qkv[l], .rows = d->qkv_rows, .K = D, .x = d->x, .norm_w = d->n_in[l],
                           .eps = c->rms_eps, .y = d->qkv, .epi = QK_EPI_STORE};
@@ -524,7 +526,7 @@ static int enqueue_step(qwen_hip_decoder *d, int variant) {
             aa.nsplit = QK_MERGE_MAX_SPLIT;
             QK_TRY(qk_attn_fused_launch(&aa, s));
             go.merge_o = d->part_o; go.merge_m = d->part_m; go.merge_l = d->part_l;
-            go.merge_pos = d->d_pos; go.merge_nsplit = QK_MERGE_MAX_SPLIT;
+            go.merge_nsplit = QK_MERGE_MAX_SPLIT;
         } else {
             aa.nsplit = QK_ATTN_MAX_SPLIT;
             aa.out = d->attn_out;

@@ -47,25 +47,71 @@ __device__ __forceinline__ uint4 ld_stream16(const uint16_t *p) {
     return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, QK_WAVE);
-    return v;
+// ---------------------------------------------------------------------------
+// Cross-lane exchange without the LDS crossbar.  DPP moves operate inside a
+// row of 16 lanes at VALU latency; gfx950's v_permlane16_swap /
+// v_permlane32_swap exchange rows.  dpp<CTRL>(v): lane i reads lane f(i):
+//   0xB1 quad_perm [1,0,3,2] (xor 1)      0x4E quad_perm [2,3,0,1] (xor 2)
+//   0x104 row_shl:4 (i+4)   0x114 row_shr:4 (i-4)   0x128 row_ror:8 (xor 8)
+//   0x124 row_ror:4
+// ---------------------------------------------------------------------------
+template <int CTRL, int BANKS = 0xF>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, 0xF, BANKS, false));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, QK_WAVE));
-    return v;
+// value of lane (i ^ M) for M in {1, 2, 4, 8}
+template <int M>
+__device__ __forceinline__ float xor_lane(float v) {
+    if (M == 1) return dpp_mov<0xB1>(v, v);
+    if (M == 2) return dpp_mov<0x4E>(v, v);
+    if (M == 8) return dpp_mov<0x128>(v, v);
+    // M == 4: lanes with bit 2 clear read i+4 (banks 0, 2), the others i-4 (banks 1, 3)
+    float t = dpp_mov<0x104, 0x5>(v, v);
+    return dpp_mov<0x114, 0xA>(t, v);
 }
 
-// Sum over aligned groups of G lanes (G a power of two <= 64).
+// {v from lanes [0,32) of a, lanes [0,32) of b} / {hi halves}: the two results
+// of v_permlane32_swap(a, b); likewise for odd/even rows with permlane16.
+__device__ __forceinline__ void swap32(float &a, float &b) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ void swap16(float &a, float &b) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+// Sum over each aligned group of G lanes (G a power of two <= 64); every lane
+// of the group receives the group's sum.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, QK_WAVE);
+    if (G >= 2) v += xor_lane<1>(v);
+    if (G >= 4) v += xor_lane<2>(v);
+    if (G >= 8) v += xor_lane<4>(v);
+    if (G >= 16) v += xor_lane<8>(v);
+    if (G >= 32) { float a = v, b = v; swap16(a, b); v = a + b; }
+    if (G >= 64) { float a = v, b = v; swap32(a, b); v = a + b; }
     return v;
 }
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    if (G >= 2) v = fmaxf(v, xor_lane<1>(v));
+    if (G >= 4) v = fmaxf(v, xor_lane<2>(v));
+    if (G >= 8) v = fmaxf(v, xor_lane<4>(v));
+    if (G >= 16) v = fmaxf(v, xor_lane<8>(v));
+    if (G >= 32) { float a = v, b = v; swap16(a, b); v = fmaxf(a, b); }
+    if (G >= 64) { float a = v, b = v; swap32(a, b); v = fmaxf(a, b); }
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
 // Argmax order: larger value wins, lower index wins an exact tie.  This is
 // the reference's strict '>' over increasing row index (qwen_asr_kernels_avx.c
@@ -79,3 +125,4 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) 
 __device__ __forceinline__ float swiglu1(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
+

@@ -30,15 +30,26 @@
 // halves the values a lane carries, so the whole reduction costs
 // log2(ROWS) + 6 - log2(ROWS) + (ROWS - 1) shuffles instead of 6 * ROWS.
 // ---------------------------------------------------------------------------
-template <int N>
-__device__ __forceinline__ void transpose_step(float (&v)[N], int n, int m, int lane) {
-    const bool up = (lane & m) != 0;
+// One halving step of the transposing reduction over lane bit M: a lane with
+// bit M clear keeps values [0, n/2) and gains its partner's copies of them; a
+// lane with bit M set keeps [n/2, n).  For M = 32 / 16 one permlane swap of
+// (v[i], v[i + n/2]) delivers both halves at once: the sum of the two swap
+// results is exactly "own kept value + partner's value of the same row".
+template <int N, int M>
+__device__ __forceinline__ void transpose_step(float (&v)[N], int n, int lane) {
 #pragma unroll
     for (int i = 0; i < N / 2; i++) {
         if (i < n / 2) {
-            float keep = up ? v[i + n / 2] : v[i];
-            float send = up ? v[i] : v[i + n / 2];
-            v[i] = keep + __shfl_xor(send, m, QK_WAVE);
+            if (M == 32 || M == 16) {
+                float a = v[i], b = v[i + n / 2];
+                if (M == 32) swap32(a, b); else swap16(a, b);
+                v[i] = a + b;
+            } else {
+                const bool up = (lane & M) != 0;
+                const float keep = up ? v[i + n / 2] : v[i];
+                const float send = up ? v[i] : v[i + n / 2];
+                v[i] = keep + xor_lane<M>(send);
+            }
         }
     }
 }
@@ -48,14 +59,14 @@ __device__ __forceinline__ void transpose_step(float (&v)[N], int n, int m, int 
 // totals of rows [KEEP*(lane / (64*KEEP/ROWS)), +KEEP).
 template <int ROWS, int KEEP>
 __device__ __forceinline__ void reduce_rows(float (&v)[ROWS], int lane) {
-    int n = ROWS, m = 32;
+    constexpr int T = ROWS / KEEP > 1 ? ROWS / KEEP : 1;   // 2^(number of transposing steps)
+    if (T >= 2) transpose_step<ROWS, 32>(v, ROWS, lane);
+    if (T >= 4) transpose_step<ROWS, 16>(v, ROWS / 2, lane);
+    if (T >= 8) transpose_step<ROWS, 8>(v, ROWS / 4, lane);
+    // all-reduce what remains over the lanes below the last transposed bit
+    constexpr int G = 64 / T;
 #pragma unroll
-    for (; n > KEEP; n >>= 1, m >>= 1) transpose_step<ROWS>(v, n, m, lane);
-#pragma unroll
-    for (; m >= 1; m >>= 1) {
-#pragma unroll
-        for (int i = 0; i < KEEP; i++) v[i] += __shfl_xor(v[i], m, QK_WAVE);
-    }
+    for (int i = 0; i < KEEP; i++) v[i] = group_sum<G>(v[i]);
 }
 
 template <int NC, int ROWS>
@@ -94,10 +105,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
         // The input is the attention output, merged here from its position
         // splits (m, l, o): x = (sum_s o_s e^(m_s - M)) * (1 / sum_s l_s e^(m_s - M)).
         // Thread t merges columns [8t, 8t + 8) into LDS for the whole block.
+        // Every one of the merge_nsplit slots is valid: splits past the live
+        // count were written with m = -inf by the attention kernel, so they
+        // weigh 0 and no position read is needed here.
         __shared__ __attribute__((aligned(16))) float xs[QK_MERGE_MAX_K];
-        const int seq_k = *a.merge_pos + 1;
-        const int ck = qk_attn_chunk(seq_k, a.merge_nsplit);
-        const int ns = (seq_k + ck - 1) / ck;
+        const int ns = a.merge_nsplit;
         for (int t = threadIdx.x; t * 8 < K; t += 256) {
             const int col = t * 8, h = col >> 7, d = col & 127;
             const float *pm = a.merge_m + (size_t)h * a.merge_nsplit;
@@ -198,6 +210,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
     // ---- rows ----
     float best_v = -1e30f;
     int best_i = 0x7fffffff;
+    // residual add: the old value of the row this lane will own after the
+    // reduction, loaded now so its latency overlaps the weight stream
+    float resid = 0.0f;
+    if constexpr (EPI == QK_EPI_ADD) {
+        const int r = rbase + lane / (64 / ROWS);
+        if (iters == 1 && r < R) resid = a.y[r];
+    }
     for (int it = 0; it < iters; it++) {
         if (rbase >= R) break;
         const int rnext = rbase + 4 * ROWS;
@@ -213,7 +232,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
             for (int c = 0; c < NC; c++) acc[j] = dot8_bf16(w[j][c], xr[c], acc[j]);
         }
 
-        if (EPI == QK_EPI_SWIGLU) {
+        if constexpr (EPI == QK_EPI_SWIGLU) {
             reduce_rows<ROWS, 2>(acc, lane);
             const int span = 128 / ROWS;                 // lanes per (g,u) pair
             const int r = rbase + 2 * (lane / span);
@@ -224,8 +243,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
             const int span = 64 / ROWS;
             const int r = rbase + lane / span;
             if ((lane % span) == 0 && r < R) {
-                if (EPI == QK_EPI_STORE) a.y[r] = acc[0];
-                else if (EPI == QK_EPI_ADD) a.y[r] += acc[0];
+                if constexpr (EPI == QK_EPI_STORE) a.y[r] = acc[0];
+                else if constexpr (EPI == QK_EPI_ADD) a.y[r] = (iters == 1 ? resid : a.y[r]) + acc[0];
                 else {
                     if (a.logits) a.logits[r] = acc[0];
                     if (argmax_better(acc[0], r, best_v, best_i)) { best_v = acc[0]; best_i = r; }
@@ -241,7 +260,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
         rbase = rnext;
     }
 
-    if (EPI == QK_EPI_ARGMAX) {
+    if constexpr (EPI == QK_EPI_ARGMAX) {
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) {
             float ov = __shfl_xor(best_v, m, QK_WAVE);
@@ -307,7 +326,7 @@ extern "C" int qk_gemv_launch(const qk_gemv_args *a, hipStream_t s) {
     if (a->epi == QK_EPI_ARGMAX && (!a->cand_val || !a->cand_idx)) return QWEN_HIP_EINVAL;
     if (a->epi != QK_EPI_ARGMAX && !a->y) return QWEN_HIP_EINVAL;
     if (!a->x && !a->tok && !a->merge_o) return QWEN_HIP_EINVAL;
-    if (a->merge_o && (!a->merge_m || !a->merge_l || !a->merge_pos || a->merge_nsplit <= 0 ||
+    if (a->merge_o && (!a->merge_m || !a->merge_l || a->merge_nsplit <= 0 ||
                        a->merge_nsplit > QK_MERGE_MAX_SPLIT || a->K > QK_MERGE_MAX_K || (a->K & 127) || a->tok))
         return QWEN_HIP_EINVAL;
     if (a->tok && !a->emb) return QWEN_HIP_EINVAL;
@@ -721,7 +740,11 @@ __global__ __launch_bounds__(256) void attn_decode_fused(qk_attn_fused_args a) {
     const int pos = *a.pos_dev, seq_k = pos + 1;
     const int chunk = qk_attn_chunk(seq_k, a.nsplit);
     const int nsplit = (seq_k + chunk - 1) / chunk;
-    if (split >= nsplit) return;
+    if (split >= nsplit) {
+        // an idle split marks its partial slot empty (m = -inf weighs 0 in the merge)
+        if (threadIdx.x < HPK) a.part_m[(size_t)(kvh * HPK + threadIdx.x) * a.nsplit + split] = -INFINITY;
+        return;
+    }
     const int s0 = split * chunk, s1 = min(s0 + chunk, seq_k);
     const bool last_split = (s1 == seq_k);
     const int cached_end = last_split ? pos : s1;        // position pos itself comes from LDS

@@ -33,9 +33,9 @@ typedef struct {
     int *cand_idx;
     int epi;
     /* merge prologue: the input row is the attention output merged from
-     * split partials (K = heads*128); replaces x */
+     * merge_nsplit split partials (K = heads*128), unused slots holding
+     * m = -inf; replaces x */
     const float *merge_o, *merge_m, *merge_l;
-    const int *merge_pos;     /* seq_k = *merge_pos + 1 */
     int merge_nsplit;         /* split budget the partials were written with */
 } qk_gemv_args;
 
