@@ -116,7 +116,8 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c1")
-    ap.add_argument("--engine", type=int, default=None, help="0 graph of fused kernels, 1 eager")
+    ap.add_argument("--engine", type=int, default=None,
+                    help="0 graph of fused kernels, 1 eager, 2 persistent kernel (default where supported)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc child runs")
     ap.add_argument("--cpu-steps", type=int, default=48)
@@ -209,7 +210,8 @@ def main():
         "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
         "config": {"workload": wl["desc"], "batch": 1, "weights": "bf16 N(0,0.02) seed 0, norms 1.0",
                    "activations": "fp32, fp32 accumulation", "kv_cache": "fp32",
-                   "prefill_rows": n_rows - 1, "decode_positions": [base, base + K - 1]},
+                   "prefill_rows": n_rows - 1, "decode_positions": [base, base + K - 1],
+                   "engine": {0: "graph", 1: "eager", 2: "persistent"}.get(d.engine(), d.engine())},
         "prefill_tok_s": round((n_rows - 1) / prefill_s, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,

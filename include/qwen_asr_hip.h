@@ -151,9 +151,16 @@ int qwen_hip_decoder_set_keep_logits(qwen_hip_decoder *dec, int on);
 int qwen_hip_decoder_read_hidden(qwen_hip_decoder *dec, float *out);
 int qwen_hip_decoder_read_logits(qwen_hip_decoder *dec, float *out);
 
-/* Decode-step engine: 0 = one kernel per fused op, replayed from a HIP graph
- * (default); 1 = same kernels launched eagerly (no graph). */
+/* Decode engine: 0 = one kernel per fused op, replayed from a HIP graph;
+ * 1 = the same kernels launched eagerly (no graph); 2 = the whole greedy loop
+ * of a forward/generate call in one persistent cooperative kernel (default
+ * where supported: 16 query / 8 kv heads, the 0.6B or 1.7B shape, 256 CUs in
+ * 8 XCDs).  set_engine(2) returns QWEN_HIP_EINVAL where it is not supported.
+ * If a persistent run fails it reports on stderr, switches the decoder to
+ * engine 0 and redoes the steps there.  No reference counterpart: the
+ * reference has one CPU path (qwen_asr_kernels.c). */
 int qwen_hip_decoder_set_engine(qwen_hip_decoder *dec, int engine);
+int qwen_hip_decoder_engine(const qwen_hip_decoder *dec);
 
 /* The stream the decoder launches on (for event timing by callers). */
 hipStream_t qwen_hip_decoder_stream(const qwen_hip_decoder *dec);

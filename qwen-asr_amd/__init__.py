@@ -63,6 +63,7 @@ SIGNATURES = [
     ("qwen_hip_decoder_read_hidden", _i, [_vp, _vp]),
     ("qwen_hip_decoder_read_logits", _i, [_vp, _vp]),
     ("qwen_hip_decoder_set_engine", _i, [_vp, _i]),
+    ("qwen_hip_decoder_engine", _i, [_vp]),
     ("qwen_hip_decoder_stream", _vp, [_vp]),
     ("qwen_hip_decoder_step_bytes", _d, [_vp, _i]),
     ("qwen_hip_last_error", C.c_char_p, []),
@@ -231,6 +232,10 @@ class Decoder:
 
     def set_engine(self, engine):
         check(lib().qwen_hip_decoder_set_engine(self.h, int(engine)), "set_engine")
+
+    def engine(self):
+        """Active decode engine: 0 graph, 1 eager, 2 persistent."""
+        return lib().qwen_hip_decoder_engine(self.h)
 
     def read_hidden(self):
         out = np.empty(self.cfg.hidden, np.float32)

@@ -57,6 +57,10 @@ void qwen_hip_config_preset(qwen_hip_config *c, int model_b) {
 #define QK_SHORT_MAX 2048
 enum { STEP_SHORT = 0, STEP_LONG = 1, STEP_VARIANTS = 2 };
 
+/* Decode engines: one kernel per fused op replayed from a HIP graph, the same
+ * kernels launched eagerly, or the whole greedy loop in one persistent kernel. */
+enum { ENGINE_GRAPH = 0, ENGINE_EAGER = 1, ENGINE_PERSIST = 2 };
+
 /* Control block (one device allocation): the input token of the next step,
  * its position (= kv_len) and the generate log cursor. */
 enum { CTL_TOK = 0, CTL_POS = 1, CTL_COUNTER = 2, CTL_INTS = 64 };
@@ -101,6 +105,14 @@ struct qwen_hip_decoder {
     hipGraph_t graph[STEP_VARIANTS];
     hipGraphExec_t gexec[STEP_VARIANTS];
     int engine, keep_logits;
+
+    /* persistent engine: exchange words (one allocation), tickets + error word */
+    int px_ok;
+    unsigned long long *px_buf;
+    size_t px_words;
+    unsigned long long *xq, *xa, *xo, *xla, *xh, *xd, *xlb, *xc, *xv;
+    unsigned *px_ctl;         /* [0, 16) per-XCD tickets, [16] error bits */
+    unsigned px_epoch;
 };
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -230,6 +242,31 @@ static int check_cfg(const qwen_hip_config *c) {
     return 1;
 }
 
+/* Exchange words of the persistent engine, zero-initialised (tag 0 is never
+ * expected: epochs start at 1). */
+static int px_alloc(qwen_hip_decoder *d) {
+    const size_t H = d->cfg.hidden, I = d->cfg.intermediate, P = 2 * QK_PX_XCD;
+    const size_t n_q = P * 512, n_a = P * QK_PX_MAX_SPLIT * QK_PX_PART, n_h = P * H, n_i = P * (I / QK_PX_XCD);
+    const size_t n_c = 2 * QK_PX_BLOCKS, n_v = QK_PX_BLOCKS;
+    d->px_words = n_q + n_a + 4 * n_h + n_i + n_c + n_v;
+    QK_TRY(dev_alloc((void **)&d->px_buf, d->px_words * 8));
+    QK_TRY(dev_alloc((void **)&d->px_ctl, 64 * sizeof(unsigned)));
+    unsigned long long *p = d->px_buf;
+    d->xq = p;  p += n_q;
+    d->xa = p;  p += n_a;
+    d->xo = p;  p += n_h;
+    d->xla = p; p += n_h;
+    d->xd = p;  p += n_h;
+    d->xlb = p; p += n_h;
+    d->xh = p;  p += n_i;
+    d->xc = p;  p += n_c;
+    d->xv = p;
+    QK_HIP(hipMemset(d->px_buf, 0, d->px_words * 8));
+    QK_HIP(hipMemset(d->px_ctl, 0, 64 * sizeof(unsigned)));
+    d->px_epoch = 1;
+    return 0;
+}
+
 qwen_hip_decoder *qwen_hip_decoder_create(const qwen_hip_config *cfg, int device, int kv_capacity) {
     if (!check_cfg(cfg)) {
         qk_set_err("unsupported decoder configuration (head_dim must be 128; hidden, "
@@ -304,6 +341,12 @@ qwen_hip_decoder *qwen_hip_decoder_create(const qwen_hip_config *cfg, int device
         }
     }
     if (kv_reserve(d, kv_capacity > 0 ? kv_capacity : 1024)) goto fail;
+    d->engine = ENGINE_GRAPH;
+    if (qk_persist_supported(cfg->hidden, cfg->intermediate, cfg->heads, cfg->kv_heads, device)) {
+        if (px_alloc(d)) goto fail;
+        d->px_ok = 1;
+        d->engine = ENGINE_PERSIST;
+    }
     return d;
 fail:
     qwen_hip_decoder_destroy(d);
@@ -329,6 +372,7 @@ void qwen_hip_decoder_destroy(qwen_hip_decoder *d) {
     dev_free(d->x); dev_free(d->qkv); dev_free(d->part_o); dev_free(d->part_m); dev_free(d->part_l);
     dev_free(d->attn_out); dev_free(d->h); dev_free(d->hidden); dev_free(d->logits);
     dev_free(d->cand_val); dev_free(d->cand_idx); dev_free(d->ctl); dev_free(d->d_log);
+    dev_free(d->px_buf); dev_free(d->px_ctl);
     prefill_free(d);
     if (d->h_row) (void)hipHostFree(d->h_row);
     if (d->h_int) (void)hipHostFree(d->h_int);
@@ -569,7 +613,7 @@ static int graph_ensure(qwen_hip_decoder *d, int v) {
 static int launch_steps(qwen_hip_decoder *d, int n) {
     for (int i = 0; i < n; i++) {
         const int v = (d->kv_len + i + 1 <= QK_SHORT_MAX) ? STEP_SHORT : STEP_LONG;
-        if (d->engine == 0) {
+        if (d->engine == ENGINE_GRAPH) {
             QK_TRY(graph_ensure(d, v));
             QK_HIP(hipGraphLaunch(d->gexec[v], d->stream));
         } else {
@@ -592,15 +636,61 @@ static int log_reserve(qwen_hip_decoder *d, int n) {
     return 0;
 }
 
-/* one forward whose input is already staged (x or d_tok set by the caller) */
-static int forward_staged(qwen_hip_decoder *d) {
-    d->h_int[2] = 0;
-    QK_HIP(hipMemcpyAsync(d->d_counter, &d->h_int[2], sizeof(int), hipMemcpyHostToDevice, d->stream));
-    QK_TRY(launch_steps(d, 1));
-    QK_HIP(hipMemcpyAsync(&d->h_int[8], d->ctl, 4 * sizeof(int), hipMemcpyDeviceToHost, d->stream));
+/* The persistent engine: n steps from position kv_len in one cooperative
+ * launch; the first input is emb[first_tok] or, for first_tok < 0, the row
+ * staged in d->x.  Synchronises and checks the kernel's error bits. */
+static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
+    const qwen_hip_config *c = &d->cfg;
+    const unsigned need = QK_PX_TAGS(c->layers, n);
+    if (d->px_epoch > 0xFFFFFF00u - need) {       /* tag space exhausted: start over on zeroed words */
+        QK_HIP(hipMemsetAsync(d->px_buf, 0, d->px_words * 8, d->stream));
+        d->px_epoch = 1;
+    }
+    QK_HIP(hipMemsetAsync(d->px_ctl, 0, 64 * sizeof(unsigned), d->stream));
+    const char *l0 = (const char *)d->w_qkv[0];
+    qk_persist_args a = {
+        .layer0 = l0, .layer_stride = c->layers > 1 ? (long)((const char *)d->w_qkv[1] - l0) : 0,
+        .off_qkv = 0, .off_o = (const char *)d->w_o[0] - l0, .off_gu = (const char *)d->w_gu[0] - l0,
+        .off_down = (const char *)d->w_down[0] - l0, .off_nin = (const char *)d->n_in[0] - l0,
+        .off_npost = (const char *)d->n_post[0] - l0, .off_nq = (const char *)d->n_q[0] - l0,
+        .off_nk = (const char *)d->n_k[0] - l0, .emb = d->emb, .fnorm = d->fnorm, .k_cache = d->kc,
+        .v_cache = d->vc, .cap = d->kv_cap, .rope_cos = d->rope_cos, .rope_sin = d->rope_sin,
+        .layers = c->layers, .vocab = c->vocab, .eps = c->rms_eps, .scale = d->scale,
+        .xq = d->xq, .xa = d->xa, .xo = d->xo, .xla = d->xla, .xh = d->xh, .xd = d->xd, .xlb = d->xlb,
+        .xc = d->xc, .xv = d->xv, .cnt = d->px_ctl, .err = d->px_ctl + 16, .epoch = d->px_epoch,
+        .pos0 = d->kv_len, .n_steps = n, .first_tok = first_tok, .x_in = d->x, .log = d->d_log,
+        .tok_out = d->d_tok, .pos_out = d->d_pos, .hidden_out = d->hidden,
+        .logits = d->keep_logits ? d->logits : NULL};
+    QK_TRY(qk_persist_launch(&a, c->hidden, c->intermediate, d->stream));
+    d->px_epoch += need;
+    QK_HIP(hipMemcpyAsync(&d->h_int[16], d->px_ctl + 16, sizeof(int), hipMemcpyDeviceToHost, d->stream));
     QK_HIP(hipStreamSynchronize(d->stream));
-    d->kv_len += 1;
-    return d->h_int[8 + CTL_TOK];
+    if (d->h_int[16]) {
+        qk_set_err("persistent decode raised error bits 0x%x (%s)", (unsigned)d->h_int[16],
+                   (d->h_int[16] & QK_PX_ERR_LAYOUT) ? "blocks not spread 32 per XCD" : "hand-over timed out");
+        return QWEN_HIP_EDEVICE;
+    }
+    return 0;
+}
+
+/* Run n steps from position kv_len; first_tok as for px_run.  Tokens land in
+ * d_log[0, n), the last one also in the control block.  Does not advance
+ * kv_len.  If the persistent engine fails it is switched off for this decoder
+ * and the steps are redone by the graph engine (they rewrite the same K/V
+ * positions, so a partial run leaves nothing behind). */
+static int steps_run(qwen_hip_decoder *d, int first_tok, int n) {
+    if (d->engine == ENGINE_PERSIST) {
+        if (px_run(d, first_tok, n) == 0) return 0;
+        fprintf(stderr, "qwen_asr_hip: %s; using the graph engine\n", qwen_hip_last_error());
+        d->px_ok = 0;
+        d->engine = ENGINE_GRAPH;
+        QK_TRY(set_dev_pos(d));       /* the failed run may have advanced it */
+    }
+    d->h_int[0] = first_tok;
+    d->h_int[2] = 0;
+    QK_HIP(hipMemcpyAsync(d->d_tok, &d->h_int[0], sizeof(int), hipMemcpyHostToDevice, d->stream));
+    QK_HIP(hipMemcpyAsync(d->d_counter, &d->h_int[2], sizeof(int), hipMemcpyHostToDevice, d->stream));
+    return launch_steps(d, n);
 }
 
 static int forward_prepare(qwen_hip_decoder *d, int steps) {
@@ -611,28 +701,33 @@ static int forward_prepare(qwen_hip_decoder *d, int steps) {
     return 0;
 }
 
+/* one forward from the staged input (first_tok or the row in d->x) */
+static int forward_one(qwen_hip_decoder *d, int first_tok) {
+    if (steps_run(d, first_tok, 1)) return -1;
+    if (hipMemcpyAsync(&d->h_int[8], d->ctl, 4 * sizeof(int), hipMemcpyDeviceToHost, d->stream) != hipSuccess ||
+        hipStreamSynchronize(d->stream) != hipSuccess) {
+        qk_set_err("forward: reading the token back failed");
+        return -1;
+    }
+    d->kv_len += 1;
+    return d->h_int[8 + CTL_TOK];
+}
+
 int qwen_hip_decoder_forward(qwen_hip_decoder *d, const float *row) {
     if (!row || forward_prepare(d, 1)) return QWEN_HIP_TOKEN_IM_END;
     memcpy(d->h_row, row, (size_t)d->cfg.hidden * 4);
-    d->h_int[0] = -1;
-    if (hipMemcpyAsync(d->x, d->h_row, (size_t)d->cfg.hidden * 4, hipMemcpyHostToDevice, d->stream) != hipSuccess ||
-        hipMemcpyAsync(d->d_tok, &d->h_int[0], sizeof(int), hipMemcpyHostToDevice, d->stream) != hipSuccess) {
+    if (hipMemcpyAsync(d->x, d->h_row, (size_t)d->cfg.hidden * 4, hipMemcpyHostToDevice, d->stream) != hipSuccess) {
         qk_set_err("forward: staging copy failed");
         return QWEN_HIP_TOKEN_IM_END;
     }
-    int t = forward_staged(d);
+    int t = forward_one(d, -1);
     return t < 0 ? QWEN_HIP_TOKEN_IM_END : t;
 }
 
 int qwen_hip_decoder_forward_token(qwen_hip_decoder *d, int token) {
     if (!d || token < 0 || token >= d->cfg.vocab) { qk_set_err("forward_token: bad token"); return QWEN_HIP_TOKEN_IM_END; }
     if (forward_prepare(d, 1)) return QWEN_HIP_TOKEN_IM_END;
-    d->h_int[0] = token;
-    if (hipMemcpyAsync(d->d_tok, &d->h_int[0], sizeof(int), hipMemcpyHostToDevice, d->stream) != hipSuccess) {
-        qk_set_err("forward_token: staging copy failed");
-        return QWEN_HIP_TOKEN_IM_END;
-    }
-    int t = forward_staged(d);
+    int t = forward_one(d, token);
     return t < 0 ? QWEN_HIP_TOKEN_IM_END : t;
 }
 
@@ -644,11 +739,7 @@ int qwen_hip_decoder_generate(qwen_hip_decoder *d, int first, int n, int *out, i
     if (n == 0) return 0;
     QK_TRY(forward_prepare(d, n));
     const int start = d->kv_len;
-    d->h_int[0] = first;
-    d->h_int[2] = 0;
-    QK_HIP(hipMemcpyAsync(d->d_tok, &d->h_int[0], sizeof(int), hipMemcpyHostToDevice, d->stream));
-    QK_HIP(hipMemcpyAsync(d->d_counter, &d->h_int[2], sizeof(int), hipMemcpyHostToDevice, d->stream));
-    QK_TRY(launch_steps(d, n));
+    QK_TRY(steps_run(d, first, n));
     QK_HIP(hipMemcpyAsync(out, d->d_log, (size_t)n * 4, hipMemcpyDeviceToHost, d->stream));
     QK_HIP(hipStreamSynchronize(d->stream));
     int kept = n;
@@ -677,10 +768,16 @@ int qwen_hip_decoder_set_keep_logits(qwen_hip_decoder *d, int on) {
 }
 
 int qwen_hip_decoder_set_engine(qwen_hip_decoder *d, int engine) {
-    if (!d || engine < 0 || engine > 1) return QWEN_HIP_EINVAL;
+    if (!d || engine < ENGINE_GRAPH || engine > ENGINE_PERSIST) { qk_set_err("set_engine: unknown engine"); return QWEN_HIP_EINVAL; }
+    if (engine == ENGINE_PERSIST && !d->px_ok) {
+        qk_set_err("set_engine: the persistent engine needs 16 query / 8 kv heads, the 0.6B or 1.7B shape and 256 CUs");
+        return QWEN_HIP_EINVAL;
+    }
     d->engine = engine;
     return 0;
 }
+
+int qwen_hip_decoder_engine(const qwen_hip_decoder *d) { return d ? d->engine : QWEN_HIP_EINVAL; }
 
 int qwen_hip_decoder_read_hidden(qwen_hip_decoder *d, float *out) {
     if (!d || !out) return QWEN_HIP_EINVAL;

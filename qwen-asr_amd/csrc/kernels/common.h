@@ -126,3 +126,57 @@ __device__ __forceinline__ float swiglu1(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
+
+// ---------------------------------------------------------------------------
+// Row reductions for GEMV tiles.  A wave owning ROWS rows holds one partial
+// sum per row in every lane; these fold them across the 64 lanes.
+// ---------------------------------------------------------------------------
+// One halving step of the transposing reduction over lane bit M: a lane with
+// bit M clear keeps values [0, n/2) and gains its partner's copies of them; a
+// lane with bit M set keeps [n/2, n).  For M = 32 / 16 one permlane swap of
+// (v[i], v[i + n/2]) delivers both halves at once: the sum of the two swap
+// results is exactly "own kept value + partner's value of the same row".
+template <int N, int M>
+__device__ __forceinline__ void transpose_step(float (&v)[N], int n, int lane) {
+#pragma unroll
+    for (int i = 0; i < N / 2; i++) {
+        if (i < n / 2) {
+            if (M == 32 || M == 16) {
+                float a = v[i], b = v[i + n / 2];
+                if (M == 32) swap32(a, b); else swap16(a, b);
+                v[i] = a + b;
+            } else {
+                const bool up = (lane & M) != 0;
+                const float keep = up ? v[i + n / 2] : v[i];
+                const float send = up ? v[i] : v[i + n / 2];
+                v[i] = keep + xor_lane<M>(send);
+            }
+        }
+    }
+}
+
+// Reduce ROWS per-lane partials to KEEP values per lane (KEEP = 1 or 2).
+// Afterwards every lane of the aligned group of 64*KEEP/ROWS lanes holds the
+// totals of rows [KEEP*(lane / (64*KEEP/ROWS)), +KEEP).
+template <int ROWS, int KEEP>
+__device__ __forceinline__ void reduce_rows(float (&v)[ROWS], int lane) {
+    constexpr int T = ROWS / KEEP > 1 ? ROWS / KEEP : 1;   // 2^(number of transposing steps)
+    if (T >= 2) transpose_step<ROWS, 32>(v, ROWS, lane);
+    if (T >= 4) transpose_step<ROWS, 16>(v, ROWS / 2, lane);
+    if (T >= 8) transpose_step<ROWS, 8>(v, ROWS / 4, lane);
+    // all-reduce what remains over the lanes below the last transposed bit
+    constexpr int G = 64 / T;
+#pragma unroll
+    for (int i = 0; i < KEEP; i++) v[i] = group_sum<G>(v[i]);
+}
+
+// one lane pair (l, l+64) of a 128-wide head: RMSNorm with weight, then RoPE
+__device__ __forceinline__ void norm_rope_pair(float &x1, float &x2, const float *nw, float eps, float c, float sn,
+                                               int lane) {
+    float ss = wave_sum(fmaf(x1, x1, x2 * x2));
+    const float rinv = 1.0f / sqrtf(ss / 128.0f + eps);
+    const float a = (x1 * nw[lane]) * rinv, b = (x2 * nw[lane + 64]) * rinv;
+    x1 = fmaf(a, c, -(b * sn));
+    x2 = fmaf(b, c, a * sn);
+}
+

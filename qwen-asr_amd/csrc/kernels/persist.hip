@@ -1,0 +1,899 @@
+// persist.hip - the greedy decode loop of the Qwen3 decoder as ONE persistent
+// kernel on gfx950: qwen_decoder_forward (reference qwen_asr_decoder.c:388-476)
+// repeated by the token loop (qwen_asr.c:729-759), n steps per launch.
+//
+// Why one kernel: a 0.6B decode step streams 1.2 GB of weights but is a chain
+// of ~140 dependent all-to-all hand-overs (5 per layer).  As separate kernels
+// each hand-over costs a launch plus a cold start of the next kernel; here the
+// blocks stay resident, hand activations over through memory, and issue the
+// next stage's weight loads before they wait, so HBM latency hides behind the
+// hand-over.
+//
+// Work layout (MI355X: 8 XCDs x 32 CUs, one block per CU).  XCD g owns kv head
+// g with its query heads 2g, 2g+1, 1/8 of the MLP intermediate rows, and the
+// matching split-K column slices of the O and down projections.  Per layer
+// only the two split-K partial sums (8 x hidden floats) cross XCDs; the other
+// five hand-overs stay inside one XCD and go through its L2.
+//
+//   Q  rms_norm(x) . Wqkv rows of the group (16 rows per block)      -> local
+//   A  q/k norm + RoPE + K/V append + attention over a position split -> local
+//   O  merge splits, W_o[:, group cols] (H/32 rows per block)         -> cross
+//   F  x += sum of O partials; rms_norm; gate|up rows + SwiGLU         -> local
+//   D  W_down[:, group cols] (H/32 rows per block)                    -> cross
+//   (next layer's Q adds the down partials to x), LM head + argmax    -> cross
+//
+// Exchange words are 64-bit: (tag << 32) | fp32 bits.  A reader polls the
+// words it needs until each carries the expected tag, so every word is its
+// own ready flag and no fence is needed.  XCD-local words are written with
+// plain stores (they land in the XCD's shared L2) and read with agent-scope
+// loads (sc1: they skip the CU-private L1).  Cross-XCD words use agent-scope
+// stores (written through to the memory side) and agent-scope loads.  Tags
+// are unique per hand-over within a launch and across launches (the host
+// advances the epoch), so a stale word can never pass as fresh: at worst a
+// wait times out, raises an error bit and every block leaves.
+//
+// Each block runs NCW compute waves and one sync wave.  Only the sync wave
+// polls, so outstanding weight prefetches of the compute waves never hold up
+// a poll (loads retire in order per wave).  Both roles walk the same barrier
+// sequence; the block barrier does not wait on global loads.
+#include "common.h"
+#include "qk_kernels.h"
+#include "qwen_asr_hip.h"
+
+#include <math.h>
+
+typedef unsigned long long u64;
+
+#define PX_SPIN_LIMIT (1u << 22)
+#define PX_QD 2048                 // 16 query heads x 128
+#define PX_KVD 1024                // 8 kv heads x 128
+
+// ---------------------------------------------------------------------------
+// exchange words
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u64 px_word(float v, unsigned tag) { return ((u64)tag << 32) | __float_as_uint(v); }
+
+__device__ __forceinline__ void px_put_local(u64 *p, float v, unsigned tag) {
+    __hip_atomic_store(p, px_word(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+
+__device__ __forceinline__ void px_put_global(u64 *p, float v, unsigned tag) {
+    __hip_atomic_store(p, px_word(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ u64 px_get(const u64 *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool px_aborted(unsigned *err) {
+    return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+
+__device__ __forceinline__ void px_raise(unsigned *err, unsigned bits) {
+    __hip_atomic_fetch_or(err, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16-byte streaming load at a wave-uniform base plus a 32-bit per-lane byte
+// offset, so the load uses the scalar-base addressing form and a lane keeps one
+// offset register per slab instead of a 64-bit address per load.
+__device__ __forceinline__ uint4 px_ld16(const void *base, unsigned off) {
+    return ld_stream16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(base) + off));
+}
+
+__device__ __forceinline__ float4 px_ldf4(const void *base, unsigned off) {
+    return *reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(base) + off);
+}
+
+// Block barrier that leaves global loads in flight (weight prefetches cross
+// it); this wave's LDS accesses are complete before it.
+__device__ __forceinline__ void px_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Sync wave: wait until the n words at addr(i), i < n, carry `tag`, then
+// dst[i] = value.  PER words per lane in flight per pass.  False on timeout or
+// when another block raised an error.
+template <int PER, typename Addr>
+__device__ bool px_poll(Addr addr, int n, unsigned tag, float *dst, unsigned *err, int lane) {
+    for (int base = 0; base < n; base += 64 * PER) {
+        for (unsigned spin = 1;; spin++) {
+            u64 w[PER];
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int i = base + j * 64 + lane;
+                w[j] = (i < n) ? px_get(addr(i)) : ((u64)tag << 32);
+            }
+            bool ok = true;
+#pragma unroll
+            for (int j = 0; j < PER; j++) ok = ok && ((unsigned)(w[j] >> 32) == tag);
+            if (__all(ok)) {
+#pragma unroll
+                for (int j = 0; j < PER; j++) {
+                    const int i = base + j * 64 + lane;
+                    if (i < n) dst[i] = __uint_as_float((unsigned)w[j]);
+                }
+                break;
+            }
+            if (spin >= PX_SPIN_LIMIT) {
+                if (lane == 0) px_raise(err, QK_PX_ERR_TIMEOUT);
+                return false;
+            }
+            if ((spin & 127u) == 0u && px_aborted(err)) return false;
+        }
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// A slab of bf16 weight rows held in registers by the compute waves.  Lanes
+// form groups of LW; a group covers 8*LW consecutive columns per 16-byte load
+// (SEGS loads per row), a wave covers 64/LW rows per batch and BPW batches.
+// Rows [0, R) of the slab start at W with row stride ld (elements).
+// ---------------------------------------------------------------------------
+template <int LW, int SEGS, int BPW>
+struct PxSlab {
+    static constexpr int RPI = 64 / LW;
+    uint4 w[BPW][SEGS];
+
+    // wave must be wave-uniform (an SGPR): every per-batch offset then folds
+    // into the scalar base and a lane needs one 32-bit offset for all loads.
+    __device__ __forceinline__ void load(const uint16_t *W, int ld, int wave, int lane) {
+        const unsigned lo = (unsigned)((lane / LW) * ld + (lane % LW) * 8) * 2u;
+#pragma unroll
+        for (int b = 0; b < BPW; b++) {
+            const uint16_t *wb = W + (long)((wave * BPW + b) * RPI) * ld;
+#pragma unroll
+            for (int s = 0; s < SEGS; s++) w[b][s] = px_ld16(wb + s * 8 * LW, lo);
+        }
+    }
+
+    // slab row of batch b for this lane
+    __device__ __forceinline__ static int row(int wave, int b, int lane) { return (wave * BPW + b) * RPI + lane / LW; }
+
+    // y[b] = W[row] . x for the row of batch b, in every lane of the LW group
+    __device__ __forceinline__ void dot(const float *x, float (&y)[BPW], int lane) const {
+        const int cl = (lane % LW) * 8;
+#pragma unroll
+        for (int b = 0; b < BPW; b++) y[b] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SEGS; s++) {
+            float xv[8];
+            const float4 p0 = *reinterpret_cast<const float4 *>(x + s * 8 * LW + cl);
+            const float4 p1 = *reinterpret_cast<const float4 *>(x + s * 8 * LW + cl + 4);
+            xv[0] = p0.x; xv[1] = p0.y; xv[2] = p0.z; xv[3] = p0.w;
+            xv[4] = p1.x; xv[5] = p1.y; xv[6] = p1.z; xv[7] = p1.w;
+#pragma unroll
+            for (int b = 0; b < BPW; b++) y[b] = dot8_bf16(w[b][s], xv, y[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < BPW; b++) y[b] = group_sum<LW>(y[b]);
+    }
+};
+
+// K/V rows of one attention split in flight: 16 lanes own a position, 8 dims each
+template <int AB>
+struct PxKv {
+    float4 k[AB][2], v[AB][2];
+    // kb, vb: wave-uniform (layer, kv head) bases; lane owns dims [8*gl, 8*gl+8)
+    // of position p0 + stride*j (positions >= end give zeros)
+    __device__ __forceinline__ void load(const float *kb, const float *vb, int gl, int p0, int stride, int end) {
+#pragma unroll
+        for (int j = 0; j < AB; j++) {
+            // every element is (re)defined so the compiler can drop the old batch
+            const int p = p0 + stride * j;
+            const bool in = p < end;
+            const unsigned o = (unsigned)((in ? p : 0) * 128 + gl * 8) * 4u;
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            k[j][0] = in ? px_ldf4(kb, o) : z;
+            k[j][1] = in ? px_ldf4(kb, o + 16u) : z;
+            v[j][0] = in ? px_ldf4(vb, o) : z;
+            v[j][1] = in ? px_ldf4(vb, o + 16u) : z;
+        }
+    }
+};
+
+// Issue the first K/V batch of a split straight into LDS (no registers held
+// across the stages in between).  Lane (16-lane group gi, gl) loads dims
+// [8gl, 8gl+8) of position p0 + stride*j; positions >= end load position 0
+// (always valid memory) and are never folded.  Each wave later reads back only
+// what it loaded itself, after s_waitcnt vmcnt(0).
+template <int AB>
+__device__ __forceinline__ void px_kv_dma(uint4 (&dst)[AB][4][64], const float *kb, const float *vb, int gl, int p0,
+                                          int stride, int end) {
+#pragma unroll
+    for (int j = 0; j < AB; j++) {
+        const int p = p0 + stride * j;
+        const unsigned o = (unsigned)((p < end ? p : 0) * 128 + gl * 8) * 4u;
+        const char *kc = reinterpret_cast<const char *>(kb) + o;
+        const char *vc = reinterpret_cast<const char *>(vb) + o;
+        __builtin_amdgcn_global_load_lds(kc, &dst[j][0][0], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(kc + 16, &dst[j][1][0], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vc, &dst[j][2][0], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vc + 16, &dst[j][3][0], 16, 0, 0);
+    }
+}
+
+__device__ __forceinline__ float4 px_u2f(uint4 u) {
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+}
+
+// online-softmax fold of one key/value position into both query heads
+__device__ __forceinline__ void px_fold(const float (&q)[2][8], float4 k0, float4 k1, float4 v0, float4 v1, float scale,
+                                        float (&m)[2], float (&l)[2], float (&o)[2][8]) {
+    const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) d = fmaf(q[h][j], kv[j], d);
+        d = group_sum<16>(d);
+        const float sc = d * scale;
+        const float mn = fmaxf(m[h], sc);
+        const float corr = __expf(m[h] - mn), pw = __expf(sc - mn);
+        l[h] = fmaf(l[h], corr, pw);
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[h][j] = fmaf(o[h][j], corr, pw * vv[j]);
+        m[h] = mn;
+    }
+}
+
+// The split of positions [0, pos] a block of the group works on.
+struct PxSplit {
+    int nsplit, s0, s1, cend;
+    bool active, last;
+    __device__ __forceinline__ PxSplit(int pos, int r) {
+        const int seq = pos + 1;
+        int chunk = (seq + QK_PX_MAX_SPLIT - 1) / QK_PX_MAX_SPLIT;
+        if (chunk < QK_PX_MIN_CHUNK) chunk = QK_PX_MIN_CHUNK;
+        nsplit = (seq + chunk - 1) / chunk;
+        active = r < nsplit;
+        s0 = r * chunk;
+        s1 = min(s0 + chunk, seq);
+        last = active && s1 == seq;
+        cend = last ? pos : s1;      // position pos itself comes from this step's k/v
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Shared state of a block
+// ---------------------------------------------------------------------------
+template <int H, int I, int NCW>
+struct PxShared {
+    static constexpr int SO = H / QK_PX_LOC;    // O / down rows per block
+    static constexpr int HG = I / QK_PX_XCD;    // SwiGLU outputs per XCD group
+    static constexpr int NG = NCW * 4;          // 16-lane attention groups
+    float xs[H];                                // residual (kept identical in every block)
+    float xn[H];                                // normed input of Q / F / LM head
+    float qkv[512];                             // raw q|q|k|v of the group
+    float qr[2][128], kr[128], vr[128];         // normed + rotated q, k; v
+    float sm_m[NG][2], sm_l[NG][2];
+    float sm_o[NG][2][128];
+    float part[QK_PX_MAX_SPLIT * QK_PX_PART];   // split partials of the group
+    float att[256];                             // merged attention output of the group
+    float hs[HG];                               // SwiGLU outputs of the group
+    float ysum[8 * SO];                         // split-K partial slices
+    float wv[NCW];
+    int wi[NCW];
+    float cand[2 * QK_PX_BLOCKS];
+    // first K/V batch of the attention split, loaded straight into LDS: per
+    // compute wave, AB positions x (k[0:4], k[4:8], v[0:4], v[4:8]) x 64 lanes
+    uint4 kvb[NCW][64 / NG][4][64];
+    int g, r, abort_, tok;
+};
+
+template <int H>
+__device__ __forceinline__ const char *px_layer(const qk_persist_args &a, int l) {
+    return a.layer0 + (long)l * a.layer_stride;
+}
+
+// ---------------------------------------------------------------------------
+// sync wave
+// ---------------------------------------------------------------------------
+template <int H, int I, int NCW>
+__device__ bool px_x_update(const qk_persist_args &a, PxShared<H, I, NCW> &S, const u64 *yp, unsigned ty, u64 *xl,
+                            unsigned tx, int lane) {
+    constexpr int SO = PxShared<H, I, NCW>::SO;
+    const int r = S.r;
+    // this block's slice of the 8 split-K partials
+    auto slice = [&](int i) { return yp + (long)(i / SO) * H + SO * r + (i % SO); };
+    if (!px_poll<8 * SO / 64>(slice, 8 * SO, ty, S.ysum, a.err, lane)) return false;
+    if (lane < SO) {
+        float o = S.ysum[lane];
+#pragma unroll
+        for (int gg = 1; gg < QK_PX_XCD; gg++) o += S.ysum[gg * SO + lane];
+        px_put_local(xl + SO * r + lane, S.xs[SO * r + lane] + o, tx);   // x += o (qwen_asr_decoder.c:458, :468)
+    }
+    // the XCD's whole new residual
+    auto whole = [&](int i) { return xl + i; };
+    return px_poll<H / 64>(whole, H, tx, S.xs, a.err, lane);
+}
+
+// xn = rms_norm(xs) * w (qwen_rms_norm, qwen_asr_kernels.c:750-809); w already in registers
+template <int H, int I, int NCW>
+__device__ void px_rmsnorm(const qk_persist_args &a, PxShared<H, I, NCW> &S, const float (&w)[H / 64], int lane) {
+    float v[H / 64], ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < H / 64; j++) {
+        v[j] = S.xs[j * 64 + lane];
+        ss = fmaf(v[j], v[j], ss);
+    }
+    ss = wave_sum(ss);
+    const float rinv = 1.0f / sqrtf(ss / (float)H + a.eps);
+#pragma unroll
+    for (int j = 0; j < H / 64; j++) S.xn[j * 64 + lane] = (v[j] * w[j]) * rinv;
+}
+
+template <int H>
+__device__ __forceinline__ void px_load_norm(const float *p, float (&w)[H / 64], int lane) {
+#pragma unroll
+    for (int j = 0; j < H / 64; j++) w[j] = p[j * 64 + lane];
+}
+
+template <int H, int I, int NCW>
+__device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, int lane) {
+    constexpr int HG = PxShared<H, I, NCW>::HG;
+    const int L = a.layers, b = blockIdx.x;
+    const long WG = (long)QK_PX_XCD;
+    float nw[H / 64];
+
+    // ---- launch check-in: every block must sit on XCD g < 8 with rank < 32 ----
+    px_sync();
+    {
+        float *dst = S.cand;   // scratch
+        auto addr = [&](int i) { return a.xv + i; };
+        bool ok = px_poll<4>(addr, QK_PX_BLOCKS, a.epoch, dst, a.err, lane);
+        if (ok) {
+            bool good = true;
+            for (int i = lane; i < QK_PX_BLOCKS; i += 64) good = good && (__float_as_uint(dst[i]) & 1u);
+            if (!__all(good)) {
+                ok = false;
+                if (lane == 0) px_raise(a.err, QK_PX_ERR_LAYOUT);
+            }
+        }
+        if (lane == 0) S.abort_ = ok ? 0 : 1;
+    }
+    px_sync();
+    if (S.abort_) return;
+    const int g = __builtin_amdgcn_readfirstlane(S.g);
+
+    for (int s = 0; s < a.n_steps; s++) {
+        const int pos = a.pos0 + s;
+        const unsigned tstep = a.epoch + 1u + (unsigned)s * (7u * (unsigned)L + 1u);
+        for (int l = 0; l < L; l++) {
+            const unsigned T = tstep + 7u * (unsigned)l;
+            const int par = l & 1;
+            const char *lb = px_layer<H>(a, l);
+            bool ok = true;
+            // ---- Q: input (embedding / x_in) or x += down partials; input norm ----
+            px_load_norm<H>((const float *)(lb + a.off_nin), nw, lane);
+            px_sync();
+            if (l == 0) {
+                if (s == 0 && a.first_tok < 0) {
+                    for (int i = lane; i < H; i += 64) S.xs[i] = a.x_in[i];
+                } else {
+                    // tok_embed_bf16_to_f32 (qwen_asr.c:353-360)
+                    const int tok = (s == 0) ? a.first_tok : S.tok;
+                    const uint16_t *e = a.emb + (long)tok * H;
+                    for (int i = lane * 8; i < H; i += 512) {
+                        const uint4 q = *reinterpret_cast<const uint4 *>(e + i);
+                        S.xs[i + 0] = bf16_lo(q.x); S.xs[i + 1] = bf16_hi(q.x);
+                        S.xs[i + 2] = bf16_lo(q.y); S.xs[i + 3] = bf16_hi(q.y);
+                        S.xs[i + 4] = bf16_lo(q.z); S.xs[i + 5] = bf16_hi(q.z);
+                        S.xs[i + 6] = bf16_lo(q.w); S.xs[i + 7] = bf16_hi(q.w);
+                    }
+                }
+            } else {
+                const int pp = (l - 1) & 1;
+                ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T - 7u + 5u, a.xlb + (pp * WG + g) * H,
+                                            T - 7u + 6u, lane);
+            }
+            if (ok) px_rmsnorm<H, I, NCW>(a, S, nw, lane);
+            if (lane == 0) S.abort_ = !ok;
+            px_sync();
+            if (S.abort_) return;
+
+            // ---- A: the group's q|q|k|v ----
+            px_sync();
+            {
+                const u64 *src = a.xq + (par * WG + g) * 512;
+                auto addr = [&](int i) { return src + i; };
+                ok = px_poll<8>(addr, 512, T, S.qkv, a.err, lane);
+            }
+            if (lane == 0) S.abort_ = !ok;
+            px_sync();
+            if (S.abort_) return;
+            px_sync();   // after q/k norm + RoPE
+            px_sync();   // after the position fold
+
+            // ---- O: the group's split partials ----
+            px_sync();
+            {
+                const PxSplit sp(pos, 0);
+                const u64 *src = a.xa + (par * WG + g) * (long)(QK_PX_MAX_SPLIT * QK_PX_PART);
+                auto addr = [&](int i) { return src + i; };
+                ok = px_poll<33>(addr, sp.nsplit * QK_PX_PART, T + 1u, S.part, a.err, lane);
+            }
+            if (lane == 0) S.abort_ = !ok;
+            px_sync();
+            if (S.abort_) return;
+            px_sync();   // after the merge
+
+            // ---- F: x += O partials; post-attention norm ----
+            px_load_norm<H>((const float *)(lb + a.off_npost), nw, lane);
+            px_sync();
+            ok = px_x_update<H, I, NCW>(a, S, a.xo + (par * WG) * H, T + 2u, a.xla + (par * WG + g) * H, T + 3u, lane);
+            if (ok) px_rmsnorm<H, I, NCW>(a, S, nw, lane);
+            if (lane == 0) S.abort_ = !ok;
+            px_sync();
+            if (S.abort_) return;
+
+            // ---- D: the group's SwiGLU outputs ----
+            px_sync();
+            {
+                const u64 *src = a.xh + (par * WG + g) * HG;
+                auto addr = [&](int i) { return src + i; };
+                ok = px_poll<(HG + 63) / 64>(addr, HG, T + 4u, S.hs, a.err, lane);
+            }
+            if (lane == 0) S.abort_ = !ok;
+            px_sync();
+            if (S.abort_) return;
+        }
+        // ---- LM: x += last down partials; final norm (in place in the reference, :474) ----
+        {
+            const unsigned T = tstep + 7u * (unsigned)(L - 1);
+            const int pp = (L - 1) & 1;
+            px_load_norm<H>(a.fnorm, nw, lane);
+            px_sync();
+            bool ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T + 5u, a.xlb + (pp * WG + g) * H, T + 6u, lane);
+            if (ok) {
+                px_rmsnorm<H, I, NCW>(a, S, nw, lane);
+                if (b == 0 && a.hidden_out)
+                    for (int i = lane; i < H; i += 64) a.hidden_out[i] = S.xn[i];
+            }
+            if (lane == 0) S.abort_ = !ok;
+            px_sync();
+            if (S.abort_) return;
+            px_sync();   // after the per-wave winners
+        }
+        // ---- T: argmax over the per-block candidates (qwen_asr_kernels.c:534-541) ----
+        {
+            const unsigned Tc = tstep + 7u * (unsigned)L;
+            px_sync();
+            auto addr = [&](int i) { return a.xc + i; };
+            bool ok = px_poll<8>(addr, 2 * QK_PX_BLOCKS, Tc, S.cand, a.err, lane);
+            if (ok) {
+                float bv = -1e30f;
+                int bi = 0x7fffffff;
+                for (int i = lane; i < QK_PX_BLOCKS; i += 64) {
+                    const float v = S.cand[i];
+                    const int ix = __float_as_int(S.cand[QK_PX_BLOCKS + i]);
+                    if (argmax_better(v, ix, bv, bi)) { bv = v; bi = ix; }
+                }
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) {
+                    const float ov = __shfl_xor(bv, m, 64);
+                    const int oi = __shfl_xor(bi, m, 64);
+                    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+                }
+                // nothing above the reference's -1e30 floor: it returns its start row
+                const int tok = bi == 0x7fffffff ? 0 : bi;
+                if (lane == 0) {
+                    S.tok = tok;
+                    if (b == 0) {
+                        if (a.log) a.log[s] = tok;
+                        if (a.tok_out) *a.tok_out = tok;
+                        if (a.pos_out) *a.pos_out = pos + 1;
+                    }
+                }
+            }
+            if (lane == 0) S.abort_ = !ok;
+            px_sync();
+            if (S.abort_) return;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// compute waves
+//
+// Weight slabs are issued stages before they are used so their HBM latency
+// overlaps the hand-overs.  DEEP (0.6B) keeps two stages in flight:
+//   end of D(l-1): K/V(l)     end of A: gate|up(l)
+//   end of O: down(l), Q(l+1) end of F: O(l+1)
+// the 1.7B slabs are 4x larger, so it issues each one stage ahead:
+//   end of D(l-1): K/V(l), O(l)   end of O: gate|up(l)   end of F: down(l), Q(l+1)
+// ---------------------------------------------------------------------------
+template <int H, int I, int NCW>
+__device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, int wave, int lane) {
+    constexpr int SO = PxShared<H, I, NCW>::SO;
+    constexpr int HG = PxShared<H, I, NCW>::HG;
+    constexpr int NG = PxShared<H, I, NCW>::NG;
+    constexpr int SEGH = H / 512;
+    constexpr int RF = 2 * I / QK_PX_BLOCKS;            // gate|up rows per block
+    constexpr int LMR = NCW == 4 ? 4 : 2;               // LM-head rows per wave batch
+    constexpr int AB = 64 / NG;                         // K/V positions per group in flight
+    constexpr bool DEEP = NCW == 4;
+    using SlabQ = PxSlab<64, SEGH, 16 / NCW>;
+    using SlabO = PxSlab<32, 1, SO / 2 / NCW>;
+    using SlabF = PxSlab<64, SEGH, RF / NCW>;
+    using SlabD = PxSlab<16, HG / 128, SO / 4 / NCW>;
+    static_assert(16 % NCW == 0 && (SO / 2) % NCW == 0 && RF % NCW == 0 && (SO / 4) % NCW == 0, "slab split");
+    // the slabs tile their row ranges exactly (no bounds checks in PxSlab::load)
+    static_assert(SlabQ::RPI * (16 / NCW) * NCW == 16 && SlabO::RPI * (SO / 2 / NCW) * NCW == SO, "tiling");
+    static_assert(SlabF::RPI * (RF / NCW) * NCW == RF && SlabD::RPI * (SO / 4 / NCW) * NCW == SO, "tiling");
+    static_assert((RF / NCW) % 2 == 0, "SwiGLU pairs must stay in one wave");
+    static_assert(HG % 128 == 0 && AB >= 1, "shape");
+
+    const int L = a.layers, b = blockIdx.x, tid = threadIdx.x;
+    const long WG = (long)QK_PX_XCD;
+    const int rpb = (a.vocab + QK_PX_BLOCKS - 1) / QK_PX_BLOCKS;
+    const int lm0 = b * rpb, lm1 = min(a.vocab, lm0 + rpb);
+    const int lmn = lm1 > lm0 ? (lm1 - lm0 + LMR - 1) / LMR : 0;
+
+    // launch check-in
+    if (tid == 0) {
+        const int xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20) & 15;   // HW_REG_XCC_ID
+        const unsigned rank = __hip_atomic_fetch_add(&a.cnt[xcc], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool good = xcc < QK_PX_XCD && rank < (unsigned)QK_PX_LOC;
+        S.g = xcc & 7;
+        S.r = (int)(rank & 31u);
+        __hip_atomic_store(&a.xv[b], ((u64)a.epoch << 32) | (good ? 1u : 0u), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    px_sync();
+    px_sync();
+    if (S.abort_) return;
+    const int g = __builtin_amdgcn_readfirstlane(S.g), r = __builtin_amdgcn_readfirstlane(S.r);
+
+    // the block's slices of every layer
+    const int qrow0 = r < 16 ? 256 * g + 16 * r
+                             : (r < 24 ? PX_QD + 128 * g + 16 * (r - 16) : PX_QD + PX_KVD + 128 * g + 16 * (r - 24));
+    auto Wq = [&](int l) { return (const uint16_t *)(px_layer<H>(a, l) + a.off_qkv) + (long)qrow0 * H; };
+    auto Wo = [&](int l) { return (const uint16_t *)(px_layer<H>(a, l) + a.off_o) + (long)(SO * r) * PX_QD + 256 * g; };
+    auto Wf = [&](int l) {
+        return (const uint16_t *)(px_layer<H>(a, l) + a.off_gu) + (long)((2 * I / QK_PX_XCD) * g + RF * r) * H;
+    };
+    auto Wd = [&](int l) { return (const uint16_t *)(px_layer<H>(a, l) + a.off_down) + (long)(SO * r) * I + HG * g; };
+    auto Kc = [&](int l) { return a.k_cache + ((long)l * QK_PX_XCD + g) * (long)a.cap * 128; };
+    auto Vc = [&](int l) { return a.v_cache + ((long)l * QK_PX_XCD + g) * (long)a.cap * 128; };
+
+    const int gid = wave * 4 + (lane >> 4), gl = lane & 15;
+    SlabQ wq;
+    SlabO wo;
+    SlabF wf;
+    SlabD wd;
+
+    // first step's layer-0 operands
+    {
+        const PxSplit sp(a.pos0, r);
+        wq.load(Wq(0), H, wave, lane);
+        wo.load(Wo(0), PX_QD, wave, lane);
+        if (sp.active) px_kv_dma<AB>(S.kvb[wave], Kc(0), Vc(0), gl, sp.s0 + gid, NG, sp.cend);
+    }
+
+    for (int s = 0; s < a.n_steps; s++) {
+        const int pos = a.pos0 + s;
+        const unsigned tstep = a.epoch + 1u + (unsigned)s * (7u * (unsigned)L + 1u);
+        const PxSplit sp(pos, r);
+        for (int l = 0; l < L; l++) {
+            const unsigned T = tstep + 7u * (unsigned)l;
+            const int par = l & 1;
+            const char *lb = px_layer<H>(a, l);
+            float *kcl = Kc(l), *vcl = Vc(l);
+
+            // ---- Q: the group's Q|K|V rows (qwen_linear_nobias_bf16_qkv, qwen_asr_kernels.c:434-460) ----
+            px_sync();
+            px_sync();
+            if (S.abort_) return;
+            {
+                float y[16 / NCW];
+                wq.dot(S.xn, y, lane);
+                if (lane == 0) {
+                    u64 *dst = a.xq + (par * WG + g) * 512 + 16 * r;
+#pragma unroll
+                    for (int i = 0; i < 16 / NCW; i++) px_put_local(dst + SlabQ::row(wave, i, 0), y[i], T);
+                }
+            }
+            // operands of the norm/RoPE step
+            float rc = 0.f, rs = 0.f, nw1 = 0.f, nw2 = 0.f;
+            if (wave < 3) {
+                rc = a.rope_cos[(long)pos * 128 + lane];
+                rs = a.rope_sin[(long)pos * 128 + lane];
+                const float *nwp = (const float *)(lb + (wave < 2 ? a.off_nq : a.off_nk));
+                nw1 = nwp[lane];
+                nw2 = nwp[lane + 64];
+            }
+
+            // ---- A: q/k norm + RoPE + K/V append + attention split (qwen_asr_decoder.c:439-455) ----
+            px_sync();
+            px_sync();
+            if (S.abort_) return;
+            if (wave < 3) {
+                const float *src = S.qkv + wave * 128;
+                float x1 = src[lane], x2 = src[lane + 64];
+                // rms_norm_per_head (qwen_asr_kernels.c:811-873) + apply_rope_neox (:1182-1247)
+                const float ss = wave_sum(fmaf(x1, x1, x2 * x2));
+                const float rinv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+                const float p1 = (x1 * nw1) * rinv, p2 = (x2 * nw2) * rinv;
+                x1 = fmaf(p1, rc, -(p2 * rs));
+                x2 = fmaf(p2, rc, p1 * rs);
+                float *dst = wave < 2 ? S.qr[wave] : S.kr;
+                dst[lane] = x1;
+                dst[lane + 64] = x2;
+                if (wave == 2 && sp.last) {   // K store at pos (qwen_asr_decoder.c:446)
+                    kcl[(long)pos * 128 + lane] = x1;
+                    kcl[(long)pos * 128 + lane + 64] = x2;
+                }
+            } else if (wave == 3) {
+                const float v1 = S.qkv[384 + lane], v2 = S.qkv[448 + lane];
+                S.vr[lane] = v1;
+                S.vr[lane + 64] = v2;
+                if (sp.last) {                // V store at pos (:447)
+                    vcl[(long)pos * 128 + lane] = v1;
+                    vcl[(long)pos * 128 + lane + 64] = v2;
+                }
+            }
+            px_sync();
+            if (sp.active) {
+                float q[2][8];
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) q[h][j] = S.qr[h][gl * 8 + j];
+                float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f}, o[2][8];
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) o[h][j] = 0.f;
+                // the first AB positions of each group were DMA'd into LDS by this wave
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int j = 0; j < AB; j++)
+                    if (sp.s0 + gid + NG * j < sp.cend)
+                        px_fold(q, px_u2f(S.kvb[wave][j][0][lane]), px_u2f(S.kvb[wave][j][1][lane]),
+                                px_u2f(S.kvb[wave][j][2][lane]), px_u2f(S.kvb[wave][j][3][lane]), a.scale, m, lsum, o);
+                // longer splits continue in register batches
+                for (int pb = sp.s0 + gid + NG * AB; pb < sp.cend; pb += NG * AB) {
+                    PxKv<AB> kv;
+                    kv.load(kcl, vcl, gl, pb, NG, sp.cend);
+#pragma unroll
+                    for (int j = 0; j < AB; j++)
+                        if (pb + NG * j < sp.cend) px_fold(q, kv.k[j][0], kv.k[j][1], kv.v[j][0], kv.v[j][1], a.scale, m, lsum, o);
+                }
+                if (sp.last && gid == 0) {
+                    const float4 *kn = reinterpret_cast<const float4 *>(&S.kr[gl * 8]);
+                    const float4 *vn = reinterpret_cast<const float4 *>(&S.vr[gl * 8]);
+                    px_fold(q, kn[0], kn[1], vn[0], vn[1], a.scale, m, lsum, o);
+                }
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    if (gl == 0) { S.sm_m[gid][h] = m[h]; S.sm_l[gid][h] = lsum[h]; }
+#pragma unroll
+                    for (int j = 0; j < 8; j++) S.sm_o[gid][h][gl * 8 + j] = o[h][j];
+                }
+            }
+            px_sync();
+            if (sp.active && tid < 256) {
+                const int h = tid >> 7, d = tid & 127;
+                float M = -INFINITY;
+                for (int i = 0; i < NG; i++) M = fmaxf(M, S.sm_m[i][h]);
+                float Lh = 0.0f, acc = 0.0f;
+                for (int i = 0; i < NG; i++) {
+                    const float mi = S.sm_m[i][h];
+                    const float e = (mi == -INFINITY) ? 0.0f : __expf(mi - M);
+                    Lh = fmaf(S.sm_l[i][h], e, Lh);
+                    acc = fmaf(S.sm_o[i][h][d], e, acc);
+                }
+                u64 *dst = a.xa + ((par * WG + g) * QK_PX_MAX_SPLIT + r) * (long)QK_PX_PART + h * 130;
+                px_put_local(dst + 2 + d, acc, T + 1u);
+                if (d == 0) {
+                    px_put_local(dst, M, T + 1u);
+                    px_put_local(dst + 1, Lh, T + 1u);
+                }
+            }
+            // The K/V row stored at pos is read by other blocks of this XCD in
+            // later steps; retire the stores before this wave writes anything
+            // those blocks can depend on.
+            if (sp.last && (wave == 2 || wave == 3)) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (DEEP) wf.load(Wf(l), H, wave, lane);
+
+            // ---- O: merge the splits, then this block's rows of W_o over the group's columns ----
+            px_sync();
+            px_sync();
+            if (S.abort_) return;
+            if (tid < 256) {
+                const int h = tid >> 7, d = tid & 127;
+                float M = -INFINITY;
+                for (int i = 0; i < sp.nsplit; i++) M = fmaxf(M, S.part[i * QK_PX_PART + h * 130]);
+                float Lh = 0.0f, acc = 0.0f;
+                for (int i = 0; i < sp.nsplit; i++) {
+                    const float *pp = S.part + i * QK_PX_PART + h * 130;
+                    const float e = (pp[0] == -INFINITY) ? 0.0f : __expf(pp[0] - M);
+                    Lh = fmaf(pp[1], e, Lh);
+                    acc = fmaf(pp[2 + d], e, acc);
+                }
+                S.att[h * 128 + d] = acc * (1.0f / Lh);   // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
+            }
+            px_sync();
+            {
+                float y[SO / 2 / NCW];
+                wo.dot(S.att, y, lane);
+                if ((lane & 31) == 0) {
+                    u64 *dst = a.xo + (par * WG + g) * H + SO * r;
+#pragma unroll
+                    for (int i = 0; i < SO / 2 / NCW; i++) px_put_global(dst + SlabO::row(wave, i, lane), y[i], T + 2u);
+                }
+            }
+            if (DEEP) {
+                wd.load(Wd(l), I, wave, lane);
+                if (l + 1 < L) wq.load(Wq(l + 1), H, wave, lane);
+            } else {
+                wf.load(Wf(l), H, wave, lane);
+            }
+
+            // ---- F: gate|up rows of the group + SwiGLU (qwen_asr_decoder.c:463-466) ----
+            px_sync();
+            px_sync();
+            if (S.abort_) return;
+            {
+                float y[RF / NCW];
+                wf.dot(S.xn, y, lane);
+                if (lane == 0) {
+                    u64 *dst = a.xh + (par * WG + g) * HG + (RF / 2) * r;
+#pragma unroll
+                    for (int i = 0; i < RF / NCW; i += 2)
+                        px_put_local(dst + SlabF::row(wave, i, 0) / 2, swiglu1(y[i], y[i + 1]), T + 4u);
+                }
+            }
+            if (DEEP) {
+                if (l + 1 < L) wo.load(Wo(l + 1), PX_QD, wave, lane);
+            } else {
+                wd.load(Wd(l), I, wave, lane);
+                if (l + 1 < L) wq.load(Wq(l + 1), H, wave, lane);
+            }
+
+            // ---- D: this block's rows of W_down over the group's columns (:467-468) ----
+            px_sync();
+            px_sync();
+            if (S.abort_) return;
+            {
+                float y[SO / 4 / NCW];
+                wd.dot(S.hs, y, lane);
+                if ((lane & 15) == 0) {
+                    u64 *dst = a.xd + (par * WG + g) * H + SO * r;
+#pragma unroll
+                    for (int i = 0; i < SO / 4 / NCW; i++) px_put_global(dst + SlabD::row(wave, i, lane), y[i], T + 5u);
+                }
+            }
+            if (l + 1 < L) {
+                if (!DEEP) wo.load(Wo(l + 1), PX_QD, wave, lane);
+                if (sp.active) px_kv_dma<AB>(S.kvb[wave], Kc(l + 1), Vc(l + 1), gl, sp.s0 + gid, NG, sp.cend);
+            }
+        }
+        // the first LM-head rows, issued before the final hand-over
+        uint4 lmw[LMR][SEGH];
+#pragma unroll
+        for (int j = 0; j < LMR; j++) {
+            const int row = lm0 + wave * LMR + j;
+#pragma unroll
+            for (int c = 0; c < SEGH; c++)
+                lmw[j][c] = px_ld16(a.emb + (long)min(row, lm1 - 1) * H + c * 512, (unsigned)lane * 16u);
+        }
+
+        // ---- LM head: argmax over this block's rows of the tied embedding (qwen_argmax_matvec_bf16, :518-543) ----
+        px_sync();
+        px_sync();
+        if (S.abort_) return;
+        {
+            float bv = -1e30f;
+            int bi = 0x7fffffff;
+            for (int k = wave; k < lmn; k += NCW) {
+                uint4 nx[LMR][SEGH];
+                const bool more = k + NCW < lmn;
+                if (more) {
+#pragma unroll
+                    for (int j = 0; j < LMR; j++) {
+                        const int row = lm0 + (k + NCW) * LMR + j;
+#pragma unroll
+                        for (int c = 0; c < SEGH; c++)
+                            nx[j][c] = px_ld16(a.emb + (long)min(row, lm1 - 1) * H + c * 512, (unsigned)lane * 16u);
+                    }
+                }
+                float acc[LMR];
+#pragma unroll
+                for (int j = 0; j < LMR; j++) acc[j] = 0.0f;
+#pragma unroll
+                for (int c = 0; c < SEGH; c++) {
+                    float xv[8];
+                    const float4 p0 = *reinterpret_cast<const float4 *>(&S.xn[c * 512 + lane * 8]);
+                    const float4 p1 = *reinterpret_cast<const float4 *>(&S.xn[c * 512 + lane * 8 + 4]);
+                    xv[0] = p0.x; xv[1] = p0.y; xv[2] = p0.z; xv[3] = p0.w;
+                    xv[4] = p1.x; xv[5] = p1.y; xv[6] = p1.z; xv[7] = p1.w;
+#pragma unroll
+                    for (int j = 0; j < LMR; j++) acc[j] = dot8_bf16(lmw[j][c], xv, acc[j]);
+                }
+                reduce_rows<LMR, 1>(acc, lane);   // lane groups of 64/LMR hold row lane / (64/LMR)
+                const int row = lm0 + k * LMR + lane / (64 / LMR);
+                if (row < lm1) {
+                    if (a.logits && (lane % (64 / LMR)) == 0) a.logits[row] = acc[0];
+                    if (argmax_better(acc[0], row, bv, bi)) { bv = acc[0]; bi = row; }
+                }
+                if (more) {
+#pragma unroll
+                    for (int j = 0; j < LMR; j++)
+#pragma unroll
+                        for (int c = 0; c < SEGH; c++) lmw[j][c] = nx[j][c];
+                }
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+                const float ov = __shfl_xor(bv, m, 64);
+                const int oi = __shfl_xor(bi, m, 64);
+                if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) { S.wv[wave] = bv; S.wi[wave] = bi; }
+        }
+        px_sync();
+        if (tid == 0) {
+            float bv = S.wv[0];
+            int bi = S.wi[0];
+            for (int w = 1; w < NCW; w++)
+                if (argmax_better(S.wv[w], S.wi[w], bv, bi)) { bv = S.wv[w]; bi = S.wi[w]; }
+            const unsigned Tc = tstep + 7u * (unsigned)L;
+            px_put_global(a.xc + b, bv, Tc);
+            px_put_global(a.xc + QK_PX_BLOCKS + b, __int_as_float(bi), Tc);
+        }
+        if (s + 1 < a.n_steps) {   // next step's layer-0 operands
+            const PxSplit sn(pos + 1, r);
+            wq.load(Wq(0), H, wave, lane);
+            wo.load(Wo(0), PX_QD, wave, lane);
+            if (sn.active) px_kv_dma<AB>(S.kvb[wave], Kc(0), Vc(0), gl, sn.s0 + gid, NG, sn.cend);
+        }
+        // ---- T: the sync wave reduces the candidates ----
+        px_sync();
+        px_sync();
+        if (S.abort_) return;
+    }
+}
+
+template <int H, int I, int NCW>
+__global__ __launch_bounds__((NCW + 1) * 64, 1) void px_decode(qk_persist_args a) {
+    __shared__ __attribute__((aligned(16))) PxShared<H, I, NCW> S;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (wave == NCW) px_sync_role<H, I, NCW>(a, S, lane);
+    else px_compute_role<H, I, NCW>(a, S, wave, lane);
+}
+
+// 0.6B: hidden 1024, intermediate 3072, 4 compute waves; 1.7B: 2048 / 6144, 8.
+#define PX_K06 px_decode<1024, 3072, 4>
+#define PX_K17 px_decode<2048, 6144, 8>
+
+static const void *px_kernel(int hidden, int inter, int *threads) {
+    if (hidden == 1024 && inter == 3072) { *threads = 5 * 64; return (const void *)PX_K06; }
+    if (hidden == 2048 && inter == 6144) { *threads = 9 * 64; return (const void *)PX_K17; }
+    return nullptr;
+}
+
+extern "C" int qk_persist_supported(int hidden, int inter, int heads, int kv_heads, int device) {
+    int threads = 0;
+    const void *k = px_kernel(hidden, inter, &threads);
+    if (!k || heads != 16 || kv_heads != QK_PX_XCD) return 0;
+    int cus = 0, coop = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess) return 0;
+    if (cus != QK_PX_BLOCKS || !coop) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, threads, 0) != hipSuccess || per < 1) return 0;
+    return 1;
+}
+
+extern "C" int qk_persist_launch(const qk_persist_args *a, int hidden, int inter, hipStream_t s) {
+    int threads = 0;
+    const void *k = px_kernel(hidden, inter, &threads);
+    if (!a || !k || a->n_steps <= 0 || a->layers <= 0 || a->epoch == 0u) return QWEN_HIP_EINVAL;
+    if (a->first_tok < 0 && !a->x_in) return QWEN_HIP_EINVAL;
+    if (a->first_tok >= a->vocab || a->pos0 < 0 || a->pos0 + a->n_steps > a->cap) return QWEN_HIP_EINVAL;
+    qk_persist_args copy = *a;
+    void *args[] = {&copy};
+    if (hipLaunchCooperativeKernel(k, dim3(QK_PX_BLOCKS), dim3(threads), args, 0, s) != hipSuccess)
+        return QWEN_HIP_EDEVICE;
+    return 0;
+}

@@ -124,6 +124,62 @@ typedef struct {
 int qk_attn_fused_launch(const qk_attn_fused_args *a, hipStream_t s);
 int qk_attn_merge_launch(const qk_attn_fused_args *a, hipStream_t s);
 
+/* ---- persistent decode (the whole greedy loop in one launch) ----------- */
+/* One block per CU, 8 XCDs x 32 CUs; XCD g owns kv head g.  Blocks exchange
+ * activations through 64-bit words carrying (tag << 32 | fp32 bits): XCD-local
+ * words go through the XCD's L2, cross-XCD words through memory-side coherent
+ * accesses.  Word counts below are per buffer. */
+#define QK_PX_XCD 8
+#define QK_PX_LOC 32
+#define QK_PX_BLOCKS (QK_PX_XCD * QK_PX_LOC)
+#define QK_PX_MAX_SPLIT 32                 /* attention splits per kv head (one per CU) */
+#define QK_PX_PART 260                     /* words per split: 2 heads x (m, l, o[128]) */
+#define QK_PX_MIN_CHUNK 64                 /* positions per split, at least */
+enum { QK_PX_ERR_LAYOUT = 1, QK_PX_ERR_TIMEOUT = 2 };
+
+typedef struct {
+    /* layer l tensors live at layer0 + l * layer_stride + off_* (bytes) */
+    const char *layer0;
+    long layer_stride;
+    long off_qkv, off_o, off_gu, off_down, off_nin, off_npost, off_nq, off_nk;
+    const uint16_t *emb;       /* [vocab][hidden] tied embedding / LM head */
+    const float *fnorm;
+    float *k_cache, *v_cache;  /* [layer][kv_head][cap][128] */
+    int cap;
+    const float *rope_cos, *rope_sin;
+    int layers, vocab;
+    float eps, scale;
+    /* exchange buffers (zero-initialised; each [2 parities][8 XCDs][...]) */
+    unsigned long long *xq;    /* [2][8][512]  q|q|k|v of the group */
+    unsigned long long *xa;    /* [2][8][32][QK_PX_PART] attention split partials */
+    unsigned long long *xo;    /* [2][8][hidden] O-projection split-K partials (cross-XCD) */
+    unsigned long long *xla;   /* [2][8][hidden] residual after attention (XCD-local copy) */
+    unsigned long long *xh;    /* [2][8][inter/8] SwiGLU outputs of the group */
+    unsigned long long *xd;    /* [2][8][hidden] down-projection split-K partials (cross-XCD) */
+    unsigned long long *xlb;   /* [2][8][hidden] residual after the MLP (XCD-local copy) */
+    unsigned long long *xc;    /* [256][2] LM-head argmax candidates (cross-XCD) */
+    unsigned long long *xv;    /* [256] launch check-in words */
+    unsigned *cnt;             /* [16] per-XCD tickets, zeroed before every launch */
+    unsigned *err;             /* QK_PX_ERR_* bits, zeroed before every launch */
+    unsigned epoch;            /* first tag of this launch (>= 1) */
+    /* the steps */
+    int pos0, n_steps;
+    int first_tok;             /* >= 0: step 0 input is emb[first_tok] */
+    const float *x_in;         /* first_tok < 0: step 0 input row [hidden] */
+    int *log;                  /* [n_steps] greedy tokens */
+    int *tok_out;              /* last token */
+    int *pos_out;              /* position after the last step (= pos0 + n_steps) */
+    float *hidden_out;         /* final-normed hidden row of each step */
+    float *logits;             /* optional [vocab] logits of each step */
+} qk_persist_args;
+
+/* tags one launch of n steps consumes (the host advances epoch by this) */
+#define QK_PX_TAGS(layers, n) (1u + (unsigned)(n) * (7u * (unsigned)(layers) + 1u))
+
+/* 1 if the persistent engine supports this shape on this device */
+int qk_persist_supported(int hidden, int inter, int heads, int kv_heads, int device);
+int qk_persist_launch(const qk_persist_args *a, int hidden, int inter, hipStream_t s);
+
 /* ---- prefill (MFMA) ---------------------------------------------------- */
 /* hi/lo = bf16 split of rms_norm(x)*w (w NULL: of x itself): hi = bf16(v),
  * lo = bf16(v - hi), so hi + lo carries v to ~2^-17 relative. */

@@ -213,26 +213,33 @@ def free_run(d, rows, g):
     return len(toks)
 
 
+@pytest.mark.parametrize("engine", [0, 2])
 @pytest.mark.parametrize("name", ["c1_short", "c1_full"])
-def test_06b_golden(P, model06, name):
+def test_06b_golden(P, model06, name, engine):
     g = np.load(os.path.join(GOLD, f"{name}.npz"))
     d, emb = model06
+    d.set_engine(engine)
     assert P.checksum_u16(emb) == int(g["emb_checksum"])
     rows, ids = prompt(P, P.CFG_06B, emb, int(g["n_audio"]), int(g["n_ids"]))
     assert np.array_equal(ids, g["ids"])
     worst, near = teacher_forced(d, rows, g)
     agree = free_run(d, rows, g)
-    print(f"{name}: max |dlogit| on reference top-8 = {worst:.3e}; near-tie steps {near}; "
+    assert d.engine() == engine, "the engine fell back during the run"
+    print(f"{name} engine {engine}: max |dlogit| on reference top-8 = {worst:.3e}; near-tie steps {near}; "
           f"free run agrees for {agree}/{len(g['tokens'])} tokens")
 
 
-def test_17b_golden(P, qa, gpu):
+@pytest.mark.parametrize("engine", [0, 2])
+def test_17b_golden(P, qa, gpu, engine):
     g = np.load(os.path.join(GOLD, "c3_short.npz"))
     d = qa.Decoder(qa.preset(1), 0, 1024)
     d.load_synthetic(0, 0.02, 0.0)
+    d.set_engine(engine)
     emb = P.synth_bf16(P.CFG_17B.vocab * P.CFG_17B.hidden, 0, P.SYNTH_EMBED).reshape(P.CFG_17B.vocab, -1)
     rows, ids = prompt(P, P.CFG_17B, emb, int(g["n_audio"]), int(g["n_ids"]))
     worst, near = teacher_forced(d, rows, g)
     agree = free_run(d, rows, g)
-    print(f"c3_short: max |dlogit| = {worst:.3e}; near-tie steps {near}; free run agrees {agree}/{len(g['tokens'])}")
+    assert d.engine() == engine, "the engine fell back during the run"
+    print(f"c3_short engine {engine}: max |dlogit| = {worst:.3e}; near-tie steps {near}; "
+          f"free run agrees {agree}/{len(g['tokens'])}")
     d.close()
