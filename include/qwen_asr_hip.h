@@ -162,6 +162,26 @@ int qwen_hip_decoder_read_logits(qwen_hip_decoder *dec, float *out);
 int qwen_hip_decoder_set_engine(qwen_hip_decoder *dec, int engine);
 int qwen_hip_decoder_engine(const qwen_hip_decoder *dec);
 
+/* Diagnostics of the persistent engine (no reference counterpart; the
+ * reference only times whole phases with gettimeofday, qwen_asr.c:362-366).
+ * set_trace(step >= 0): every later persistent launch records, for its step
+ * index `step`, a 100 MHz wall-clock stamp per block at each hand-over point
+ * (step < 0 turns it off).  read_trace copies the last record,
+ * [256 blocks][704] uint64 (n >= 256*704), and returns the words per block.
+ * Per layer l the stamps sit at 10*l + {0 Q entered, 1 Q input ready,
+ * 2 attention entered, 3 its input ready, 4 O entered, 5 ready, 6 MLP entered,
+ * 7 ready, 8 down entered, 9 ready}, then 10*layers + {0 LM head entered,
+ * 1 ready, 2 token reduction entered, 3 token ready}; "entered" means the
+ * block's compute of the previous stage is done.  Compute-side stamps of
+ * layer l sit at 320 + 10*l + {0 QKV dot done, 1 its stores and the next
+ * prefetches issued, 2 q/k norm done, 3 attention fold done, 4 split partial
+ * stored, 5 splits merged, 6 O dot done, 7 O stores and prefetches issued,
+ * 8 gate/up dot done, 9 down dot done}; 640 + 2*l + {0, 1}: the cross-XCD
+ * half of the residual update before QKV / before the MLP is done (640 + 2*layers:
+ * the final one). */
+int qwen_hip_decoder_set_trace(qwen_hip_decoder *dec, int step);
+int qwen_hip_decoder_read_trace(qwen_hip_decoder *dec, uint64_t *out, size_t n);
+
 /* The stream the decoder launches on (for event timing by callers). */
 hipStream_t qwen_hip_decoder_stream(const qwen_hip_decoder *dec);
 

@@ -64,6 +64,8 @@ SIGNATURES = [
     ("qwen_hip_decoder_read_logits", _i, [_vp, _vp]),
     ("qwen_hip_decoder_set_engine", _i, [_vp, _i]),
     ("qwen_hip_decoder_engine", _i, [_vp]),
+    ("qwen_hip_decoder_set_trace", _i, [_vp, _i]),
+    ("qwen_hip_decoder_read_trace", _i, [_vp, _vp, C.c_size_t]),
     ("qwen_hip_decoder_stream", _vp, [_vp]),
     ("qwen_hip_decoder_step_bytes", _d, [_vp, _i]),
     ("qwen_hip_last_error", C.c_char_p, []),
@@ -236,6 +238,15 @@ class Decoder:
     def engine(self):
         """Active decode engine: 0 graph, 1 eager, 2 persistent."""
         return lib().qwen_hip_decoder_engine(self.h)
+
+    def set_trace(self, step):
+        check(lib().qwen_hip_decoder_set_trace(self.h, int(step)), "set_trace")
+
+    def read_trace(self):
+        """[256 blocks][704] wall-clock stamps (100 MHz) of the traced step."""
+        out = np.zeros((256, 704), np.uint64)
+        check(lib().qwen_hip_decoder_read_trace(self.h, _ptr(out), out.size), "read_trace")
+        return out
 
     def read_hidden(self):
         out = np.empty(self.cfg.hidden, np.float32)

@@ -113,6 +113,8 @@ struct qwen_hip_decoder {
     unsigned long long *xq, *xa, *xo, *xla, *xh, *xd, *xlb, *xc, *xv;
     unsigned *px_ctl;         /* [0, 16) per-XCD tickets, [16] error bits */
     unsigned px_epoch;
+    unsigned long long *px_trace;   /* [256][QK_PX_TRACE] when tracing */
+    int px_trace_step;              /* < 0: off */
 };
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -264,6 +266,7 @@ static int px_alloc(qwen_hip_decoder *d) {
     QK_HIP(hipMemset(d->px_buf, 0, d->px_words * 8));
     QK_HIP(hipMemset(d->px_ctl, 0, 64 * sizeof(unsigned)));
     d->px_epoch = 1;
+    d->px_trace_step = -1;
     return 0;
 }
 
@@ -372,7 +375,7 @@ void qwen_hip_decoder_destroy(qwen_hip_decoder *d) {
     dev_free(d->x); dev_free(d->qkv); dev_free(d->part_o); dev_free(d->part_m); dev_free(d->part_l);
     dev_free(d->attn_out); dev_free(d->h); dev_free(d->hidden); dev_free(d->logits);
     dev_free(d->cand_val); dev_free(d->cand_idx); dev_free(d->ctl); dev_free(d->d_log);
-    dev_free(d->px_buf); dev_free(d->px_ctl);
+    dev_free(d->px_buf); dev_free(d->px_ctl); dev_free(d->px_trace);
     prefill_free(d);
     if (d->h_row) (void)hipHostFree(d->h_row);
     if (d->h_int) (void)hipHostFree(d->h_int);
@@ -660,7 +663,8 @@ static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
         .xc = d->xc, .xv = d->xv, .cnt = d->px_ctl, .err = d->px_ctl + 16, .epoch = d->px_epoch,
         .pos0 = d->kv_len, .n_steps = n, .first_tok = first_tok, .x_in = d->x, .log = d->d_log,
         .tok_out = d->d_tok, .pos_out = d->d_pos, .hidden_out = d->hidden,
-        .logits = d->keep_logits ? d->logits : NULL};
+        .logits = d->keep_logits ? d->logits : NULL,
+        .trace = d->px_trace_step >= 0 && d->px_trace_step < n ? d->px_trace : NULL, .trace_step = d->px_trace_step};
     QK_TRY(qk_persist_launch(&a, c->hidden, c->intermediate, d->stream));
     d->px_epoch += need;
     QK_HIP(hipMemcpyAsync(&d->h_int[16], d->px_ctl + 16, sizeof(int), hipMemcpyDeviceToHost, d->stream));
@@ -778,6 +782,27 @@ int qwen_hip_decoder_set_engine(qwen_hip_decoder *d, int engine) {
 }
 
 int qwen_hip_decoder_engine(const qwen_hip_decoder *d) { return d ? d->engine : QWEN_HIP_EINVAL; }
+
+int qwen_hip_decoder_set_trace(qwen_hip_decoder *d, int step) {
+    if (!d) return QWEN_HIP_EINVAL;
+    if (!d->px_ok) { qk_set_err("set_trace: the persistent engine is not available"); return QWEN_HIP_ESTATE; }
+    QK_TRY(use_device(d));
+    if (step >= 0 && !d->px_trace) {
+        QK_TRY(dev_alloc((void **)&d->px_trace, (size_t)QK_PX_BLOCKS * QK_PX_TRACE * 8));
+        QK_HIP(hipMemset(d->px_trace, 0, (size_t)QK_PX_BLOCKS * QK_PX_TRACE * 8));
+    }
+    d->px_trace_step = step < 0 ? -1 : step;
+    return 0;
+}
+
+int qwen_hip_decoder_read_trace(qwen_hip_decoder *d, uint64_t *out, size_t n) {
+    const size_t need = (size_t)QK_PX_BLOCKS * QK_PX_TRACE;
+    if (!d || !out || n < need) { qk_set_err("read_trace: need %zu words", need); return QWEN_HIP_EINVAL; }
+    if (!d->px_trace) { qk_set_err("read_trace: tracing was never enabled"); return QWEN_HIP_ESTATE; }
+    QK_TRY(use_device(d));
+    QK_HIP(hipMemcpy(out, d->px_trace, need * 8, hipMemcpyDeviceToHost));
+    return (int)QK_PX_TRACE;
+}
 
 int qwen_hip_decoder_read_hidden(qwen_hip_decoder *d, float *out) {
     if (!d || !out) return QWEN_HIP_EINVAL;

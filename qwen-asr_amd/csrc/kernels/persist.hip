@@ -191,17 +191,19 @@ struct PxKv {
 };
 
 // Issue the first K/V batch of a split straight into LDS (no registers held
-// across the stages in between).  Lane (16-lane group gi, gl) loads dims
-// [8gl, 8gl+8) of position p0 + stride*j; positions >= end load position 0
-// (always valid memory) and are never folded.  Each wave later reads back only
-// what it loaded itself, after s_waitcnt vmcnt(0).
+// across the stages in between).  Lane (16-lane group, gl) loads dims
+// [8gl, 8gl+8) of position p0 + stride*j; positions >= end, and every position
+// of a block without a split, read position 0 (always valid memory) and are
+// never folded.  Every block issues the same loads, which keeps the
+// compiler's wait counting exact.  Each wave later reads back only what it
+// loaded itself, after waiting for its loads.
 template <int AB>
 __device__ __forceinline__ void px_kv_dma(uint4 (&dst)[AB][4][64], const float *kb, const float *vb, int gl, int p0,
-                                          int stride, int end) {
+                                          int stride, int end, bool active) {
 #pragma unroll
     for (int j = 0; j < AB; j++) {
         const int p = p0 + stride * j;
-        const unsigned o = (unsigned)((p < end ? p : 0) * 128 + gl * 8) * 4u;
+        const unsigned o = active ? (unsigned)((p < end ? p : 0) * 128 + gl * 8) * 4u : 0u;
         const char *kc = reinterpret_cast<const char *>(kb) + o;
         const char *vc = reinterpret_cast<const char *>(vb) + o;
         __builtin_amdgcn_global_load_lds(kc, &dst[j][0][0], 16, 0, 0);
@@ -211,11 +213,16 @@ __device__ __forceinline__ void px_kv_dma(uint4 (&dst)[AB][4][64], const float *
     }
 }
 
+// Wait for every load and store this wave issued (vmcnt(0)); the builtin keeps
+// the compiler's own wait bookkeeping in step.
+__device__ __forceinline__ void px_wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 __device__ __forceinline__ float4 px_u2f(uint4 u) {
     return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
 }
 
 // online-softmax fold of one key/value position into both query heads
+// (qwen_causal_attention_heads, qwen_asr_kernels.c:1073-1089)
 __device__ __forceinline__ void px_fold(const float (&q)[2][8], float4 k0, float4 k1, float4 v0, float4 v1, float scale,
                                         float (&m)[2], float (&l)[2], float (&o)[2][8]) {
     const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
@@ -265,8 +272,8 @@ struct PxShared {
     float xn[H];                                // normed input of Q / F / LM head
     float qkv[512];                             // raw q|q|k|v of the group
     float qr[2][128], kr[128], vr[128];         // normed + rotated q, k; v
-    float sm_m[NG][2], sm_l[NG][2];
-    float sm_o[NG][2][128];
+    float sm_m[NG][2], sm_l[NG][2];             // per 16-lane group: running max / sum
+    float sm_o[NG][2][128];                     // ... and output
     float part[QK_PX_MAX_SPLIT * QK_PX_PART];   // split partials of the group
     float att[256];                             // merged attention output of the group
     float hs[HG];                               // SwiGLU outputs of the group
@@ -274,11 +281,15 @@ struct PxShared {
     float wv[NCW];
     int wi[NCW];
     float cand[2 * QK_PX_BLOCKS];
-    // first K/V batch of the attention split, loaded straight into LDS: per
-    // compute wave, AB positions x (k[0:4], k[4:8], v[0:4], v[4:8]) x 64 lanes
-    uint4 kvb[NCW][64 / NG][4][64];
     int g, r, abort_, tok;
 };
+
+// First K/V batch of each attention split, loaded straight into LDS: per
+// compute wave, AB positions x (k[0:4], k[4:8], v[0:4], v[4:8]) x 64 lanes.
+// A __shared__ object of its own: LDS reads of PxShared then provably do not
+// alias the in-flight DMA, and the compiler does not wait for it ahead of them.
+template <int NCW>
+using PxKvLds = uint4[NCW][64 / (NCW * 4)][4][64];
 
 template <int H>
 __device__ __forceinline__ const char *px_layer(const qk_persist_args &a, int l) {
@@ -290,12 +301,13 @@ __device__ __forceinline__ const char *px_layer(const qk_persist_args &a, int l)
 // ---------------------------------------------------------------------------
 template <int H, int I, int NCW>
 __device__ bool px_x_update(const qk_persist_args &a, PxShared<H, I, NCW> &S, const u64 *yp, unsigned ty, u64 *xl,
-                            unsigned tx, int lane) {
+                            unsigned tx, int lane, unsigned long long *tr_hop = nullptr) {
     constexpr int SO = PxShared<H, I, NCW>::SO;
     const int r = S.r;
     // this block's slice of the 8 split-K partials
     auto slice = [&](int i) { return yp + (long)(i / SO) * H + SO * r + (i % SO); };
     if (!px_poll<8 * SO / 64>(slice, 8 * SO, ty, S.ysum, a.err, lane)) return false;
+    if (tr_hop) *tr_hop = wall_clock64();
     if (lane < SO) {
         float o = S.ysum[lane];
 #pragma unroll
@@ -353,19 +365,24 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
     }
     px_sync();
     if (S.abort_) return;
-    const int g = __builtin_amdgcn_readfirstlane(S.g);
+    const int g = __builtin_amdgcn_readfirstlane(S.g), r = __builtin_amdgcn_readfirstlane(S.r);
 
     for (int s = 0; s < a.n_steps; s++) {
         const int pos = a.pos0 + s;
-        const unsigned tstep = a.epoch + 1u + (unsigned)s * (7u * (unsigned)L + 1u);
+        const unsigned tstep = a.epoch + 1u + (unsigned)s * (QK_PX_TPL * (unsigned)L + 1u);
+        unsigned long long *tr = (a.trace && s == a.trace_step && lane == 0) ? a.trace + (long)b * QK_PX_TRACE : nullptr;
+        auto mark = [&](int i) {
+            if (tr) tr[i] = wall_clock64();
+        };
         for (int l = 0; l < L; l++) {
-            const unsigned T = tstep + 7u * (unsigned)l;
+            const unsigned T = tstep + QK_PX_TPL * (unsigned)l;
             const int par = l & 1;
             const char *lb = px_layer<H>(a, l);
             bool ok = true;
             // ---- Q: input (embedding / x_in) or x += down partials; input norm ----
             px_load_norm<H>((const float *)(lb + a.off_nin), nw, lane);
             px_sync();
+            mark(10 * l + 0);
             if (l == 0) {
                 if (s == 0 && a.first_tok < 0) {
                     for (int i = lane; i < H; i += 64) S.xs[i] = a.x_in[i];
@@ -383,21 +400,24 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
                 }
             } else {
                 const int pp = (l - 1) & 1;
-                ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T - 7u + 5u, a.xlb + (pp * WG + g) * H,
-                                            T - 7u + 6u, lane);
+                ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T - QK_PX_TPL + 5u, a.xlb + (pp * WG + g) * H,
+                                            T - QK_PX_TPL + 6u, lane, tr ? tr + QK_PX_TRACE_XU + 2 * l : nullptr);
             }
             if (ok) px_rmsnorm<H, I, NCW>(a, S, nw, lane);
+            mark(10 * l + 1);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
             if (S.abort_) return;
 
             // ---- A: the group's q|q|k|v ----
             px_sync();
+            mark(10 * l + 2);
             {
                 const u64 *src = a.xq + (par * WG + g) * 512;
                 auto addr = [&](int i) { return src + i; };
                 ok = px_poll<8>(addr, 512, T, S.qkv, a.err, lane);
             }
+            mark(10 * l + 3);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
             if (S.abort_) return;
@@ -406,12 +426,14 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
 
             // ---- O: the group's split partials ----
             px_sync();
+            mark(10 * l + 4);
             {
                 const PxSplit sp(pos, 0);
                 const u64 *src = a.xa + (par * WG + g) * (long)(QK_PX_MAX_SPLIT * QK_PX_PART);
                 auto addr = [&](int i) { return src + i; };
                 ok = px_poll<33>(addr, sp.nsplit * QK_PX_PART, T + 1u, S.part, a.err, lane);
             }
+            mark(10 * l + 5);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
             if (S.abort_) return;
@@ -420,35 +442,43 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             // ---- F: x += O partials; post-attention norm ----
             px_load_norm<H>((const float *)(lb + a.off_npost), nw, lane);
             px_sync();
-            ok = px_x_update<H, I, NCW>(a, S, a.xo + (par * WG) * H, T + 2u, a.xla + (par * WG + g) * H, T + 3u, lane);
+            mark(10 * l + 6);
+            ok = px_x_update<H, I, NCW>(a, S, a.xo + (par * WG) * H, T + 2u, a.xla + (par * WG + g) * H, T + 3u, lane,
+                                        tr ? tr + QK_PX_TRACE_XU + 2 * l + 1 : nullptr);
             if (ok) px_rmsnorm<H, I, NCW>(a, S, nw, lane);
+            mark(10 * l + 7);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
             if (S.abort_) return;
 
             // ---- D: the group's SwiGLU outputs ----
             px_sync();
+            mark(10 * l + 8);
             {
                 const u64 *src = a.xh + (par * WG + g) * HG;
                 auto addr = [&](int i) { return src + i; };
                 ok = px_poll<(HG + 63) / 64>(addr, HG, T + 4u, S.hs, a.err, lane);
             }
+            mark(10 * l + 9);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
             if (S.abort_) return;
         }
         // ---- LM: x += last down partials; final norm (in place in the reference, :474) ----
         {
-            const unsigned T = tstep + 7u * (unsigned)(L - 1);
+            const unsigned T = tstep + QK_PX_TPL * (unsigned)(L - 1);
             const int pp = (L - 1) & 1;
             px_load_norm<H>(a.fnorm, nw, lane);
             px_sync();
-            bool ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T + 5u, a.xlb + (pp * WG + g) * H, T + 6u, lane);
+            mark(10 * L + 0);
+            bool ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T + 5u, a.xlb + (pp * WG + g) * H, T + 6u, lane,
+                                             tr ? tr + QK_PX_TRACE_XU + 2 * L : nullptr);
             if (ok) {
                 px_rmsnorm<H, I, NCW>(a, S, nw, lane);
                 if (b == 0 && a.hidden_out)
                     for (int i = lane; i < H; i += 64) a.hidden_out[i] = S.xn[i];
             }
+            mark(10 * L + 1);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
             if (S.abort_) return;
@@ -456,10 +486,12 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
         }
         // ---- T: argmax over the per-block candidates (qwen_asr_kernels.c:534-541) ----
         {
-            const unsigned Tc = tstep + 7u * (unsigned)L;
+            const unsigned Tc = tstep + QK_PX_TPL * (unsigned)L;
             px_sync();
+            mark(10 * L + 2);
             auto addr = [&](int i) { return a.xc + i; };
             bool ok = px_poll<8>(addr, 2 * QK_PX_BLOCKS, Tc, S.cand, a.err, lane);
+            mark(10 * L + 3);
             if (ok) {
                 float bv = -1e30f;
                 int bi = 0x7fffffff;
@@ -503,14 +535,15 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
 //   end of D(l-1): K/V(l), O(l)   end of O: gate|up(l)   end of F: down(l), Q(l+1)
 // ---------------------------------------------------------------------------
 template <int H, int I, int NCW>
-__device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, int wave, int lane) {
+__device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, PxKvLds<NCW> &kvb, int wave,
+                                int lane) {
     constexpr int SO = PxShared<H, I, NCW>::SO;
     constexpr int HG = PxShared<H, I, NCW>::HG;
     constexpr int NG = PxShared<H, I, NCW>::NG;
+    constexpr int AB = 64 / NG;                         // K/V positions per 16-lane group in the LDS batch
     constexpr int SEGH = H / 512;
     constexpr int RF = 2 * I / QK_PX_BLOCKS;            // gate|up rows per block
     constexpr int LMR = NCW == 4 ? 4 : 2;               // LM-head rows per wave batch
-    constexpr int AB = 64 / NG;                         // K/V positions per group in flight
     constexpr bool DEEP = NCW == 4;
     using SlabQ = PxSlab<64, SEGH, 16 / NCW>;
     using SlabO = PxSlab<32, 1, SO / 2 / NCW>;
@@ -557,6 +590,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
     auto Vc = [&](int l) { return a.v_cache + ((long)l * QK_PX_XCD + g) * (long)a.cap * 128; };
 
     const int gid = wave * 4 + (lane >> 4), gl = lane & 15;
+    const bool tracer = a.trace && tid == 0;
     SlabQ wq;
     SlabO wo;
     SlabF wf;
@@ -567,18 +601,22 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
         const PxSplit sp(a.pos0, r);
         wq.load(Wq(0), H, wave, lane);
         wo.load(Wo(0), PX_QD, wave, lane);
-        if (sp.active) px_kv_dma<AB>(S.kvb[wave], Kc(0), Vc(0), gl, sp.s0 + gid, NG, sp.cend);
+        px_kv_dma<AB>(kvb[wave], Kc(0), Vc(0), gl, sp.s0 + gid, NG, sp.cend, sp.active);
     }
 
     for (int s = 0; s < a.n_steps; s++) {
         const int pos = a.pos0 + s;
-        const unsigned tstep = a.epoch + 1u + (unsigned)s * (7u * (unsigned)L + 1u);
+        const unsigned tstep = a.epoch + 1u + (unsigned)s * (QK_PX_TPL * (unsigned)L + 1u);
         const PxSplit sp(pos, r);
+        unsigned long long *tr = (tracer && s == a.trace_step) ? a.trace + (long)b * QK_PX_TRACE + QK_PX_TRACE_CW : nullptr;
         for (int l = 0; l < L; l++) {
-            const unsigned T = tstep + 7u * (unsigned)l;
+            const unsigned T = tstep + QK_PX_TPL * (unsigned)l;
             const int par = l & 1;
             const char *lb = px_layer<H>(a, l);
             float *kcl = Kc(l), *vcl = Vc(l);
+            auto mark = [&](int i) {
+                if (tr) tr[10 * l + i] = wall_clock64();
+            };
 
             // ---- Q: the group's Q|K|V rows (qwen_linear_nobias_bf16_qkv, qwen_asr_kernels.c:434-460) ----
             px_sync();
@@ -587,6 +625,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             {
                 float y[16 / NCW];
                 wq.dot(S.xn, y, lane);
+                mark(0);
                 if (lane == 0) {
                     u64 *dst = a.xq + (par * WG + g) * 512 + 16 * r;
 #pragma unroll
@@ -602,6 +641,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 nw1 = nwp[lane];
                 nw2 = nwp[lane + 64];
             }
+            mark(1);
 
             // ---- A: q/k norm + RoPE + K/V append + attention split (qwen_asr_decoder.c:439-455) ----
             px_sync();
@@ -632,7 +672,12 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     vcl[(long)pos * 128 + lane + 64] = v2;
                 }
             }
+            mark(2);
             px_sync();
+            // Causal attention of the group's two query heads over this block's
+            // positions (qwen_causal_attention_heads, qwen_asr_kernels.c:1050-1097):
+            // each 16-lane group folds every NG-th position into its online softmax,
+            // then the NG groups merge in LDS.
             if (sp.active) {
                 float q[2][8];
 #pragma unroll
@@ -645,12 +690,12 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
 #pragma unroll
                     for (int j = 0; j < 8; j++) o[h][j] = 0.f;
                 // the first AB positions of each group were DMA'd into LDS by this wave
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                px_wait_loads();
 #pragma unroll
                 for (int j = 0; j < AB; j++)
                     if (sp.s0 + gid + NG * j < sp.cend)
-                        px_fold(q, px_u2f(S.kvb[wave][j][0][lane]), px_u2f(S.kvb[wave][j][1][lane]),
-                                px_u2f(S.kvb[wave][j][2][lane]), px_u2f(S.kvb[wave][j][3][lane]), a.scale, m, lsum, o);
+                        px_fold(q, px_u2f(kvb[wave][j][0][lane]), px_u2f(kvb[wave][j][1][lane]),
+                                px_u2f(kvb[wave][j][2][lane]), px_u2f(kvb[wave][j][3][lane]), a.scale, m, lsum, o);
                 // longer splits continue in register batches
                 for (int pb = sp.s0 + gid + NG * AB; pb < sp.cend; pb += NG * AB) {
                     PxKv<AB> kv;
@@ -659,11 +704,12 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     for (int j = 0; j < AB; j++)
                         if (pb + NG * j < sp.cend) px_fold(q, kv.k[j][0], kv.k[j][1], kv.v[j][0], kv.v[j][1], a.scale, m, lsum, o);
                 }
-                if (sp.last && gid == 0) {
+                if (sp.last && gid == 0) {   // position pos: this step's k/v
                     const float4 *kn = reinterpret_cast<const float4 *>(&S.kr[gl * 8]);
                     const float4 *vn = reinterpret_cast<const float4 *>(&S.vr[gl * 8]);
                     px_fold(q, kn[0], kn[1], vn[0], vn[1], a.scale, m, lsum, o);
                 }
+                mark(3);
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
                     if (gl == 0) { S.sm_m[gid][h] = m[h]; S.sm_l[gid][h] = lsum[h]; }
@@ -675,8 +721,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             if (sp.active && tid < 256) {
                 const int h = tid >> 7, d = tid & 127;
                 float M = -INFINITY;
+#pragma unroll
                 for (int i = 0; i < NG; i++) M = fmaxf(M, S.sm_m[i][h]);
                 float Lh = 0.0f, acc = 0.0f;
+#pragma unroll
                 for (int i = 0; i < NG; i++) {
                     const float mi = S.sm_m[i][h];
                     const float e = (mi == -INFINITY) ? 0.0f : __expf(mi - M);
@@ -693,7 +741,8 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             // The K/V row stored at pos is read by other blocks of this XCD in
             // later steps; retire the stores before this wave writes anything
             // those blocks can depend on.
-            if (sp.last && (wave == 2 || wave == 3)) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (sp.last && (wave == 2 || wave == 3)) px_wait_loads();
+            mark(4);
             if (DEEP) wf.load(Wf(l), H, wave, lane);
 
             // ---- O: merge the splits, then this block's rows of W_o over the group's columns ----
@@ -701,22 +750,42 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             px_sync();
             if (S.abort_) return;
             if (tid < 256) {
+                // online merge over chunks of 8 splits; a chunk's LDS reads are
+                // issued together (one latency per chunk, not per split)
                 const int h = tid >> 7, d = tid & 127;
-                float M = -INFINITY;
-                for (int i = 0; i < sp.nsplit; i++) M = fmaxf(M, S.part[i * QK_PX_PART + h * 130]);
-                float Lh = 0.0f, acc = 0.0f;
-                for (int i = 0; i < sp.nsplit; i++) {
-                    const float *pp = S.part + i * QK_PX_PART + h * 130;
-                    const float e = (pp[0] == -INFINITY) ? 0.0f : __expf(pp[0] - M);
-                    Lh = fmaf(pp[1], e, Lh);
-                    acc = fmaf(pp[2 + d], e, acc);
+                float M = -INFINITY, Lh = 0.0f, acc = 0.0f;
+                for (int c0 = 0; c0 < sp.nsplit; c0 += 8) {
+                    float mv[8], lv[8], ov[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const bool in = c0 + j < sp.nsplit;
+                        const float *pp = S.part + (in ? c0 + j : 0) * QK_PX_PART + h * 130;
+                        mv[j] = in ? pp[0] : -INFINITY;
+                        lv[j] = in ? pp[1] : 0.0f;
+                        ov[j] = in ? pp[2 + d] : 0.0f;
+                    }
+                    float Mc = M;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) Mc = fmaxf(Mc, mv[j]);
+                    const float sc = (M == -INFINITY) ? 0.0f : __expf(M - Mc);
+                    Lh *= sc;
+                    acc *= sc;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float e = (mv[j] == -INFINITY) ? 0.0f : __expf(mv[j] - Mc);
+                        Lh = fmaf(lv[j], e, Lh);
+                        acc = fmaf(ov[j], e, acc);
+                    }
+                    M = Mc;
                 }
                 S.att[h * 128 + d] = acc * (1.0f / Lh);   // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
             }
+            mark(5);
             px_sync();
             {
                 float y[SO / 2 / NCW];
                 wo.dot(S.att, y, lane);
+                mark(6);
                 if ((lane & 31) == 0) {
                     u64 *dst = a.xo + (par * WG + g) * H + SO * r;
 #pragma unroll
@@ -725,10 +794,11 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             }
             if (DEEP) {
                 wd.load(Wd(l), I, wave, lane);
-                if (l + 1 < L) wq.load(Wq(l + 1), H, wave, lane);
+                wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
             } else {
                 wf.load(Wf(l), H, wave, lane);
             }
+            mark(7);
 
             // ---- F: gate|up rows of the group + SwiGLU (qwen_asr_decoder.c:463-466) ----
             px_sync();
@@ -737,6 +807,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             {
                 float y[RF / NCW];
                 wf.dot(S.xn, y, lane);
+                mark(8);
                 if (lane == 0) {
                     u64 *dst = a.xh + (par * WG + g) * HG + (RF / 2) * r;
 #pragma unroll
@@ -745,10 +816,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 }
             }
             if (DEEP) {
-                if (l + 1 < L) wo.load(Wo(l + 1), PX_QD, wave, lane);
+                wo.load(Wo(l + 1 < L ? l + 1 : 0), PX_QD, wave, lane);
             } else {
                 wd.load(Wd(l), I, wave, lane);
-                if (l + 1 < L) wq.load(Wq(l + 1), H, wave, lane);
+                wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
             }
 
             // ---- D: this block's rows of W_down over the group's columns (:467-468) ----
@@ -758,15 +829,18 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             {
                 float y[SO / 4 / NCW];
                 wd.dot(S.hs, y, lane);
+                mark(9);
                 if ((lane & 15) == 0) {
                     u64 *dst = a.xd + (par * WG + g) * H + SO * r;
 #pragma unroll
                     for (int i = 0; i < SO / 4 / NCW; i++) px_put_global(dst + SlabD::row(wave, i, lane), y[i], T + 5u);
                 }
             }
-            if (l + 1 < L) {
-                if (!DEEP) wo.load(Wo(l + 1), PX_QD, wave, lane);
-                if (sp.active) px_kv_dma<AB>(S.kvb[wave], Kc(l + 1), Vc(l + 1), gl, sp.s0 + gid, NG, sp.cend);
+            {   // the next layer's operands (after the last layer: layer 0 of the next step)
+                const int ln = l + 1 < L ? l + 1 : 0;
+                const PxSplit sn(l + 1 < L ? pos : pos + 1, r);
+                if (!DEEP) wo.load(Wo(ln), PX_QD, wave, lane);
+                px_kv_dma<AB>(kvb[wave], Kc(ln), Vc(ln), gl, sn.s0 + gid, NG, sn.cend, sn.active);
             }
         }
         // the first LM-head rows, issued before the final hand-over
@@ -838,15 +912,9 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             int bi = S.wi[0];
             for (int w = 1; w < NCW; w++)
                 if (argmax_better(S.wv[w], S.wi[w], bv, bi)) { bv = S.wv[w]; bi = S.wi[w]; }
-            const unsigned Tc = tstep + 7u * (unsigned)L;
+            const unsigned Tc = tstep + QK_PX_TPL * (unsigned)L;
             px_put_global(a.xc + b, bv, Tc);
             px_put_global(a.xc + QK_PX_BLOCKS + b, __int_as_float(bi), Tc);
-        }
-        if (s + 1 < a.n_steps) {   // next step's layer-0 operands
-            const PxSplit sn(pos + 1, r);
-            wq.load(Wq(0), H, wave, lane);
-            wo.load(Wo(0), PX_QD, wave, lane);
-            if (sn.active) px_kv_dma<AB>(S.kvb[wave], Kc(0), Vc(0), gl, sn.s0 + gid, NG, sn.cend);
         }
         // ---- T: the sync wave reduces the candidates ----
         px_sync();
@@ -858,9 +926,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
 template <int H, int I, int NCW>
 __global__ __launch_bounds__((NCW + 1) * 64, 1) void px_decode(qk_persist_args a) {
     __shared__ __attribute__((aligned(16))) PxShared<H, I, NCW> S;
+    __shared__ __attribute__((aligned(16))) PxKvLds<NCW> kvb;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (wave == NCW) px_sync_role<H, I, NCW>(a, S, lane);
-    else px_compute_role<H, I, NCW>(a, S, wave, lane);
+    else px_compute_role<H, I, NCW>(a, S, kvb, wave, lane);
 }
 
 // 0.6B: hidden 1024, intermediate 3072, 4 compute waves; 1.7B: 2048 / 6144, 8.
@@ -889,6 +958,9 @@ extern "C" int qk_persist_launch(const qk_persist_args *a, int hidden, int inter
     int threads = 0;
     const void *k = px_kernel(hidden, inter, &threads);
     if (!a || !k || a->n_steps <= 0 || a->layers <= 0 || a->epoch == 0u) return QWEN_HIP_EINVAL;
+    if (a->trace && (10 * a->layers + 4 > QK_PX_TRACE_CW || QK_PX_TRACE_CW + 10 * a->layers > QK_PX_TRACE_XU ||
+                     QK_PX_TRACE_XU + 2 * a->layers + 1 > QK_PX_TRACE))
+        return QWEN_HIP_EINVAL;
     if (a->first_tok < 0 && !a->x_in) return QWEN_HIP_EINVAL;
     if (a->first_tok >= a->vocab || a->pos0 < 0 || a->pos0 + a->n_steps > a->cap) return QWEN_HIP_EINVAL;
     qk_persist_args copy = *a;

@@ -135,6 +135,7 @@ int qk_attn_merge_launch(const qk_attn_fused_args *a, hipStream_t s);
 #define QK_PX_MAX_SPLIT 32                 /* attention splits per kv head (one per CU) */
 #define QK_PX_PART 260                     /* words per split: 2 heads x (m, l, o[128]) */
 #define QK_PX_MIN_CHUNK 64                 /* positions per split, at least */
+#define QK_PX_TPL 7                        /* exchange tags per layer */
 enum { QK_PX_ERR_LAYOUT = 1, QK_PX_ERR_TIMEOUT = 2 };
 
 typedef struct {
@@ -171,10 +172,26 @@ typedef struct {
     int *pos_out;              /* position after the last step (= pos0 + n_steps) */
     float *hidden_out;         /* final-normed hidden row of each step */
     float *logits;             /* optional [vocab] logits of each step */
+    unsigned long long *trace; /* optional [256][QK_PX_TRACE] wall-clock stamps of step trace_step */
+    int trace_step;
 } qk_persist_args;
 
+/* Trace points per block (100 MHz wall clock).  Sync wave, per layer l at
+ * 10*l + {0: Q entered (previous compute done), 1: Q input ready, 2: A entered,
+ * 3: A input ready, 4: O entered, 5: O input ready, 6: F entered, 7: F input
+ * ready, 8: D entered, 9: D input ready}; then 10*L + {0: LM entered, 1: LM
+ * input ready, 2: token reduce entered, 3: token ready}.  Compute wave 0 at
+ * QK_PX_TRACE_CW + 10*l + {0: Q dot done, 1: Q stores + prefetch issued,
+ * 2: q/k norm done, 3: fold done, 4: split merged + stored, 5: O splits merged,
+ * 6: O dot done, 7: O stores + prefetch issued, 8: F dot done, 9: D dot done}.
+ * Sync wave again at QK_PX_TRACE_XU + 2*l + {0: cross-XCD half of the residual
+ * update before Q done, 1: the same before F}, and 2*L for the final one. */
+#define QK_PX_TRACE_CW 320
+#define QK_PX_TRACE_XU 640
+#define QK_PX_TRACE 704
+
 /* tags one launch of n steps consumes (the host advances epoch by this) */
-#define QK_PX_TAGS(layers, n) (1u + (unsigned)(n) * (7u * (unsigned)(layers) + 1u))
+#define QK_PX_TAGS(layers, n) (1u + (unsigned)(n) * (QK_PX_TPL * (unsigned)(layers) + 1u))
 
 /* 1 if the persistent engine supports this shape on this device */
 int qk_persist_supported(int hidden, int inter, int heads, int kv_heads, int device);
