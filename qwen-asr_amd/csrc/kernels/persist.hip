@@ -270,11 +270,20 @@ struct PxShared {
     static constexpr int NG = NCW * 4;          // 16-lane attention groups
     float xs[H];                                // residual (kept identical in every block)
     float xn[H];                                // normed input of Q / F / LM head
+    float nw[H];                                // norm weight of the pending RMSNorm (sync wave)
     float qkv[512];                             // raw q|q|k|v of the group
     float qr[2][128], kr[128], vr[128];         // normed + rotated q, k; v
-    float sm_m[NG][2], sm_l[NG][2];             // per 16-lane group: running max / sum
-    float sm_o[NG][2][128];                     // ... and output
-    float part[QK_PX_MAX_SPLIT * QK_PX_PART];   // split partials of the group
+
+    // attention scratch: the 16-lane groups' (max, sum, output) while the split
+    // is folded (stage A), then the group's split partials polled for the merge
+    // (stage O); the stages are barrier-separated, so they share storage
+    union {
+        struct {
+            float sm_m[NG][2], sm_l[NG][2];
+            float sm_o[NG][2][128];
+        };
+        float part[QK_PX_MAX_SPLIT * QK_PX_PART];
+    };
     float att[256];                             // merged attention output of the group
     float hs[HG];                               // SwiGLU outputs of the group
     float ysum[8 * SO];                         // split-K partial slices
@@ -316,28 +325,33 @@ __device__ bool px_x_update(const qk_persist_args &a, PxShared<H, I, NCW> &S, co
     }
     // the XCD's whole new residual
     auto whole = [&](int i) { return xl + i; };
-    return px_poll<H / 64>(whole, H, tx, S.xs, a.err, lane);
+    return px_poll<(H / 64 < 16 ? H / 64 : 16)>(whole, H, tx, S.xs, a.err, lane);
 }
 
-// xn = rms_norm(xs) * w (qwen_rms_norm, qwen_asr_kernels.c:750-809); w already in registers
+// xn = rms_norm(xs) * w (qwen_rms_norm, qwen_asr_kernels.c:750-809); w was
+// DMA'd into LDS by px_load_norm and has landed (the caller's polls waited
+// for every load of this wave).
 template <int H, int I, int NCW>
-__device__ void px_rmsnorm(const qk_persist_args &a, PxShared<H, I, NCW> &S, const float (&w)[H / 64], int lane) {
-    float v[H / 64], ss = 0.0f;
+__device__ void px_rmsnorm(const qk_persist_args &a, PxShared<H, I, NCW> &S, const float *w, int lane) {
+    float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < H / 64; j++) {
-        v[j] = S.xs[j * 64 + lane];
-        ss = fmaf(v[j], v[j], ss);
+        const float v = S.xs[j * 64 + lane];
+        ss = fmaf(v, v, ss);
     }
     ss = wave_sum(ss);
     const float rinv = 1.0f / sqrtf(ss / (float)H + a.eps);
 #pragma unroll
-    for (int j = 0; j < H / 64; j++) S.xn[j * 64 + lane] = (v[j] * w[j]) * rinv;
+    for (int j = 0; j < H / 64; j++) S.xn[j * 64 + lane] = (S.xs[j * 64 + lane] * w[j * 64 + lane]) * rinv;
 }
 
+// Start the DMA of a norm weight vector [H] into LDS (no registers held while
+// the sync wave polls).
 template <int H>
-__device__ __forceinline__ void px_load_norm(const float *p, float (&w)[H / 64], int lane) {
+__device__ __forceinline__ void px_load_norm(const float *p, float *dst, int lane) {
 #pragma unroll
-    for (int j = 0; j < H / 64; j++) w[j] = p[j * 64 + lane];
+    for (int j = 0; j < H / 256; j++)
+        __builtin_amdgcn_global_load_lds(p + j * 256 + lane * 4, dst + j * 256, 16, 0, 0);
 }
 
 template <int H, int I, int NCW>
@@ -345,7 +359,6 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
     constexpr int HG = PxShared<H, I, NCW>::HG;
     const int L = a.layers, b = blockIdx.x;
     const long WG = (long)QK_PX_XCD;
-    float nw[H / 64];
 
     // ---- launch check-in: every block must sit on XCD g < 8 with rank < 32 ----
     px_sync();
@@ -380,7 +393,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             const char *lb = px_layer<H>(a, l);
             bool ok = true;
             // ---- Q: input (embedding / x_in) or x += down partials; input norm ----
-            px_load_norm<H>((const float *)(lb + a.off_nin), nw, lane);
+            px_load_norm<H>((const float *)(lb + a.off_nin), S.nw, lane);
             px_sync();
             mark(10 * l + 0);
             if (l == 0) {
@@ -403,7 +416,10 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
                 ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T - QK_PX_TPL + 5u, a.xlb + (pp * WG + g) * H,
                                             T - QK_PX_TPL + 6u, lane, tr ? tr + QK_PX_TRACE_XU + 2 * l : nullptr);
             }
-            if (ok) px_rmsnorm<H, I, NCW>(a, S, nw, lane);
+            if (ok) {
+                px_wait_loads();
+                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane);
+            }
             mark(10 * l + 1);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
@@ -431,7 +447,8 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
                 const PxSplit sp(pos, 0);
                 const u64 *src = a.xa + (par * WG + g) * (long)(QK_PX_MAX_SPLIT * QK_PX_PART);
                 auto addr = [&](int i) { return src + i; };
-                ok = px_poll<33>(addr, sp.nsplit * QK_PX_PART, T + 1u, S.part, a.err, lane);
+                // words per lane in flight: the 1.7B kernel has fewer registers per wave
+                ok = px_poll<(NCW == 4 ? 33 : 17)>(addr, sp.nsplit * QK_PX_PART, T + 1u, S.part, a.err, lane);
             }
             mark(10 * l + 5);
             if (lane == 0) S.abort_ = !ok;
@@ -440,12 +457,15 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             px_sync();   // after the merge
 
             // ---- F: x += O partials; post-attention norm ----
-            px_load_norm<H>((const float *)(lb + a.off_npost), nw, lane);
+            px_load_norm<H>((const float *)(lb + a.off_npost), S.nw, lane);
             px_sync();
             mark(10 * l + 6);
             ok = px_x_update<H, I, NCW>(a, S, a.xo + (par * WG) * H, T + 2u, a.xla + (par * WG + g) * H, T + 3u, lane,
                                         tr ? tr + QK_PX_TRACE_XU + 2 * l + 1 : nullptr);
-            if (ok) px_rmsnorm<H, I, NCW>(a, S, nw, lane);
+            if (ok) {
+                px_wait_loads();
+                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane);
+            }
             mark(10 * l + 7);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
@@ -468,13 +488,14 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
         {
             const unsigned T = tstep + QK_PX_TPL * (unsigned)(L - 1);
             const int pp = (L - 1) & 1;
-            px_load_norm<H>(a.fnorm, nw, lane);
+            px_load_norm<H>(a.fnorm, S.nw, lane);
             px_sync();
             mark(10 * L + 0);
             bool ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T + 5u, a.xlb + (pp * WG + g) * H, T + 6u, lane,
                                              tr ? tr + QK_PX_TRACE_XU + 2 * L : nullptr);
             if (ok) {
-                px_rmsnorm<H, I, NCW>(a, S, nw, lane);
+                px_wait_loads();
+                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane);
                 if (b == 0 && a.hidden_out)
                     for (int i = lane; i < H; i += 64) a.hidden_out[i] = S.xn[i];
             }
