@@ -40,7 +40,11 @@ WORKLOADS = {
                desc="C3 Qwen3-ASR-1.7B decoder: 1500 audio rows + 16 ids, prefill 1515, greedy decode"),
     "c4": dict(model_b=0, n_audio=8192, n_ids=0,
                desc="C4 0.6B long context: prefill 8191 audio rows, greedy decode over up to 8.7k positions"),
+    "c5": dict(model_b=0, n_audio=26, n_ids=9,
+               desc="C5 0.6B streaming: 60 chunks x (roll back 5 tokens, prefill 5 token + 26 audio rows, "
+                    "24 greedy forwards), KV window capped at 1024 positions"),
 }
+C5_CHUNKS, C5_AUDIO, C5_ROLLBACK, C5_STEPS, C5_CAP, C5_HEAD, C5_KEEP = 60, 26, 5, 24, 1024, 9, 3
 HBM_PEAK_GBS = 8000.0
 
 
@@ -48,20 +52,24 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-DECODE_KERNELS = ("gemv_kernel", "attn_decode_fused", "attn_merge", "argmax_finish")
+GRAPH_KERNELS = ("gemv_kernel", "attn_decode_fused", "attn_merge", "argmax_finish")
+PMC_STEPS = 16
 
 
 def pmc_pass(counter, workload, timeout=150):
     """One child run of this script under rocprofv3 --pmc <counter>: a short
-    decode (plus a 256 MiB calibration copy kernel).  Returns (KiB per decode
-    step summed over the step's kernels, calibration factor), or None."""
+    decode of PMC_STEPS steps (plus a 256 MiB calibration copy kernel).
+    Returns (KiB per decode step, calibration factor), or None.  Persistent
+    engine: the counter of the last px_decode dispatch (the timed launch of
+    PMC_STEPS steps) / PMC_STEPS.  Graph engine: the step's kernels summed,
+    per argmax_finish."""
     exe = shutil.which("rocprofv3")
     if not exe:
         return None
     out = tempfile.mkdtemp(prefix="qk_pmc_")
     cmd = [exe, "--pmc", counter, "-d", out, "-o", "run", "--output-format", "csv", "--",
-           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--steps", "16", "--warmup", "2",
-           "--calib-copy-mb", "256", "--workload", workload]
+           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--steps", str(PMC_STEPS),
+           "--warmup", "2", "--calib-copy-mb", "256", "--workload", workload]
     env = dict(os.environ, TMPDIR="/tmp")
     try:
         subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
@@ -69,22 +77,65 @@ def pmc_pass(counter, workload, timeout=150):
         files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
         if not files:
             return None
-        total, steps, cal = 0.0, 0, None
+        per_dispatch, names, cal = {}, {}, None
         for r in csv.DictReader(open(files[0])):
             name, v = r["Kernel_Name"], float(r["Counter_Value"])
+            did = int(r.get("Dispatch_Id", len(per_dispatch)))
             if "AUnaryFunctor" in name:
-                cal = v
-            elif any(k in name for k in DECODE_KERNELS):
-                total += v
-                steps += "argmax_finish" in name
-        if not steps or not cal:
+                cal = v if cal is None else cal + v
+                continue
+            per_dispatch[did] = per_dispatch.get(did, 0.0) + v
+            names[did] = name
+        if not cal:
             return None
         factor = 256 * 1024 / cal
+        px = sorted(d for d, n in names.items() if "px_decode" in n)
+        if px:
+            return per_dispatch[px[-1]] / PMC_STEPS * factor, factor
+        total = sum(v for d, v in per_dispatch.items() if any(k in names[d] for k in GRAPH_KERNELS))
+        steps = sum(1 for n in names.values() if "argmax_finish" in n)
+        if not steps:
+            return None
         return total / steps * factor, factor
     except (subprocess.SubprocessError, OSError, KeyError, ValueError):
         return None
     finally:
         shutil.rmtree(out, ignore_errors=True)
+
+
+def run_streaming(qa, d, cfg, chunks):
+    """The C5 op pattern (the reference's streaming KV reuse, qwen_asr.c:1748-1829):
+    a 9-row template head, then per chunk: roll the KV back by the last 5
+    decoded tokens (set_kv_len), prefill their embeddings + the chunk's 26
+    audio rows, forward the last row and generate 23 more tokens greedily.
+    When the next chunk would pass 1024 positions, keep the template head and
+    re-prefill the audio of the last 3 chunks.  Returns (tokens of every
+    chunk, seconds per chunk)."""
+    import numpy as np
+    import torch
+    emb = qa.synth_bf16(cfg.vocab * cfg.hidden, 0, qa.SYNTH_EMBED).reshape(cfg.vocab, cfg.hidden)
+    head, _, _ = qa.prompt_rows(cfg, 0, C5_HEAD, emb=emb)
+    audio = [qa.prompt_rows(cfg, C5_AUDIO, 0, audio_chunk=c, emb=emb)[0] for c in range(chunks)]
+    e = lambda t: qa.bf16_to_f32(emb[np.asarray(t)]).reshape(-1, cfg.hidden)
+    d.set_kv_len(0)
+    d.prefill(head)
+    out, times, prev = [], [], []
+    for c in range(chunks):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        if prev:
+            d.set_kv_len(d.kv_len() - C5_ROLLBACK)
+        if d.kv_len() + C5_ROLLBACK + C5_AUDIO + C5_STEPS > C5_CAP:
+            d.set_kv_len(C5_HEAD)
+            d.prefill(np.concatenate(audio[max(0, c - C5_KEEP):c]))
+        rows = np.concatenate([e(prev[-C5_ROLLBACK:]), audio[c]]) if prev else audio[c]
+        d.prefill(rows[:-1])
+        first = d.forward(rows[-1])
+        toks = [first] + list(d.generate(first, C5_STEPS - 1))
+        times.append(time.perf_counter() - t0)
+        out.append(toks)
+        prev = toks
+    return out, times
 
 
 def cpu_baseline(wl, rows, first_token, threads, decode_steps):
@@ -108,6 +159,19 @@ def cpu_baseline(wl, rows, first_token, threads, decode_steps):
             "sample": f"reference decoder (oracle/_ref, no BLAS) on the same weights/rows: prefill "
                       f"{rows.shape[0] - 1} rows, then {decode_steps} greedy decode steps; decode tok/s over those steps",
             "first_token_matches_gpu": bool(tok == first_token)}
+
+
+def launch_fields(engine, K, step_bytes, gpu_ms):
+    """What one launch of the dominant kernel is: the persistent engine runs the
+    K timed steps in one px_decode dispatch; the graph engine replays one graph
+    (per-layer GEMV/attention kernels + LM head argmax) per step."""
+    if engine == 2:
+        return {"kernel": f"px_decode (persistent cooperative kernel: {K} greedy decode steps per launch)",
+                "steps_per_launch": K, "bytes_per_launch": round(sum(step_bytes)),
+                "launch_us": round(gpu_ms * 1e3, 3), "step_us": round(gpu_ms * 1e3 / K, 3)}
+    return {"kernel": "decode step graph (one token: all layers + LM head argmax)", "steps_per_launch": 1,
+            "bytes_per_launch": round(sum(step_bytes) / K), "launch_us": round(gpu_ms * 1e3 / K, 3),
+            "step_us": round(gpu_ms * 1e3 / K, 3)}
 
 
 def main():
@@ -135,6 +199,26 @@ def main():
     qa = importlib.import_module("qwen-asr_amd")
     wl = WORKLOADS[args.workload]
     cfg = qa.preset(wl["model_b"])
+    if args.workload == "c5":
+        d = qa.Decoder(cfg, 0, C5_CAP + 64)
+        if args.engine is not None:
+            d.set_engine(args.engine)
+        d.load_synthetic(0, 0.02, 0.0)
+        run_streaming(qa, d, cfg, 2)                      # warm-up
+        toks, times = run_streaming(qa, d, cfg, C5_CHUNKS)
+        total = sum(times)
+        value = C5_CHUNKS * C5_STEPS / total
+        log(f"[gpu] c5: {C5_CHUNKS} chunks in {total * 1e3:.1f} ms ({total / C5_CHUNKS * 1e3:.3f} ms per chunk, "
+            f"{value:.1f} generated tok/s)")
+        print(json.dumps({
+            "metric": "streaming chunk latency (C5) and generated tok/s", "value": round(value, 3),
+            "unit": "tok/s", "n_gpus": 1, "steps": C5_CHUNKS, "warmup": 2,
+            "ms_per_step": round(total / C5_CHUNKS * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": wl["desc"], "engine": {0: "graph", 1: "eager", 2: "persistent"}.get(d.engine())},
+            "chunk_ms": {"mean": round(total / C5_CHUNKS * 1e3, 4), "max": round(max(times) * 1e3, 4)},
+            "tokens_head": [int(t) for t in toks[0][:8]]}), flush=True)
+        return
     n_rows = wl["n_audio"] + wl["n_ids"]
     K, W = args.steps, args.warmup
     d = qa.Decoder(cfg, 0, n_rows + K + W + 1024)
@@ -187,14 +271,24 @@ def main():
 
     traffic = None
     traffic_note = None
-    if not args.no_traffic:
+    if d.engine() == 2 and not args.no_traffic:
+        # rocprofv3 --pmc (dispatch counter collection) did not complete on the
+        # cooperative launch of px_decode within 150 s; not run on it again.
+        traffic_note = ("null: rocprofv3 --pmc counter collection does not complete on the cooperative px_decode "
+                        "launch; per-kernel HBM traffic of the same step is measured on the graph engine "
+                        "(bench.py --engine 0)")
+        log("[gpu] traffic passes skipped for the persistent engine (counter collection on a cooperative launch)")
+    elif not args.no_traffic:
         fr = pmc_pass("FETCH_SIZE", args.workload)
         wr = pmc_pass("WRITE_SIZE", args.workload)
         if fr and wr:
-            traffic = round((fr[0] + wr[0]) * 1024)
-            traffic_note = (f"per decode step at positions {n_rows}-{n_rows + 17}: FETCH_SIZE x {fr[1]:.4f} + "
+            per_step = (fr[0] + wr[0]) * 1024
+            per_launch = K if d.engine() == 2 else 1
+            traffic = round(per_step * per_launch)
+            traffic_note = (f"per launch = {per_launch} x the per-step HBM bytes measured over {PMC_STEPS} decode "
+                            f"steps at positions {n_rows}-{n_rows + PMC_STEPS + 1}: FETCH_SIZE x {fr[1]:.4f} + "
                             f"WRITE_SIZE x {wr[1]:.4f} (factors from a 256 MiB copy kernel)")
-            log(f"[gpu] traffic per step {traffic / 1e6:.1f} MB ({traffic / avg_bytes:.3f} x algorithmic)")
+            log(f"[gpu] traffic per step {per_step / 1e6:.1f} MB ({per_step / avg_bytes:.3f} x algorithmic)")
         else:
             log("[gpu] rocprofv3 traffic passes unavailable: traffic null")
 
@@ -215,8 +309,7 @@ def main():
         "prefill_tok_s": round((n_rows - 1) / prefill_s, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
-                     "kernel": "decode step (one token: all layers + LM head argmax)",
-                     "bytes_per_launch": round(avg_bytes), "launch_us": round(gpu_ms * 1e3 / K, 3)},
+                     **launch_fields(d.engine(), K, step_bytes, gpu_ms)},
         "cpu_baseline": cpu,
         "tokens_head": [int(first)] + [int(t) for t in toks[:7]],
     }

@@ -191,3 +191,61 @@ def test_engine_errors(qa, gpu):
         d.set_engine(3)
     assert d.engine() == ENGINE_GRAPH
     d.close()
+
+
+def test_streaming_rollback_pattern(qa, dec06):
+    """The streaming op pattern (qwen_asr.c:1748-1829): per chunk roll the KV
+    back by the last 5 decoded tokens, prefill their embeddings + 26 new audio
+    rows, decode; when the window would pass its cap, keep the 9-row head and
+    re-prefill recent audio.  The persistent engine is teacher-forced with the
+    graph engine's tokens and their logits compared step by step."""
+    d, _ = dec06
+    cfg = qa.preset(0)
+    emb = qa.synth_bf16(cfg.vocab * cfg.hidden, 0, qa.SYNTH_EMBED).reshape(cfg.vocab, cfg.hidden)
+    head, _, _ = qa.prompt_rows(cfg, 0, 9, emb=emb)
+    audio = [qa.prompt_rows(cfg, 26, 0, audio_chunk=c, emb=emb)[0] for c in range(5)]
+    cap, n_dec = 160, 10
+
+    def stream(engine, forced=None):
+        d.set_engine(engine)
+        d.set_keep_logits(True)
+        d.set_kv_len(0)
+        d.prefill(head)
+        toks, logits, prev, resets = [], [], [], 0
+        for c in range(len(audio)):
+            if prev:
+                d.set_kv_len(d.kv_len() - 5)
+            if d.kv_len() + 5 + 26 + n_dec > cap:
+                d.set_kv_len(9)
+                d.prefill(np.concatenate(audio[max(0, c - 2):c]))
+                resets += 1
+            rows = audio[c]
+            if prev:
+                rows = np.concatenate([qa.bf16_to_f32(emb[prev[-5:]]).reshape(-1, cfg.hidden), rows])
+            d.prefill(rows[:-1])
+            chunk = []
+            for i in range(n_dec):
+                if i == 0:
+                    t = d.forward(rows[-1])
+                else:
+                    t = d.forward_token(forced[c][i - 1] if forced else chunk[-1])
+                chunk.append(t)
+                logits.append(d.read_logits())
+            toks.append(chunk)
+            prev = forced[c] if forced else chunk
+        d.set_keep_logits(False)
+        return toks, np.array(logits), resets
+
+    tg, lg, resets = stream(ENGINE_GRAPH)
+    tp, lp, _ = stream(ENGINE_PERSIST, forced=tg)
+    assert resets >= 1, "the window reset path was not exercised"
+    assert d.engine() == ENGINE_PERSIST
+    err = float(np.abs(lp - lg).max())
+    print(f"streaming, {len(audio)} chunks x {n_dec} steps, {resets} window reset(s): max |dlogit| {err:.2e}")
+    assert err < AGREE, err
+    flat_g = [t for c in tg for t in c]
+    flat_p = [t for c in tp for t in c]
+    for i, (a, b) in enumerate(zip(flat_g, flat_p)):
+        if a != b:
+            s = np.sort(lg[i])
+            assert s[-1] - s[-2] < TIE, (i, a, b)
