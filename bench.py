@@ -36,9 +36,12 @@ sys.path.insert(0, ROOT)
 WORKLOADS = {
     "c1": dict(model_b=0, n_audio=390, n_ids=12,
                desc="C1 Qwen3-ASR-0.6B decoder token loop: 390 audio rows + 12 ids, prefill 401, greedy decode"),
-    "c3": dict(model_b=1, n_audio=1500, n_ids=16,
+    "c2": dict(model_b=0, n_audio=0, n_ids=0,
+               desc="C2 bf16-weight GEMV sweep with fp32 x (op-level qwen_hip_linear_nobias_bf16, seq 1), "
+                    "cold weights (rotation over >= 1 GiB of copies)"),
+    "c3": dict(model_b=1, n_audio=1500, n_ids=16, steps=256,
                desc="C3 Qwen3-ASR-1.7B decoder: 1500 audio rows + 16 ids, prefill 1515, greedy decode"),
-    "c4": dict(model_b=0, n_audio=8192, n_ids=0,
+    "c4": dict(model_b=0, n_audio=8192, n_ids=0, steps=512,
                desc="C4 0.6B long context: prefill 8191 audio rows, greedy decode over up to 8.7k positions"),
     "c5": dict(model_b=0, n_audio=26, n_ids=9,
                desc="C5 0.6B streaming: 60 chunks x (roll back 5 tokens, prefill 5 token + 26 audio rows, "
@@ -101,6 +104,76 @@ def pmc_pass(counter, workload, timeout=150):
         return None
     finally:
         shutil.rmtree(out, ignore_errors=True)
+
+
+C2_SHAPES = [(2048, 1024), (1024, 2048), (6144, 1024), (1024, 3072), (151936, 1024), (4096, 2048),
+             (2048, 4096), (12288, 2048), (2048, 6144), (151936, 2048), (2048, 2048)]
+
+
+def run_gemv_sweep(qa, threads, with_cpu):
+    """C2: y = W x for each (rows, cols), W bf16 N(0, 0.02), x U[-1, 1].  GPU:
+    the op-level GEMV (qwen_hip_linear_nobias_bf16 at seq 1, the reference's
+    qwen_linear_nobias_bf16 decode path, qwen_asr_kernels.c:462-466), timed
+    with HIP events over launches that rotate through >= 4 copies of W
+    spanning >= 1 GiB, so each launch streams its weights from HBM, not from
+    the 256 MB last-level cache.  Bytes per launch 2RC + 4C + 4R.  CPU: the
+    reference's own qwen_linear_nobias_bf16 (oracle/_ref) on `threads`
+    threads, same W and x."""
+    import numpy as np
+    import torch
+    out = []
+    ref = None
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pyoracle as P
+        ref = P.ref_lib() if P.ref_available() else None
+        if ref is not None:
+            ref.ref_set_threads(threads)
+    for R, Cc in C2_SHAPES:
+        W = qa.synth_bf16(R * Cc, 0, 9000 + R + Cc).reshape(R, Cc)
+        x = qa.synth_uniform(Cc, 0, 9100 + Cc)
+        wbytes = 2 * R * Cc
+        copies = max(4, -(-(1 << 30) // wbytes))
+        dW0 = torch.from_numpy(W.view(np.int16)).to("cuda")
+        dWs = [dW0] + [dW0.clone() for _ in range(copies - 1)]
+        dx = torch.from_numpy(x).to("cuda")
+        dy = torch.empty(R, dtype=torch.float32, device="cuda")
+        lib = qa.lib()
+        call = lambda w: lib.qwen_hip_linear_nobias_bf16(dy.data_ptr(), dx.data_ptr(), w.data_ptr(), 1, Cc, R, None)
+        for i in range(copies):
+            qa.check(call(dWs[i]), "gemv")
+        reps = max(copies * 4, min(400, int(4e9 // wbytes)))
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps):
+            call(dWs[i % copies])
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = wbytes + 4 * Cc + 4 * R
+        gbs = nbytes / (us * 1e-6) / 1e9
+        row = {"rows": R, "cols": Cc, "bytes": nbytes, "us": round(us, 3), "gb_s": round(gbs, 1),
+               "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+        if ref is not None:
+            yc = np.empty(R, np.float32)
+            Wc = np.ascontiguousarray(W)
+            ref.qwen_linear_nobias_bf16(yc, x, Wc, 1, Cc, R)      # warm (thread pool, pages)
+            n, t0 = 0, time.perf_counter()
+            while n < 3 or time.perf_counter() - t0 < 0.5:
+                ref.qwen_linear_nobias_bf16(yc, x, Wc, 1, Cc, R)
+                n += 1
+            cpu_s = (time.perf_counter() - t0) / n
+            row["cpu_gb_s"] = round(nbytes / cpu_s / 1e9, 2)
+            row["cpu_us"] = round(cpu_s * 1e6, 1)
+            yg = dy.cpu().numpy()
+            row["max_rel_diff_vs_ref"] = float(np.max(np.abs(yg - yc)) / (np.max(np.abs(yc)) + 1e-30))
+        log(f"[gpu] gemv {R}x{Cc}: {us:.2f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)"
+            + (f"; cpu {row['cpu_gb_s']} GB/s" if "cpu_gb_s" in row else ""))
+        out.append(row)
+        del dWs, dW0
+        torch.cuda.empty_cache()
+    return out
 
 
 def run_streaming(qa, d, cfg, chunks):
@@ -177,7 +250,8 @@ def launch_fields(engine, K, step_bytes, gpu_ms):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed decode steps (default: the workload's count, C1 128, C3 256, C4 512)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c1")
     ap.add_argument("--engine", type=int, default=None,
@@ -199,6 +273,30 @@ def main():
     qa = importlib.import_module("qwen-asr_amd")
     wl = WORKLOADS[args.workload]
     cfg = qa.preset(wl["model_b"])
+    if args.workload == "c2":
+        threads = min(os.cpu_count() or 1, 16)
+        rows = run_gemv_sweep(qa, threads, not args.no_cpu)
+        tot_b = sum(r["bytes"] for r in rows)
+        tot_us = sum(r["us"] for r in rows)
+        big = max(rows, key=lambda r: r["bytes"])
+        cpu = None
+        if "cpu_gb_s" in rows[0]:
+            cpu_us = sum(r["cpu_us"] for r in rows)
+            cpu = {"value": round(tot_b / (cpu_us * 1e-6) / 1e9, 2), "unit": "GB/s", "cores": threads,
+                   "kind": "reference",
+                   "sample": "the reference's qwen_linear_nobias_bf16 (oracle/_ref, seq 1 threaded matvec) on "
+                             "each shape, >= 0.5 s per shape; value = all shapes' bytes / summed time"}
+        print(json.dumps({
+            "metric": "bf16 GEMV GB/s (C2 sweep)", "value": round(tot_b / (tot_us * 1e-6) / 1e9, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": len(rows), "warmup": 1,
+            "ms_per_step": round(tot_us / len(rows) / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": wl["desc"]},
+            "roofline": {"bound": "hbm", "achieved": big["gb_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": big["frac"], "traffic": None,
+                         "kernel": f"gemv {big['rows']}x{big['cols']} (largest shape)"},
+            "per_shape": rows, "cpu_baseline": cpu}), flush=True)
+        return
     if args.workload == "c5":
         d = qa.Decoder(cfg, 0, C5_CAP + 64)
         if args.engine is not None:
@@ -220,7 +318,7 @@ def main():
             "tokens_head": [int(t) for t in toks[0][:8]]}), flush=True)
         return
     n_rows = wl["n_audio"] + wl["n_ids"]
-    K, W = args.steps, args.warmup
+    K, W = args.steps or wl.get("steps", 128), args.warmup
     d = qa.Decoder(cfg, 0, n_rows + K + W + 1024)
     if args.engine is not None:
         d.set_engine(args.engine)

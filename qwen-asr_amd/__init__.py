@@ -147,6 +147,12 @@ def synth_f32(n, seed, tensor_id, std=1.0, mean=0.0):
     return out
 
 
+def synth_uniform(n, seed, tensor_id, lo=-1.0, hi=1.0):
+    out = np.empty(n, np.float32)
+    lib().qwen_synth_uniform_f32(_ptr(out), n, seed, tensor_id, lo, hi, 0)
+    return out
+
+
 def synth_tokens(n, seed, tensor_id, n_ids=151643):
     out = np.empty(n, np.int32)
     lib().qwen_synth_tokens(_ptr(out), n, seed, tensor_id, n_ids)
