@@ -100,6 +100,10 @@ struct qwen_hip_decoder {
     /* prefill buffers, sized pref_cap rows */
     int pref_cap;
     float *px, *pqkv, *pqrot;
+    float *pattn;            /* prefill attention split partials */
+    size_t pattn_floats;
+    float *pgemm;            /* prefill split-K GEMM partials */
+    size_t pgemm_floats;
     uint16_t *pxh, *pxl, *pah, *pal, *phh, *phl;
 
     hipGraph_t graph[STEP_VARIANTS];
@@ -363,6 +367,12 @@ static void prefill_free(qwen_hip_decoder *d) {
     d->px = d->pqkv = d->pqrot = NULL;
     d->pxh = d->pxl = d->pah = d->pal = d->phh = d->phl = NULL;
     d->pref_cap = 0;
+    dev_free(d->pattn);
+    d->pattn = NULL;
+    d->pattn_floats = 0;
+    dev_free(d->pgemm);
+    d->pgemm = NULL;
+    d->pgemm_floats = 0;
 }
 
 void qwen_hip_decoder_destroy(qwen_hip_decoder *d) {
@@ -502,26 +512,88 @@ static int prefill_layers(qwen_hip_decoder *d, int S) {
     const qwen_hip_config *c = &d->cfg;
     const int D = c->hidden, I = c->intermediate, hd = c->head_dim, start = d->kv_len;
     hipStream_t s = d->stream;
+    int chunk = 0, nsplit = 0;
+    const size_t pf = qk_attn_prefill_plan(S, start + S, start, c->heads, c->kv_heads, &chunk, &nsplit);
+    /* GEMM tilings; with split-K the partials go to pgemm and their consumer
+     * (RoPE/append, the next RMSNorm, the SwiGLU reduce) sums them in order */
+    qk_gemm_plan gq, go, gg, gd;
+    qk_gemm_plan_for(S, d->qkv_rows, D, &gq);
+    qk_gemm_plan_for(S, D, d->qd, &go);
+    qk_gemm_plan_for(S, 2 * I, D, &gg);
+    qk_gemm_plan_for(S, D, I, &gd);
+    size_t pg = 0;
+    const size_t cand[4] = {gq.nsplit > 1 ? (size_t)gq.nsplit * S * d->qkv_rows : 0,
+                            go.nsplit > 1 ? (size_t)go.nsplit * S * D : 0,
+                            gg.nsplit > 1 ? (size_t)gg.nsplit * S * 2 * I : 0,
+                            gd.nsplit > 1 ? (size_t)gd.nsplit * S * D : 0};
+    for (int i = 0; i < 4; i++) pg = cand[i] > pg ? cand[i] : pg;
+    if (pf > d->pattn_floats || pg > d->pgemm_floats) {
+        QK_HIP(hipStreamSynchronize(s));          /* old buffers may still be in use */
+        if (pf > d->pattn_floats) {
+            dev_free(d->pattn);
+            d->pattn = NULL;
+            d->pattn_floats = 0;
+            QK_TRY(dev_alloc((void **)&d->pattn, pf * sizeof(float)));
+            d->pattn_floats = pf;
+        }
+        if (pg > d->pgemm_floats) {
+            dev_free(d->pgemm);
+            d->pgemm = NULL;
+            d->pgemm_floats = 0;
+            QK_TRY(dev_alloc((void **)&d->pgemm, pg * sizeof(float)));
+            d->pgemm_floats = pg;
+        }
+    }
+    float *const qkv = gq.nsplit > 1 ? d->pgemm : d->pqkv;
+    int pending = 0;                 /* split-K partials of the last down projection not yet in px */
     for (int l = 0; l < c->layers; l++) {
-        QK_TRY(qk_rmsnorm_split_launch(d->px, d->n_in[l], S, D, c->rms_eps, d->pxh, d->pxl, s));
-        QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_qkv[l], S, d->qkv_rows, D, QK_GEMM_STORE, d->pqkv, NULL, NULL, s));
+        /* input RMSNorm (completing the previous layer's residual first) + Q|K|V */
+        QK_TRY(qk_rmsnorm_split_launch(d->px, d->pgemm, pending, (long)S * D, d->n_in[l], S, D, c->rms_eps,
+                                       d->pxh, d->pxl, s));
+        QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_qkv[l], S, d->qkv_rows, D, &gq, QK_GEMM_STORE, qkv, NULL, NULL,
+                              s));
         qk_rope_append_args ra = {
-            .qkv = d->pqkv, .q_norm = d->n_q[l], .k_norm = d->n_k[l], .eps = c->rms_eps,
-            .rope_cos = d->rope_cos, .rope_sin = d->rope_sin, .k_cache = kc_layer(d, l),
-            .v_cache = vc_layer(d, l), .cap = d->kv_cap, .pos_dev = NULL, .start = start, .S = S,
-            .heads = c->heads, .kv_heads = c->kv_heads, .q_out = d->pqrot};
+            .qkv = qkv, .nsum = gq.nsplit, .pstride = (long)S * d->qkv_rows, .q_norm = d->n_q[l],
+            .k_norm = d->n_k[l], .eps = c->rms_eps, .rope_cos = d->rope_cos, .rope_sin = d->rope_sin,
+            .k_cache = kc_layer(d, l), .v_cache = vc_layer(d, l), .cap = d->kv_cap, .pos_dev = NULL,
+            .start = start, .S = S, .heads = c->heads, .kv_heads = c->kv_heads, .q_out = d->pqrot};
         QK_TRY(qk_rope_append_launch(&ra, s));
         qk_attn_args aa = {
             .q = d->pqrot, .k = kc_layer(d, l), .v = vc_layer(d, l), .pos_stride = hd,
             .head_stride = (long)d->kv_cap * hd, .pos_dev = NULL, .seq_k = start + S, .seq_q = S,
             .q_offset = start, .heads = c->heads, .kv_heads = c->kv_heads, .scale = d->scale,
-            .out = NULL, .out_hi = d->pah, .out_lo = d->pal};
+            .part = d->pattn, .nsplit = nsplit, .chunk = chunk, .out = NULL, .out_hi = d->pah, .out_lo = d->pal};
         QK_TRY(qk_attn_prefill_launch(&aa, s));
-        QK_TRY(qk_gemm_launch(d->pah, d->pal, d->w_o[l], S, D, d->qd, QK_GEMM_ADD, d->px, NULL, NULL, s));
-        QK_TRY(qk_rmsnorm_split_launch(d->px, d->n_post[l], S, D, c->rms_eps, d->pxh, d->pxl, s));
-        QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_gu[l], S, 2 * I, D, QK_GEMM_SWIGLU, NULL, d->phh, d->phl, s));
-        QK_TRY(qk_gemm_launch(d->phh, d->phl, d->w_down[l], S, D, I, QK_GEMM_ADD, d->px, NULL, NULL, s));
+        /* O projection + residual, post-attention RMSNorm */
+        if (go.nsplit > 1) {
+            QK_TRY(qk_gemm_launch(d->pah, d->pal, d->w_o[l], S, D, d->qd, &go, QK_GEMM_STORE, d->pgemm, NULL, NULL,
+                                  s));
+            QK_TRY(qk_rmsnorm_split_launch(d->px, d->pgemm, go.nsplit, (long)S * D, d->n_post[l], S, D, c->rms_eps,
+                                           d->pxh, d->pxl, s));
+        } else {
+            QK_TRY(qk_gemm_launch(d->pah, d->pal, d->w_o[l], S, D, d->qd, &go, QK_GEMM_ADD, d->px, NULL, NULL, s));
+            QK_TRY(qk_rmsnorm_split_launch(d->px, NULL, 0, 0, d->n_post[l], S, D, c->rms_eps, d->pxh, d->pxl, s));
+        }
+        /* gate|up + SwiGLU */
+        if (gg.nsplit > 1) {
+            QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_gu[l], S, 2 * I, D, &gg, QK_GEMM_STORE, d->pgemm, NULL, NULL,
+                                  s));
+            QK_TRY(qk_gemm_reduce_launch(d->pgemm, gg.nsplit, S, 2 * I, QK_GEMM_SWIGLU, NULL, d->phh, d->phl, s));
+        } else {
+            QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_gu[l], S, 2 * I, D, &gg, QK_GEMM_SWIGLU, NULL, d->phh, d->phl,
+                                  s));
+        }
+        /* down projection + residual (split-K: completed by the next RMSNorm) */
+        if (gd.nsplit > 1) {
+            QK_TRY(qk_gemm_launch(d->phh, d->phl, d->w_down[l], S, D, I, &gd, QK_GEMM_STORE, d->pgemm, NULL, NULL,
+                                  s));
+            pending = gd.nsplit;
+        } else {
+            QK_TRY(qk_gemm_launch(d->phh, d->phl, d->w_down[l], S, D, I, &gd, QK_GEMM_ADD, d->px, NULL, NULL, s));
+            pending = 0;
+        }
     }
+    if (pending) QK_TRY(qk_gemm_reduce_launch(d->pgemm, pending, S, D, QK_GEMM_ADD, d->px, NULL, NULL, s));
     return 0;
 }
 

@@ -80,10 +80,24 @@ int qwen_hip_linear_nobias_bf16(float *y, const float *x, const uint16_t *W, int
     pthread_mutex_lock(&g_ws_lock);
     void *ws = NULL;
     const size_t n = (size_t)S * in_dim;
-    int rc = workspace(2 * n * sizeof(uint16_t), &ws);
-    if (!rc) rc = qk_split_bf16_launch(x, (long)n, (uint16_t *)ws, (uint16_t *)ws + n, s);
-    if (!rc) rc = qk_gemm_launch((uint16_t *)ws, (uint16_t *)ws + n, W, S, out_dim, in_dim, QK_GEMM_STORE, y,
-                                 NULL, NULL, s);
+    qk_gemm_plan p;
+    qk_gemm_plan_for(S, out_dim, in_dim, &p);
+    if (p.nsplit > 1 && (out_dim & 1)) {              /* the reduce pass works on column pairs */
+        p.kc = ((in_dim + 63) / 64) * 64;
+        p.nsplit = 1;
+    }
+    const size_t part = p.nsplit > 1 ? (size_t)p.nsplit * S * out_dim : 0;
+    const size_t abytes = (2 * n * sizeof(uint16_t) + 255) & ~(size_t)255;
+    int rc = workspace(abytes + part * sizeof(float), &ws);
+    uint16_t *ah = (uint16_t *)ws, *al = ah + n;
+    float *pp = (float *)((char *)ws + abytes);
+    if (!rc) rc = qk_split_bf16_launch(x, (long)n, ah, al, s);
+    if (!rc && p.nsplit > 1) {
+        rc = qk_gemm_launch(ah, al, W, S, out_dim, in_dim, &p, QK_GEMM_STORE, pp, NULL, NULL, s);
+        if (!rc) rc = qk_gemm_reduce_launch(pp, p.nsplit, S, out_dim, QK_GEMM_STORE, y, NULL, NULL, s);
+    } else if (!rc) {
+        rc = qk_gemm_launch(ah, al, W, S, out_dim, in_dim, &p, QK_GEMM_STORE, y, NULL, NULL, s);
+    }
     if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = QWEN_HIP_EDEVICE;
     pthread_mutex_unlock(&g_ws_lock);
     return rc;
@@ -106,7 +120,20 @@ int qwen_hip_causal_attention(float *out, const float *Q, const float *K, const 
     qk_attn_args a = {.q = Q, .k = K, .v = V, .pos_stride = (long)n_kv_heads * head_dim, .head_stride = head_dim,
                       .seq_k = seq_k, .seq_q = seq_q, .q_offset = q_offset, .heads = n_heads,
                       .kv_heads = n_kv_heads, .scale = scale, .out = out};
-    if (seq_q > 1) return qk_attn_prefill_launch(&a, s);
+    if (seq_q > 1) {
+        const size_t pf = qk_attn_prefill_plan(seq_q, seq_k, q_offset, n_heads, n_kv_heads, &a.chunk, &a.nsplit);
+        if (pf == 0) return qk_attn_prefill_launch(&a, s);
+        pthread_mutex_lock(&g_ws_lock);
+        void *ws = NULL;
+        int rc = workspace(pf * sizeof(float), &ws);
+        if (!rc) {
+            a.part = (float *)ws;
+            rc = qk_attn_prefill_launch(&a, s);
+        }
+        if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = QWEN_HIP_EDEVICE;
+        pthread_mutex_unlock(&g_ws_lock);
+        return rc;
+    }
     /* one query row: keys j <= q_offset, capped at seq_k (qwen_asr_kernels.c:1065-1067) */
     a.seq_k = q_offset + 1 < seq_k ? q_offset + 1 : seq_k;
     a.nsplit = QK_OP_NSPLIT;

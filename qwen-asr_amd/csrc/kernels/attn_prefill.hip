@@ -1,0 +1,329 @@
+// attn_prefill.hip - causal GQA attention over many query rows (the prefill
+// half of qwen_causal_attention, reference qwen_asr_kernels.c:1050-1141) on
+// the fp32 matrix cores of gfx950.
+//
+// The products stay fp32 x fp32 with fp32 accumulation, as in the reference;
+// only the summation order differs.  v_mfma_f32_16x16x4_f32 operand layout
+// (one 16x16 block, k = 4): lane l supplies A[l & 15][l >> 4] and
+// B[l >> 4][l & 15]; the result D[4 (l >> 4) + r][l & 15], r = 0..3, lands in
+// lane l.
+//
+// A block owns one kv head, 64 consecutive queries of both query heads that
+// share it (4 waves: head = wave & 1, queries 32 (wave >> 1) .. + 32) and one
+// split of the key range.  Per 32-key tile staged in LDS:
+//   S^T = K Q^T   A = K rows (keys), B = this wave's queries; each k-step
+//                 takes 4 dims, and over a 16-dim block lane l feeds dims
+//                 4 (l >> 4) .. + 3 in turn, so both operands are one float4
+//                 per 16 dims (the dot products are permuted sums, not
+//                 reordered terms of different queries).
+//   online softmax per query: a query's 32 scores live in the 4 lanes
+//                 l & 15 = query (keys 4 (l >> 4) + r of each 16-key half),
+//                 so the row max / sum are in-lane over 8 values plus two
+//                 cross-lane steps; the rescale factor is lane-local.
+//   O^T += V^T P^T  A = V^T (dims x keys) from a transposed LDS tile, B = the
+//                 probabilities exactly where S^T left them (k-step s uses
+//                 key 4 (l >> 4) + s of lane l).
+// O^T lands as lane l: dims 16 dt + 4 (l >> 4) + r of query l & 15, written
+// back as float4 per dt.
+//
+// Splits: with few query tiles the key range is cut into chunks (a multiple
+// of 32 keys) so the launch fills the chip; each split writes unnormalised
+// partials (o[128], m, l) and attn_prefill_merge combines them in split order.
+// Query tiles are dispatched longest first (causal tiles grow with the query
+// index), so long prefills end without a long single-block tail.
+#include "common.h"
+#include "qk_kernels.h"
+#include "qwen_asr_hip.h"
+
+#include <math.h>
+
+#define PF_Q 64                   // queries per block (per query head)
+#define PF_KT 32                  // keys per LDS tile
+#define PF_KLD (QWEN_HIP_HEAD_DIM + 4)   // sK row stride: rows 4 banks apart
+#define PF_VLD (PF_KT + 4)        // sVt row stride
+#define PF_MINIT (-1.0e30f)       // running-max start, as the reference's -1e30 (:1069)
+
+__device__ __forceinline__ f32x4 mfma_f32_4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float xor_max16_32(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, QK_WAVE));
+    return fmaxf(v, __shfl_xor(v, 32, QK_WAVE));
+}
+
+__device__ __forceinline__ float xor_sum16_32(float v) {
+    v += __shfl_xor(v, 16, QK_WAVE);
+    return v + __shfl_xor(v, 32, QK_WAVE);
+}
+
+// The next K/V tile, held in registers while the current one is consumed.
+struct PfStage {
+    float4 k[4];     // K rows: float4 (tid + 256 i): key (.. >> 5), dims 4 (.. & 31)
+    float v[16];     // V: dim (tid & 127), keys 4 ((tid >> 7) + 2 j) + e
+};
+
+__device__ __forceinline__ void pf_load(PfStage &st, const float *kb, const float *vb, long ps, int k0, int kend,
+                                        int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int idx = tid + 256 * i, key = k0 + (idx >> 5);
+        st.k[i] = key < kend ? *reinterpret_cast<const float4 *>(kb + (size_t)key * ps + (idx & 31) * 4)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const int d = tid & 127;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int key = k0 + 4 * ((tid >> 7) + 2 * j) + e;
+            st.v[4 * j + e] = key < kend ? vb[(size_t)key * ps + d] : 0.0f;
+        }
+    }
+}
+
+__device__ __forceinline__ void pf_store(const PfStage &st, float (*sK)[PF_KLD], float (*sVt)[PF_VLD], int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int idx = tid + 256 * i;
+        *reinterpret_cast<float4 *>(&sK[idx >> 5][(idx & 31) * 4]) = st.k[i];
+    }
+    const int d = tid & 127;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        *reinterpret_cast<float4 *>(&sVt[d][4 * ((tid >> 7) + 2 * j)]) =
+            make_float4(st.v[4 * j], st.v[4 * j + 1], st.v[4 * j + 2], st.v[4 * j + 3]);
+}
+
+__device__ __forceinline__ void pf_write_out(const qk_attn_args &a, size_t base, float4 v) {
+    if (a.out) {
+        *reinterpret_cast<float4 *>(a.out + base) = v;
+    } else {
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint16_t hi = f32_to_bf16_rne(e[i]);
+            a.out_hi[base + i] = hi;
+            a.out_lo[base + i] = f32_to_bf16_rne(e[i] - bf16_to_f32(hi));
+        }
+    }
+}
+
+__global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
+    constexpr int hd = QWEN_HIP_HEAD_DIM;
+    __shared__ __attribute__((aligned(16))) float sK[PF_KT][PF_KLD];
+    __shared__ __attribute__((aligned(16))) float sVt[hd][PF_VLD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 15, kq = lane >> 4;
+    const int nq = (a.seq_q + PF_Q - 1) / PF_Q;
+    const int t = nq - 1 - (int)blockIdx.x;              // longest query tiles first
+    const int g = blockIdx.y, split = blockIdx.z;
+    const int q0 = t * PF_Q;
+    const int qn = min(PF_Q, a.seq_q - q0);
+    const int kend_tile = min(a.seq_k, a.q_offset + q0 + qn);
+    const int ks0 = split * a.chunk;
+    if (ks0 >= kend_tile) return;                         // block-uniform
+    const int ks1 = min(kend_tile, ks0 + a.chunk);
+    const int h = g * 2 + (wave & 1);
+    const int qs = q0 + 32 * (wave >> 1);                 // first query of this wave
+    const bool wave_on = qs < a.seq_q;
+    const int qstride = a.heads * hd;
+    const float *kb = a.k + (size_t)g * a.head_stride;
+    const float *vb = a.v + (size_t)g * a.head_stride;
+
+    // this lane's query rows (16 per tile qt), dims 16 b + 4 kq .. + 3
+    float4 q[2][8];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int qi = qs + 16 * qt + ql;
+#pragma unroll
+        for (int b = 0; b < 8; b++)
+            q[qt][b] = qi < a.seq_q
+                           ? *reinterpret_cast<const float4 *>(a.q + (size_t)qi * qstride + h * hd + 16 * b + 4 * kq)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    f32x4 o[2][8];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[qt][dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m[2] = {PF_MINIT, PF_MINIT}, l[2] = {0.f, 0.f};
+
+    PfStage st;
+    pf_load(st, kb, vb, a.pos_stride, ks0, ks1, tid);
+    for (int k0 = ks0; k0 < ks1; k0 += PF_KT) {
+        __syncthreads();                                  // previous tile fully consumed
+        pf_store(st, sK, sVt, tid);
+        __syncthreads();
+        if (k0 + PF_KT < ks1) pf_load(st, kb, vb, a.pos_stride, k0 + PF_KT, ks1, tid);
+        if (!wave_on) continue;
+
+        // scores: s[qt][kt][r] = q(query qs + 16 qt + ql) . k(key k0 + 16 kt + 4 kq + r)
+        f32x4 s[2][2];
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) s[qt][kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            float4 kf[2];
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) kf[kt] = *reinterpret_cast<const float4 *>(&sK[16 * kt + ql][16 * b + 4 * kq]);
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++) {
+                    s[qt][kt] = mfma_f32_4(kf[kt].x, q[qt][b].x, s[qt][kt]);
+                    s[qt][kt] = mfma_f32_4(kf[kt].y, q[qt][b].y, s[qt][kt]);
+                    s[qt][kt] = mfma_f32_4(kf[kt].z, q[qt][b].z, s[qt][kt]);
+                    s[qt][kt] = mfma_f32_4(kf[kt].w, q[qt][b].w, s[qt][kt]);
+                }
+        }
+
+        // online softmax (causal mask: key <= q_offset + query; keys past ks1 belong elsewhere)
+        float p[2][2][4];
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            const int qpos = a.q_offset + qs + 16 * qt + ql;
+            float sc[2][4], mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = k0 + 16 * kt + 4 * kq + r;
+                    sc[kt][r] = (key <= qpos && key < ks1) ? s[qt][kt][r] * a.scale : -INFINITY;
+                    mx = fmaxf(mx, sc[kt][r]);
+                }
+            mx = xor_max16_32(mx);
+            const float mn = fmaxf(m[qt], mx);
+            const float corr = __expf(m[qt] - mn);
+            float sum = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    p[qt][kt][r] = __expf(sc[kt][r] - mn);
+                    sum += p[qt][kt][r];
+                }
+            sum = xor_sum16_32(sum);
+            l[qt] = fmaf(l[qt], corr, sum);
+            m[qt] = mn;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) o[qt][dt] *= corr;
+        }
+
+        // O^T[d][query] += V^T[d][key] P^T[key][query]
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const float4 vf = *reinterpret_cast<const float4 *>(&sVt[16 * dt + ql][16 * kt + 4 * kq]);
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++) {
+                    o[qt][dt] = mfma_f32_4(vf.x, p[qt][kt][0], o[qt][dt]);
+                    o[qt][dt] = mfma_f32_4(vf.y, p[qt][kt][1], o[qt][dt]);
+                    o[qt][dt] = mfma_f32_4(vf.z, p[qt][kt][2], o[qt][dt]);
+                    o[qt][dt] = mfma_f32_4(vf.w, p[qt][kt][3], o[qt][dt]);
+                }
+            }
+    }
+    if (!wave_on) return;
+
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int qi = qs + 16 * qt + ql;
+        if (qi >= a.seq_q) continue;
+        if (a.nsplit == 1) {
+            const float inv = l[qt] > 0.0f ? 1.0f / l[qt] : 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const f32x4 v = o[qt][dt];
+                pf_write_out(a, (size_t)qi * qstride + h * hd + 16 * dt + 4 * kq,
+                             make_float4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv));
+            }
+        } else {
+            float *pp = a.part + ((size_t)(split * a.seq_q + qi) * a.heads + h) * QK_PF_PART;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const f32x4 v = o[qt][dt];
+                *reinterpret_cast<float4 *>(pp + 16 * dt + 4 * kq) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+            if (kq == 0) {
+                pp[hd] = m[qt];
+                pp[hd + 1] = l[qt];
+            }
+        }
+    }
+}
+
+// One wave per (query, head): combine the splits of the query's tile in split
+// order (max, then rescaled sums), normalise, store.
+__global__ __launch_bounds__(64) void attn_prefill_merge(qk_attn_args a) {
+    constexpr int hd = QWEN_HIP_HEAD_DIM;
+    const int qi = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int t = qi / PF_Q;
+    const int kend_tile = min(a.seq_k, a.q_offset + min(a.seq_q, (t + 1) * PF_Q));
+    const int n = (kend_tile + a.chunk - 1) / a.chunk;
+    const size_t stride = (size_t)a.seq_q * a.heads * QK_PF_PART;
+    const float *p0 = a.part + ((size_t)qi * a.heads + h) * QK_PF_PART;
+    float M = PF_MINIT;
+    for (int s = 0; s < n; s++) M = fmaxf(M, p0[s * stride + hd]);
+    float L = 0.0f, ox = 0.0f, oy = 0.0f;
+    for (int s = 0; s < n; s++) {
+        const float *p = p0 + s * stride;
+        const float w = __expf(p[hd] - M);
+        L = fmaf(p[hd + 1], w, L);
+        const float2 v = *reinterpret_cast<const float2 *>(p + 2 * lane);
+        ox = fmaf(v.x, w, ox);
+        oy = fmaf(v.y, w, oy);
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const size_t base = (size_t)qi * a.heads * hd + h * hd + 2 * lane;
+    if (a.out) {
+        *reinterpret_cast<float2 *>(a.out + base) = make_float2(ox * inv, oy * inv);
+    } else {
+        const float e[2] = {ox * inv, oy * inv};
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint16_t hi = f32_to_bf16_rne(e[i]);
+            a.out_hi[base + i] = hi;
+            a.out_lo[base + i] = f32_to_bf16_rne(e[i] - bf16_to_f32(hi));
+        }
+    }
+}
+
+extern "C" size_t qk_attn_prefill_plan(int seq_q, int seq_k, int q_offset, int heads, int kv_heads, int *chunk,
+                                       int *nsplit) {
+    const int nq = (seq_q + PF_Q - 1) / PF_Q;
+    long tiles = 0;
+    int kmax = 0;
+    for (int t = 0; t < nq; t++) {
+        const int qe = (t + 1) * PF_Q < seq_q ? (t + 1) * PF_Q : seq_q;
+        int ke = q_offset + qe;
+        if (ke > seq_k) ke = seq_k;
+        if (ke > kmax) kmax = ke;
+        tiles += (ke + PF_KT - 1) / PF_KT;
+    }
+    // about QK_PF_TARGET blocks in flight: enough to fill 256 CUs twice over
+    long per = (tiles * kv_heads + QK_PF_TARGET - 1) / QK_PF_TARGET;
+    if (per < 1) per = 1;
+    long c = per * PF_KT;
+    if (c > kmax) c = (kmax + PF_KT - 1) / PF_KT * PF_KT;
+    *chunk = (int)c;
+    *nsplit = (int)((kmax + c - 1) / c);
+    return *nsplit > 1 ? (size_t)*nsplit * seq_q * heads * QK_PF_PART : 0;
+}
+
+extern "C" int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s) {
+    if (!a || a->seq_q <= 0 || a->seq_k <= 0 || a->kv_heads <= 0 || a->heads != 2 * a->kv_heads)
+        return QWEN_HIP_EINVAL;
+    if (!a->out && (!a->out_hi || !a->out_lo)) return QWEN_HIP_EINVAL;
+    if (a->chunk <= 0 || a->chunk % PF_KT || a->nsplit < 1 || (a->nsplit > 1 && !a->part)) return QWEN_HIP_EINVAL;
+    const int nq = (a->seq_q + PF_Q - 1) / PF_Q;
+    // every key the last query tile sees must fall in some split
+    const int kmax = a->seq_k < a->q_offset + a->seq_q ? a->seq_k : a->q_offset + a->seq_q;
+    if ((long)a->chunk * a->nsplit < kmax) return QWEN_HIP_EINVAL;
+    attn_prefill<<<dim3(nq, a->kv_heads, a->nsplit), 256, 0, s>>>(*a);
+    if (a->nsplit > 1) attn_prefill_merge<<<dim3(a->seq_q, a->heads), 64, 0, s>>>(*a);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}

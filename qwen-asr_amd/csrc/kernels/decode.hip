@@ -15,7 +15,6 @@
 //                     the op-level ABI.
 //  attn_decode_fused  the decoder's per-layer attention: q/k norm + RoPE + K/V
 //                     append + split attention + in-kernel combine.
-//  attn_prefill       many query rows, causal, K/V tiles staged in LDS.
 #include "common.h"
 #include "qk_kernels.h"
 #include "qwen_asr_hip.h"
@@ -356,6 +355,13 @@ extern "C" int qk_argmax_finish_launch(const float *cand_val, const int *cand_id
 // q/k RMSNorm + NeoX RoPE + K/V append.  One wave per (head, row); lane l
 // owns the RoPE pair (l, l+64) of the 128-wide head.
 // ---------------------------------------------------------------------------
+// Element i of the projection row: the sum of its nsum split-K partials.
+__device__ __forceinline__ float qkv_at(const float *p, int nsum, long pstride) {
+    float v = p[0];
+    for (int s = 1; s < nsum; s++) v += p[s * pstride];
+    return v;
+}
+
 __global__ __launch_bounds__(64) void rope_append(qk_rope_append_args a) {
     const int hd = QWEN_HIP_HEAD_DIM, half = hd / 2;
     const int lane = threadIdx.x;
@@ -369,7 +375,8 @@ __global__ __launch_bounds__(64) void rope_append(qk_rope_append_args a) {
     const int kvh = head - a.heads;
     const float *src = is_q ? row + head * hd : row + qd + kvh * hd;
     const float *nw = is_q ? a.q_norm : a.k_norm;
-    float x1 = src[lane], x2 = src[lane + half];
+    const int ns = a.nsum > 0 ? a.nsum : 1;
+    float x1 = qkv_at(src + lane, ns, a.pstride), x2 = qkv_at(src + lane + half, ns, a.pstride);
     float ss = fmaf(x1, x1, x2 * x2);
     ss = wave_sum(ss);
     const float rinv = 1.0f / sqrtf(ss / (float)hd + a.eps);
@@ -388,8 +395,8 @@ __global__ __launch_bounds__(64) void rope_append(qk_rope_append_args a) {
         a.k_cache[off + lane] = r1;
         a.k_cache[off + lane + half] = r2;
         const float *vs = row + qd + kvd + kvh * hd;
-        a.v_cache[off + lane] = vs[lane];
-        a.v_cache[off + lane + half] = vs[lane + half];
+        a.v_cache[off + lane] = qkv_at(vs + lane, ns, a.pstride);
+        a.v_cache[off + lane + half] = qkv_at(vs + lane + half, ns, a.pstride);
     }
 }
 
@@ -533,118 +540,6 @@ extern "C" int qk_attn_decode_launch(const qk_attn_args *a, hipStream_t s) {
     default: return QWEN_HIP_EINVAL;
     }
     attn_combine<<<a->heads, 128, 0, s>>>(*a);
-    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
-}
-
-// ---------------------------------------------------------------------------
-// Prefill attention (causal).  Block = 64 query rows of one head; four lanes
-// per query row, each owning 32 of the 128 dims.  K/V tiles of 32 positions
-// are staged in LDS and shared by all 64 rows.
-// ---------------------------------------------------------------------------
-#define QK_PA_ROWS 64
-#define QK_PA_TILE 32
-
-__global__ __launch_bounds__(256) void attn_prefill(qk_attn_args a) {
-    const int hd = QWEN_HIP_HEAD_DIM;
-    __shared__ float4 sk[QK_PA_TILE][hd / 4];
-    __shared__ float4 sv[QK_PA_TILE][hd / 4];
-    const int h = blockIdx.y;
-    const int kvh = h / (a.heads / a.kv_heads);
-    const int qi = blockIdx.x * QK_PA_ROWS + (threadIdx.x >> 2);
-    const int quarter = threadIdx.x & 3;
-    const int qstride = a.heads * hd;
-    const bool valid = qi < a.seq_q;
-
-    float4 q[8], o[8];
-    if (valid) {
-        const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)qi * qstride + h * hd + quarter * 32);
-#pragma unroll
-        for (int j = 0; j < 8; j++) q[j] = qp[j];
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; j++) q[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; j++) o[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    float m = -INFINITY, l = 0.0f;
-
-    const int last_q = min(a.seq_q, (int)(blockIdx.x + 1) * QK_PA_ROWS) - 1;
-    const int kend_block = min(a.seq_k, a.q_offset + last_q + 1);
-    const int my_kend = valid ? min(a.seq_k, a.q_offset + qi + 1) : 0;
-    const float *kb = a.k + (size_t)kvh * a.head_stride;
-    const float *vb = a.v + (size_t)kvh * a.head_stride;
-
-    for (int t0 = 0; t0 < kend_block; t0 += QK_PA_TILE) {
-        const int nk = min(QK_PA_TILE, kend_block - t0);
-        __syncthreads();
-        for (int e = threadIdx.x; e < QK_PA_TILE * hd / 4; e += 256) {
-            const int r = e / (hd / 4), c = e % (hd / 4);
-            if (r < nk) {
-                sk[r][c] = *reinterpret_cast<const float4 *>(kb + (size_t)(t0 + r) * a.pos_stride + c * 4);
-                sv[r][c] = *reinterpret_cast<const float4 *>(vb + (size_t)(t0 + r) * a.pos_stride + c * 4);
-            }
-        }
-        __syncthreads();
-        const int jmax = min(nk, my_kend - t0);
-        for (int j = 0; j < nk; j++) {
-            // lanes of one query row agree on (j < jmax); rows in a wave may not
-            float d = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const float4 kk = sk[j][quarter * 8 + c];
-                d = fmaf(q[c].x, kk.x, d);
-                d = fmaf(q[c].y, kk.y, d);
-                d = fmaf(q[c].z, kk.z, d);
-                d = fmaf(q[c].w, kk.w, d);
-            }
-            d = group_sum<4>(d);
-            if (j < jmax) {
-                const float sc = d * a.scale;
-                const float mn = fmaxf(m, sc);
-                const float corr = __expf(m - mn);
-                const float pw = __expf(sc - mn);
-                l = fmaf(l, corr, pw);
-#pragma unroll
-                for (int c = 0; c < 8; c++) {
-                    const float4 vv = sv[j][quarter * 8 + c];
-                    o[c].x = fmaf(o[c].x, corr, pw * vv.x);
-                    o[c].y = fmaf(o[c].y, corr, pw * vv.y);
-                    o[c].z = fmaf(o[c].z, corr, pw * vv.z);
-                    o[c].w = fmaf(o[c].w, corr, pw * vv.w);
-                }
-                m = mn;
-            }
-        }
-    }
-    if (!valid) return;
-    const float inv = (l > 0.0f) ? 1.0f / l : 0.0f;
-    const size_t base = (size_t)qi * qstride + h * hd + quarter * 32;
-    if (a.out) {
-        float4 *op = reinterpret_cast<float4 *>(a.out + base);
-#pragma unroll
-        for (int c = 0; c < 8; c++)
-            op[c] = make_float4(o[c].x * inv, o[c].y * inv, o[c].z * inv, o[c].w * inv);
-    } else {
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const float vals[4] = {o[c].x * inv, o[c].y * inv, o[c].z * inv, o[c].w * inv};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint16_t hi = f32_to_bf16_rne(vals[e]);
-                const uint16_t lo = f32_to_bf16_rne(vals[e] - bf16_to_f32(hi));
-                a.out_hi[base + c * 4 + e] = hi;
-                a.out_lo[base + c * 4 + e] = lo;
-            }
-        }
-    }
-}
-
-extern "C" int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s) {
-    if (!a || a->seq_q <= 0 || a->seq_k <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads)
-        return QWEN_HIP_EINVAL;
-    if (!a->out && (!a->out_hi || !a->out_lo)) return QWEN_HIP_EINVAL;
-    dim3 grid((a->seq_q + QK_PA_ROWS - 1) / QK_PA_ROWS, a->heads);
-    attn_prefill<<<grid, 256, 0, s>>>(*a);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 

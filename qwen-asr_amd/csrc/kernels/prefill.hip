@@ -30,111 +30,159 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
 
 // ---------------------------------------------------------------------------
 // RMSNorm (qwen_asr_kernels.c:750-809) writing the bf16 hi/lo split the GEMM
-// consumes.  One block per row.
+// consumes.  One block per row.  With nsum > 0 the row is first completed
+// in place: x += part[0] + ... + part[nsum-1] (the split-K partials of the
+// projection that produced it, summed in split order), which is the
+// residual add of qwen_asr_decoder.c:318 / :331.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void rmsnorm_split(const float *x, const float *w, int D, float eps,
-                                                     uint16_t *hi, uint16_t *lo) {
+__global__ __launch_bounds__(256) void rmsnorm_split(float *x, const float *part, int nsum, long pstride,
+                                                     const float *w, int D, float eps, uint16_t *hi, uint16_t *lo) {
     __shared__ float red[4];
-    const float *xr = x + (size_t)blockIdx.x * D;
+    float *xr = x + (size_t)blockIdx.x * D;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < D; i += 256) {
+        float v = xr[i];
+        if (nsum) {
+            const float *pr = part + (size_t)blockIdx.x * D + i;
+            float add = pr[0];
+            for (int sp = 1; sp < nsum; sp++) add += pr[sp * pstride];
+            v += add;
+            xr[i] = v;
+        }
+        ss = fmaf(v, v, ss);
+    }
     float rinv = 1.0f;
     if (w) {
-        float ss = 0.0f;
-        for (int i = threadIdx.x; i < D; i += 256) ss = fmaf(xr[i], xr[i], ss);
         ss = block_sum256(ss, red);
         rinv = 1.0f / sqrtf(ss / (float)D + eps);
     }
+    if (!hi) return;
     uint16_t *h = hi + (size_t)blockIdx.x * D, *l = lo + (size_t)blockIdx.x * D;
-    for (int i = threadIdx.x; i < D; i += 256) {
+    for (int i = threadIdx.x; i < D; i += 256) {      // each thread re-reads only what it wrote
         const float v = w ? (xr[i] * w[i]) * rinv : xr[i];
         split2(v, h[i], l[i]);
     }
 }
 
-extern "C" int qk_rmsnorm_split_launch(const float *x, const float *w, int S, int D, float eps,
-                                       uint16_t *hi, uint16_t *lo, hipStream_t s) {
-    if (S <= 0 || D <= 0 || !x || !hi || !lo) return QWEN_HIP_EINVAL;
-    rmsnorm_split<<<S, 256, 0, s>>>(x, w, D, eps, hi, lo);
+extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride, const float *w, int S,
+                                       int D, float eps, uint16_t *hi, uint16_t *lo, hipStream_t s) {
+    if (S <= 0 || D <= 0 || !x || nsum < 0 || (nsum && !part) || (!hi) != (!lo) || (!hi && !nsum))
+        return QWEN_HIP_EINVAL;
+    rmsnorm_split<<<S, 256, 0, s>>>(x, part, nsum, pstride, w, D, eps, hi, lo);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 
 // ---------------------------------------------------------------------------
-// GEMM on v_mfma_f32_16x16x32_bf16.  Block tile BM x BN (4 waves in 2x2, each
-// WM x WN MFMA tiles of 16x16), K staged through LDS 64 at a time.  Operand
-// fragments: lane l supplies row (l & 15) and the 8 consecutive k values
-// [8*(l>>4), +8) of its 32-wide k step, for both the activation tile (A) and
-// the weight tile (W rows play the B columns), so the k pairing is the same
-// on both sides.  Result: lane l holds D[4*(l>>4) + r][l & 15], r = 0..3.
+// GEMM on v_mfma_f32_16x16x32_bf16.  Block tile BM x BN = (WGM TM 16) x
+// (WGN TN 16): 4 waves in a WGM x WGN grid, each TM x TN MFMA tiles of 16x16.
+// K is walked 64 at a time through two LDS buffers: the next tile's global
+// loads are in flight (in registers) while the current one feeds the MFMAs,
+// then land in the other buffer; one barrier per k tile.  Operand fragments:
+// lane l supplies row (l & 15) and the 8 consecutive k values [8 (l >> 4), +8)
+// of its 32-wide k step, for both the activation tile (A) and the weight tile
+// (W rows play the B columns), so the k pairing is the same on both sides.
+// Result: lane l holds D[4 (l >> 4) + r][l & 15], r = 0..3.
+//
+// Split-K: block z covers k in [z kc, (z + 1) kc).  With more than one split
+// the STORE epilogue writes split z's partial product to y + z M N and the
+// consumer sums the splits in order (fixed order: the result does not depend
+// on scheduling).  ADD and SWIGLU epilogues run with one split only.
 // ---------------------------------------------------------------------------
 #define QK_BK 64
 #define QK_LDK (QK_BK + 8)   // +16 B per row keeps the 16-row fragment reads conflict free
 
-template <int WM, int WN, int EPI>
+template <int WGM, int WGN, int TM, int TN, int EPI>
 __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ahi, const uint16_t *__restrict__ alo,
-                                                 const uint16_t *__restrict__ W, int M, int N, int K,
+                                                 const uint16_t *__restrict__ W, int M, int N, int K, int kc,
                                                  float *y, uint16_t *ohi, uint16_t *olo) {
-    constexpr int BM = 32 * WM, BN = 32 * WN;
-    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM][QK_LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t sB[BN][QK_LDK];
+    static_assert(WGM * WGN == 4, "4 waves");
+    constexpr int BM = WGM * TM * 16, BN = WGN * TN * 16;
+    constexpr int ACH = BM * (QK_BK / 8), BCH = BN * (QK_BK / 8);   // 16-byte chunks per tile
+    constexpr int APT = (ACH + 255) / 256, BPT = (BCH + 255) / 256;
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][2][BM][QK_LDK];   // [buffer][hi, lo]
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN][QK_LDK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb = blockIdx.z * kc, ke = min(K, kb + kc);
 
-    f32x4 acc[WM][WN];
+    uint4 ra[2][APT], rb[BPT];
+    auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < WM; i++)
+        for (int i = 0; i < APT; i++) {
+            const int c = tid + 256 * i, r = c >> 3, gm = m0 + r, gk = k0 + (c & 7) * 8;
+            const bool ok = (ACH % 256 == 0 || c < ACH) && gm < M && gk < ke;
+            ra[0][i] = ok ? *reinterpret_cast<const uint4 *>(ahi + (size_t)gm * K + gk) : make_uint4(0u, 0u, 0u, 0u);
+            ra[1][i] = ok ? *reinterpret_cast<const uint4 *>(alo + (size_t)gm * K + gk) : make_uint4(0u, 0u, 0u, 0u);
+        }
 #pragma unroll
-        for (int j = 0; j < WN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-    for (int k0 = 0; k0 < K; k0 += QK_BK) {
-        __syncthreads();
-        for (int c = tid; c < BM * (QK_BK / 8); c += 256) {
-            const int r = c / (QK_BK / 8), kc = (c % (QK_BK / 8)) * 8;
-            const int gm = m0 + r, gk = k0 + kc;
-            uint4 vh = make_uint4(0u, 0u, 0u, 0u), vl = vh;
-            if (gm < M && gk < K) {
-                vh = *reinterpret_cast<const uint4 *>(ahi + (size_t)gm * K + gk);
-                vl = *reinterpret_cast<const uint4 *>(alo + (size_t)gm * K + gk);
+        for (int i = 0; i < BPT; i++) {
+            const int c = tid + 256 * i, r = c >> 3, gn = n0 + r, gk = k0 + (c & 7) * 8;
+            const bool ok = (BCH % 256 == 0 || c < BCH) && gn < N && gk < ke;
+            rb[i] = ok ? ld_stream16(W + (size_t)gn * K + gk) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < APT; i++) {
+            const int c = tid + 256 * i;
+            if (ACH % 256 == 0 || c < ACH) {
+                *reinterpret_cast<uint4 *>(&sA[buf][0][c >> 3][(c & 7) * 8]) = ra[0][i];
+                *reinterpret_cast<uint4 *>(&sA[buf][1][c >> 3][(c & 7) * 8]) = ra[1][i];
             }
-            *reinterpret_cast<uint4 *>(&sA[0][r][kc]) = vh;
-            *reinterpret_cast<uint4 *>(&sA[1][r][kc]) = vl;
         }
-        for (int c = tid; c < BN * (QK_BK / 8); c += 256) {
-            const int r = c / (QK_BK / 8), kc = (c % (QK_BK / 8)) * 8;
-            const int gn = n0 + r, gk = k0 + kc;
-            uint4 vb = make_uint4(0u, 0u, 0u, 0u);
-            if (gn < N && gk < K) vb = *reinterpret_cast<const uint4 *>(W + (size_t)gn * K + gk);
-            *reinterpret_cast<uint4 *>(&sB[r][kc]) = vb;
+#pragma unroll
+        for (int i = 0; i < BPT; i++) {
+            const int c = tid + 256 * i;
+            if (BCH % 256 == 0 || c < BCH) *reinterpret_cast<uint4 *>(&sB[buf][c >> 3][(c & 7) * 8]) = rb[i];
         }
-        __syncthreads();
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    const int nk = (ke - kb + QK_BK - 1) / QK_BK;
+    gload(kb);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kb + (kt + 1) * QK_BK);
 #pragma unroll
         for (int kk = 0; kk < QK_BK; kk += 32) {
             const int koff = kk + (lane >> 4) * 8;
-            bf16x8 bfr[WN];
+            bf16x8 bfr[TN];
 #pragma unroll
-            for (int j = 0; j < WN; j++)
-                bfr[j] = *reinterpret_cast<const bf16x8 *>(&sB[wn * (BN / 2) + j * 16 + (lane & 15)][koff]);
+            for (int j = 0; j < TN; j++)
+                bfr[j] = *reinterpret_cast<const bf16x8 *>(&sB[buf][(wn * TN + j) * 16 + (lane & 15)][koff]);
 #pragma unroll
-            for (int i = 0; i < WM; i++) {
-                const int ra = wm * (BM / 2) + i * 16 + (lane & 15);
-                const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(&sA[0][ra][koff]);
-                const bf16x8 al = *reinterpret_cast<const bf16x8 *>(&sA[1][ra][koff]);
+            for (int i = 0; i < TM; i++) {
+                const int ra_ = (wm * TM + i) * 16 + (lane & 15);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(&sA[buf][0][ra_][koff]);
+                const bf16x8 al = *reinterpret_cast<const bf16x8 *>(&sA[buf][1][ra_][koff]);
 #pragma unroll
-                for (int j = 0; j < WN; j++) {
+                for (int j = 0; j < TN; j++) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bfr[j], acc[i][j], 0, 0, 0);
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bfr[j], acc[i][j], 0, 0, 0);
                 }
             }
         }
+        if (kt + 1 < nk) lstore(buf ^ 1);
+        __syncthreads();
     }
 
+    float *yz = y + (EPI == QK_GEMM_STORE ? (size_t)blockIdx.z * M * N : 0);
 #pragma unroll
-    for (int i = 0; i < WM; i++) {
+    for (int i = 0; i < TM; i++) {
 #pragma unroll
-        for (int j = 0; j < WN; j++) {
-            const int n = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + (wn * TN + j) * 16 + (lane & 15);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + r;
+                const int m = m0 + (wm * TM + i) * 16 + 4 * (lane >> 4) + r;
                 const float v = acc[i][j][r];
                 if (EPI == QK_GEMM_SWIGLU) {
                     const float u = __shfl_xor(v, 1, QK_WAVE);   // column n+1 lives in lane l^1
@@ -143,7 +191,7 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
                         split2(swiglu1(v, u), ohi[o], olo[o]);
                     }
                 } else if (m < M && n < N) {
-                    if (EPI == QK_GEMM_STORE) y[(size_t)m * N + n] = v;
+                    if (EPI == QK_GEMM_STORE) yz[(size_t)m * N + n] = v;
                     else y[(size_t)m * N + n] += v;
                 }
             }
@@ -151,21 +199,83 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
     }
 }
 
-template <int WM, int WN>
+template <int WGM, int WGN, int TM, int TN>
 static void gemm_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int N, int K,
-                          int epi, float *y, uint16_t *oh, uint16_t *ol, hipStream_t s) {
-    dim3 grid((N + 32 * WN - 1) / (32 * WN), (M + 32 * WM - 1) / (32 * WM));
-    if (epi == QK_GEMM_STORE) gemm_hilo<WM, WN, QK_GEMM_STORE><<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, N, K, y, oh, ol);
-    else if (epi == QK_GEMM_ADD) gemm_hilo<WM, WN, QK_GEMM_ADD><<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, N, K, y, oh, ol);
-    else gemm_hilo<WM, WN, QK_GEMM_SWIGLU><<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, N, K, y, oh, ol);
+                          const qk_gemm_plan *p, int epi, float *y, uint16_t *oh, uint16_t *ol, hipStream_t s) {
+    dim3 grid((N + WGN * TN * 16 - 1) / (WGN * TN * 16), (M + WGM * TM * 16 - 1) / (WGM * TM * 16), p->nsplit);
+    if (epi == QK_GEMM_STORE)
+        gemm_hilo<WGM, WGN, TM, TN, QK_GEMM_STORE><<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+    else if (epi == QK_GEMM_ADD)
+        gemm_hilo<WGM, WGN, TM, TN, QK_GEMM_ADD><<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+    else
+        gemm_hilo<WGM, WGN, TM, TN, QK_GEMM_SWIGLU><<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+}
+
+extern "C" void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p) {
+    p->bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+    const long tiles = (long)((M + p->bm - 1) / p->bm) * ((N + QK_GEMM_BN - 1) / QK_GEMM_BN);
+    const int kt = (K + QK_BK - 1) / QK_BK;
+    long ns = tiles >= QK_GEMM_TARGET ? 1 : (QK_GEMM_TARGET + tiles - 1) / tiles;
+    if (ns > QK_GEMM_MAX_SPLIT) ns = QK_GEMM_MAX_SPLIT;
+    if (ns > kt) ns = kt;
+    const int per = (int)((kt + ns - 1) / ns);      // k tiles per split
+    p->kc = per * QK_BK;
+    p->nsplit = (kt + per - 1) / per;
 }
 
 extern "C" int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int N, int K,
-                              int epi, float *y, uint16_t *out_hi, uint16_t *out_lo, hipStream_t s) {
-    if (M <= 0 || N <= 0 || K <= 0 || (K & 7) || !a_hi || !a_lo || !W) return QWEN_HIP_EINVAL;
+                              const qk_gemm_plan *p, int epi, float *y, uint16_t *out_hi, uint16_t *out_lo,
+                              hipStream_t s) {
+    if (M <= 0 || N <= 0 || K <= 0 || (K & 7) || !a_hi || !a_lo || !W || !p) return QWEN_HIP_EINVAL;
+    if (p->nsplit < 1 || p->kc <= 0 || p->kc % QK_BK || (long)p->kc * p->nsplit < K ||
+        (long)p->kc * (p->nsplit - 1) >= K)
+        return QWEN_HIP_EINVAL;
+    if (p->nsplit > 1 && epi != QK_GEMM_STORE) return QWEN_HIP_EINVAL;
     if (epi == QK_GEMM_SWIGLU ? (!out_hi || !out_lo || (N & 1)) : !y) return QWEN_HIP_EINVAL;
-    if (M >= 256) gemm_dispatch<2, 2>(a_hi, a_lo, W, M, N, K, epi, y, out_hi, out_lo, s);
-    else gemm_dispatch<1, 2>(a_hi, a_lo, W, M, N, K, epi, y, out_hi, out_lo, s);
+    if (p->bm == 32) gemm_dispatch<1, 4, 2, 2>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);
+    else if (p->bm == 64) gemm_dispatch<2, 2, 2, 4>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);
+    else if (p->bm == 128) gemm_dispatch<2, 2, 4, 4>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);
+    else return QWEN_HIP_EINVAL;
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// Sum of the nsum split-K partials part[s][M][N] in split order, then the
+// epilogue: STORE y = sum, ADD y += sum, SWIGLU hi/lo of silu(sum[2j]) sum[2j+1].
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_reduce(const float *part, int nsum, long M, long N, float *y,
+                                                   uint16_t *ohi, uint16_t *olo) {
+    const long pairs = M * N / 2, pstride = M * N;
+    for (long t = blockIdx.x * 256L + threadIdx.x; t < pairs; t += (long)gridDim.x * 256) {
+        const float2 *p = reinterpret_cast<const float2 *>(part) + t;
+        float2 v = p[0];
+        for (int sp = 1; sp < nsum; sp++) {
+            const float2 w = p[sp * pstride / 2];
+            v.x += w.x;
+            v.y += w.y;
+        }
+        if (EPI == QK_GEMM_SWIGLU) {
+            split2(swiglu1(v.x, v.y), ohi[t], olo[t]);
+        } else if (EPI == QK_GEMM_ADD) {
+            float2 *o = reinterpret_cast<float2 *>(y) + t;
+            float2 a = *o;
+            a.x += v.x;
+            a.y += v.y;
+            *o = a;
+        } else {
+            reinterpret_cast<float2 *>(y)[t] = v;
+        }
+    }
+}
+
+extern "C" int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, float *y, uint16_t *out_hi,
+                                     uint16_t *out_lo, hipStream_t s) {
+    if (!part || nsum < 1 || M <= 0 || N <= 0 || (N & 1)) return QWEN_HIP_EINVAL;
+    if (epi == QK_GEMM_SWIGLU ? (!out_hi || !out_lo) : !y) return QWEN_HIP_EINVAL;
+    long blocks = ((long)M * N / 2 + 255) / 256;
+    if (blocks > 2048) blocks = 2048;
+    if (epi == QK_GEMM_STORE) gemm_reduce<QK_GEMM_STORE><<<(int)blocks, 256, 0, s>>>(part, nsum, M, N, y, out_hi, out_lo);
+    else if (epi == QK_GEMM_ADD) gemm_reduce<QK_GEMM_ADD><<<(int)blocks, 256, 0, s>>>(part, nsum, M, N, y, out_hi, out_lo);
+    else gemm_reduce<QK_GEMM_SWIGLU><<<(int)blocks, 256, 0, s>>>(part, nsum, M, N, y, out_hi, out_lo);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 

@@ -55,7 +55,9 @@ int qk_argmax_finish_launch(const float *cand_val, const int *cand_idx, int n,
 
 /* ---- q/k RMSNorm + NeoX RoPE + KV append ---------------------------- */
 typedef struct {
-    const float *qkv;         /* [S][q_dim + 2*kv_dim] raw projections */
+    const float *qkv;         /* [S][q_dim + 2*kv_dim] raw projections, or nsum split-K */
+    int nsum;                 /* partials pstride floats apart, summed in order (0: 1) */
+    long pstride;
     const float *q_norm, *k_norm;
     float eps;
     const float *rope_cos, *rope_sin;   /* [cap][head_dim], indexed by position */
@@ -79,13 +81,25 @@ typedef struct {
     int seq_q, q_offset;      /* prefill: query i sees keys j <= q_offset + i */
     int heads, kv_heads;
     float scale;
-    float *part;              /* decode split partials [heads][nsplit][head_dim+2] */
+    float *part;              /* decode: split partials [heads][nsplit][head_dim+2];
+                                 prefill: [nsplit][seq_q][heads][QK_PF_PART] */
     int nsplit;
+    int chunk;                /* prefill: keys per split (multiple of 32) */
     float *out;               /* fp32 [seq_q][heads*head_dim] */
     uint16_t *out_hi, *out_lo;/* prefill alternative: bf16 hi/lo split of out */
 } qk_attn_args;
 
 int qk_attn_decode_launch(const qk_attn_args *a, hipStream_t s);
+
+/* Prefill attention (fp32 MFMA, heads == 2 * kv_heads, head_dim 128): the
+ * key range of each 64-query tile is cut into splits of `chunk` keys; with
+ * nsplit > 1 the splits write partials to `part` and a merge kernel follows.
+ * qk_attn_prefill_plan picks chunk/nsplit for a launch of about
+ * QK_PF_TARGET blocks and returns the partial buffer size in floats (0 when
+ * nsplit == 1). */
+#define QK_PF_PART 130              /* o[128], m, l */
+#define QK_PF_TARGET 384
+size_t qk_attn_prefill_plan(int seq_q, int seq_k, int q_offset, int heads, int kv_heads, int *chunk, int *nsplit);
 int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s);
 
 /* ---- fused decode attention (one kernel per layer) -------------------- */
@@ -198,18 +212,31 @@ int qk_persist_supported(int hidden, int inter, int heads, int kv_heads, int dev
 int qk_persist_launch(const qk_persist_args *a, int hidden, int inter, hipStream_t s);
 
 /* ---- prefill (MFMA) ---------------------------------------------------- */
-/* hi/lo = bf16 split of rms_norm(x)*w (w NULL: of x itself): hi = bf16(v),
- * lo = bf16(v - hi), so hi + lo carries v to ~2^-17 relative. */
-int qk_rmsnorm_split_launch(const float *x, const float *w, int S, int D, float eps,
-                            uint16_t *hi, uint16_t *lo, hipStream_t s);
+/* Optionally x += part[0] + ... + part[nsum-1] (rows of pstride floats apart,
+ * in place, split order), then hi/lo = bf16 split of rms_norm(x)*w (w NULL:
+ * of x itself): hi = bf16(v), lo = bf16(v - hi), so hi + lo carries v to
+ * ~2^-17 relative.  hi/lo NULL: only the sum. */
+int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride, const float *w, int S, int D,
+                            float eps, uint16_t *hi, uint16_t *lo, hipStream_t s);
 
 enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2 };
+/* Tiling of one M x N x K product: block rows bm (32 / 64 / 128, columns
+ * QK_GEMM_BN), and nsplit slices of kc (a multiple of 64) along K so a launch
+ * has about QK_GEMM_TARGET blocks. */
+#define QK_GEMM_BN 128
+#define QK_GEMM_TARGET 256
+#define QK_GEMM_MAX_SPLIT 16
+typedef struct { int bm, nsplit, kc; } qk_gemm_plan;
+void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p);
 /* Y[M][N] (=, +=) (A_hi + A_lo)[M][K] . W[N][K]^T on bf16 MFMA with fp32
  * accumulation; SWIGLU writes silu(Y[:,2j]) * Y[:,2j+1] as a bf16 hi/lo
- * split [M][N/2] into out_hi/out_lo. */
-int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W,
-                   int M, int N, int K, int epi, float *y,
-                   uint16_t *out_hi, uint16_t *out_lo, hipStream_t s);
+ * split [M][N/2] into out_hi/out_lo.  With nsplit > 1 only STORE is allowed
+ * and y is [nsplit][M][N]: split z's partial product at y + z M N. */
+int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int N, int K,
+                   const qk_gemm_plan *p, int epi, float *y, uint16_t *out_hi, uint16_t *out_lo, hipStream_t s);
+/* Sum nsum partials [nsum][M][N] in order and apply epi (N even). */
+int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, float *y, uint16_t *out_hi,
+                          uint16_t *out_lo, hipStream_t s);
 
 /* ---- elementwise (op-level ABI) --------------------------------------- */
 int qk_add_launch(float *a, const float *b, long n, hipStream_t s);

@@ -3,6 +3,8 @@ called through the C ABI on device memory, against the CPU oracle on the same
 seeded inputs.  Tolerances are stated per test; fp32 accumulation order
 differs between the GPU and CPU, so GEMV checks use the rounding bound
 4*K*2^-24*sum|w*x| (and the bf16 hi/lo GEMM adds 2^-16*sum|w*x|)."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -43,8 +45,11 @@ def test_gemv_sweep(P, qa, gpu, rows, cols):
     assert np.all(np.abs(y - yo) <= bound), float(np.max(np.abs(y - yo) / bound))
 
 
+# covers every tiling of qk_gemm_plan_for: 32 / 64 / 128-row blocks, split-K
+# with its reduce pass (and the odd-N case that cannot split), one split
 @pytest.mark.parametrize("M,N,K", [(2, 64, 256), (31, 4096, 1024), (64, 1024, 2048), (401, 6144, 1024),
-                                   (130, 2048, 6144), (7, 100, 200)])
+                                   (130, 2048, 6144), (7, 100, 200), (33, 101, 64), (1000, 1024, 1024),
+                                   (2100, 4096, 256), (30, 1024, 3072)])
 def test_gemm_hilo(P, qa, gpu, M, N, K):
     W = P.synth_bf16(N * K, 1, 9200 + N).reshape(N, K)
     x = P.synth_f32(M * K, 1, 9300 + M).reshape(M, K)
@@ -113,7 +118,8 @@ def test_elementwise_ops(P, qa, gpu):
 
 
 @pytest.mark.parametrize("sq,sk,q_off", [(1, 1, 0), (1, 529, 528), (1, 3000, 2999), (1, 100, 40),
-                                         (7, 7, 0), (64, 100, 36), (130, 130, 0), (33, 300, 200)])
+                                         (7, 7, 0), (64, 100, 36), (130, 130, 0), (33, 300, 200),
+                                         (30, 1000, 970), (401, 401, 0), (600, 650, 40), (1100, 3000, 1900)])
 def test_causal_attention(P, qa, gpu, sq, sk, q_off):
     nh, nkv, hd = 16, 8, 128
     r = np.random.default_rng(sq * 1000 + sk)
@@ -129,6 +135,41 @@ def test_causal_attention(P, qa, gpu, sq, sk, q_off):
     exp = np.empty((sq, nh * hd), np.float32)
     P.orc_lib().orc_causal_attention(exp, Q, K, V, sq, sk, nh, nkv, hd, scale, q_off)
     np.testing.assert_allclose(host(dout), exp, atol=3e-5, rtol=1e-4)
+
+
+def test_causal_attention_long_unsplit(P, qa, gpu):
+    """6400 query rows: the launch plan keeps one split per query tile (each
+    block walks up to 6400 keys), the path the 8k-row prefill takes.  Checked
+    against a float64 causal softmax attention computed with torch on the
+    same device (the CPU oracle is too slow at this size)."""
+    sq = sk = 6400
+    nh, nkv, hd = 16, 8, 128
+    chunk, nsplit = C.c_int(), C.c_int()
+    qa.lib().qk_attn_prefill_plan(sq, sk, 0, nh, nkv, C.byref(chunk), C.byref(nsplit))
+    assert nsplit.value == 1, (chunk.value, nsplit.value)
+    g = gpu.Generator(device="cuda").manual_seed(11)
+    Q = gpu.randn((sq, nh * hd), generator=g, device="cuda", dtype=gpu.float32)
+    K = gpu.randn((sk, nkv * hd), generator=g, device="cuda", dtype=gpu.float32)
+    V = gpu.randn((sk, nkv * hd), generator=g, device="cuda", dtype=gpu.float32)
+    scale = 1.0 / np.sqrt(128.0)
+    out = gpu.empty((sq, nh * hd), dtype=gpu.float32, device="cuda")
+    qa.check(qa.lib().qwen_hip_causal_attention(ptr(out), ptr(Q), ptr(K), ptr(V), sq, sk, nh, nkv, hd,
+                                                scale, 0, None), "attention")
+    gpu.cuda.synchronize()
+    mask = gpu.triu(gpu.ones((sq, sk), dtype=gpu.bool, device="cuda"), diagonal=1)
+    worst = 0.0
+    for h in range(0, nh, 3):
+        q = Q[:, h * hd:(h + 1) * hd].double()
+        k = K[:, (h // 2) * hd:(h // 2 + 1) * hd].double().contiguous()
+        v = V[:, (h // 2) * hd:(h // 2 + 1) * hd].double().contiguous()
+        sc = (q @ k.t().contiguous()) * scale
+        sc.masked_fill_(mask, float("-inf"))
+        ref = gpu.softmax(sc, dim=-1) @ v
+        got = out[:, h * hd:(h + 1) * hd].double()
+        err = (got - ref).abs() - (3e-5 + 1e-4 * ref.abs())
+        worst = max(worst, float(err.max()))
+        del sc, ref
+    assert worst <= 0.0, worst
 
 
 def test_argmax_matvec(P, qa, gpu):
