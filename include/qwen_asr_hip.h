@@ -191,6 +191,71 @@ double qwen_hip_decoder_step_bytes(const qwen_hip_decoder *dec, int kv_len);
 
 const char *qwen_hip_last_error(void);
 
+/* The configuration the decoder was created with (NULL for NULL). */
+const qwen_hip_config *qwen_hip_decoder_config(const qwen_hip_decoder *dec);
+
+/* ------------------------------------------------------------------------
+ * Checkpoint loading: a Qwen3-ASR safetensors directory (model.safetensors,
+ * or model-*.safetensors shards in name order) mapped read-only; replaces
+ * multi_safetensors_open / multi_safetensors_find / safetensors_get_*
+ * (reference qwen_asr_safetensors.h:47-73, qwen_asr_safetensors.c:194-394),
+ * qwen_decoder_load (qwen_asr_decoder.c:45-116) and the decoder part of
+ * detect_config (qwen_asr.c:135-191).  Only the decoder tensors
+ * (thinker.model.*) are read.
+ * ------------------------------------------------------------------------ */
+#define QWEN_HIP_ST_F32    0       /* dtype codes, as safetensor_dtype_t (qwen_asr_safetensors.h:15-23) */
+#define QWEN_HIP_ST_F16    1
+#define QWEN_HIP_ST_BF16   2
+#define QWEN_HIP_ST_OTHER -1
+
+typedef struct qwen_hip_checkpoint qwen_hip_checkpoint;
+
+/* NULL on failure (message in qwen_hip_last_error). */
+qwen_hip_checkpoint *qwen_hip_checkpoint_open(const char *model_dir);
+void qwen_hip_checkpoint_close(qwen_hip_checkpoint *ck);
+/* number of tensors over all shards */
+int qwen_hip_checkpoint_count(const qwen_hip_checkpoint *ck);
+/* Look a tensor up by name (multi_safetensors_find): dtype, rank, shape
+ * (up to 8 dims) and a pointer to its bytes inside the mapping (valid until
+ * close).  Any output may be NULL.  QWEN_HIP_EINVAL when absent. */
+int qwen_hip_checkpoint_tensor(const qwen_hip_checkpoint *ck, const char *name, int *dtype, int *ndim,
+                               long long *shape, const void **data);
+/* The decoder shape from the tensor shapes: hidden and vocab from
+ * embed_tokens, heads / kv_heads from the q / k projection rows, the MLP
+ * width from gate_proj, layers = count of consecutive layers present;
+ * rms eps 1e-6 and rope theta 1e6 (qwen_asr.c:187-188). */
+int qwen_hip_checkpoint_config(const qwen_hip_checkpoint *ck, qwen_hip_config *cfg);
+/* Upload every decoder tensor: BF16 matrices straight from the mapping
+ * (load_bf16_direct), F32 or BF16 norm vectors widened to fp32 (load_f32). */
+int qwen_hip_decoder_load_checkpoint(qwen_hip_decoder *dec, const qwen_hip_checkpoint *ck);
+/* open + config + create + load + close in one call; NULL on failure. */
+qwen_hip_decoder *qwen_hip_decoder_create_from_checkpoint(const char *model_dir, int device, int kv_capacity);
+
+/* ------------------------------------------------------------------------
+ * Streaming driver: the decoder half of qwen_transcribe_stream (reference
+ * qwen_asr.c:1747-1829).  Each call takes one chunk's complete decoder
+ * input rows (the caller assembles template + audio + suffix + carried
+ * tokens as the reference builds input_embeds), keeps the cached positions
+ * of the longest prefix of rows[0..n_rows-1) that is bitwise equal to the
+ * previous call's (the reference's memcmp, :1752-1764), prefills the rest,
+ * forwards the last row and decodes greedily like the reference's loop
+ * (:1802-1814): tokens are appended (and forwarded) until <|endoftext|> /
+ * <|im_end|> or max_new of them.  Returns the number of tokens written to
+ * out_tokens (room for max_new), negative on error; *reused_rows (may be
+ * NULL) receives the reused prefix length.  The stream does not own the
+ * decoder; one stream per decoder at a time.
+ * ------------------------------------------------------------------------ */
+typedef struct qwen_hip_stream qwen_hip_stream;
+qwen_hip_stream *qwen_hip_stream_create(qwen_hip_decoder *dec);
+void qwen_hip_stream_destroy(qwen_hip_stream *st);
+/* forget the previous rows: the next chunk prefills from position 0 */
+void qwen_hip_stream_reset(qwen_hip_stream *st);
+int qwen_hip_stream_chunk(qwen_hip_stream *st, const float *rows, int n_rows, int max_new, int *out_tokens,
+                          int *reused_rows);
+/* prefill rows seen and reused so far (the reference's prefill_total_tokens /
+ * prefill_reused_tokens, :1768-1769) */
+int qwen_hip_stream_stats(const qwen_hip_stream *st, long long *rows_total, long long *rows_reused);
+
 /* ------------------------------------------------------------------------
  * Op-level ABI: the qwen_asr_kernels.h operators on device pointers.
  * Same argument order and meaning as the reference, plus a stream.

@@ -69,6 +69,19 @@ SIGNATURES = [
     ("qwen_hip_decoder_stream", _vp, [_vp]),
     ("qwen_hip_decoder_step_bytes", _d, [_vp, _i]),
     ("qwen_hip_last_error", C.c_char_p, []),
+    ("qwen_hip_decoder_config", _vp, [_vp]),
+    ("qwen_hip_checkpoint_open", _vp, [C.c_char_p]),
+    ("qwen_hip_checkpoint_close", None, [_vp]),
+    ("qwen_hip_checkpoint_count", _i, [_vp]),
+    ("qwen_hip_checkpoint_tensor", _i, [_vp, C.c_char_p, _vp, _vp, _vp, _vp]),
+    ("qwen_hip_checkpoint_config", _i, [_vp, _vp]),
+    ("qwen_hip_decoder_load_checkpoint", _i, [_vp, _vp]),
+    ("qwen_hip_decoder_create_from_checkpoint", _vp, [C.c_char_p, _i, _i]),
+    ("qwen_hip_stream_create", _vp, [_vp]),
+    ("qwen_hip_stream_destroy", None, [_vp]),
+    ("qwen_hip_stream_reset", None, [_vp]),
+    ("qwen_hip_stream_chunk", _i, [_vp, _vp, _i, _i, _vp, _vp]),
+    ("qwen_hip_stream_stats", _i, [_vp, _vp, _vp]),
     ("qwen_hip_add_inplace", _i, [_vp, _vp, _i, _vp]),
     ("qwen_hip_rms_norm", _i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     ("qwen_hip_rms_norm_per_head", _i, [_vp, _vp, _i, _i, _i, _f, _vp]),
@@ -177,6 +190,48 @@ def prompt_rows(cfg, n_audio, n_ids, seed=0, audio_chunk=0, token_set=0, emb=Non
     return np.ascontiguousarray(np.concatenate([head, audio, tail]), np.float32), ids, emb
 
 
+ST_F32, ST_F16, ST_BF16, ST_OTHER = 0, 1, 2, -1
+
+
+class Checkpoint:
+    """A safetensors checkpoint directory mapped read-only (host only, no GPU)."""
+
+    def __init__(self, model_dir):
+        self.h = lib().qwen_hip_checkpoint_open(os.fsencode(model_dir))
+        if not self.h:
+            raise RuntimeError(f"qwen_hip_checkpoint_open: {last_error()}")
+
+    def __len__(self):
+        return lib().qwen_hip_checkpoint_count(self.h)
+
+    def config(self):
+        cfg = HipConfig()
+        check(lib().qwen_hip_checkpoint_config(self.h, C.byref(cfg)), "checkpoint_config")
+        return cfg
+
+    def tensor(self, name):
+        """(dtype code, shape, raw bytes) of one tensor; None when absent."""
+        dt, nd, shape, ptr = C.c_int(), C.c_int(), (C.c_longlong * 8)(), C.c_void_p()
+        if lib().qwen_hip_checkpoint_tensor(self.h, name.encode(), C.byref(dt), C.byref(nd), shape,
+                                            C.byref(ptr)) != 0:
+            return None
+        shp = tuple(int(shape[i]) for i in range(nd.value))
+        n = int(np.prod(shp)) if shp else 1
+        size = {ST_F32: 4, ST_F16: 2, ST_BF16: 2}.get(dt.value, 0) * n
+        return dt.value, shp, C.string_at(ptr.value, size) if size else b""
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().qwen_hip_checkpoint_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Decoder:
     """One decoder context on one GPU (the decoder-level ABI)."""
 
@@ -185,6 +240,21 @@ class Decoder:
         self.h = lib().qwen_hip_decoder_create(C.byref(cfg), device, kv_capacity)
         if not self.h:
             raise RuntimeError(f"qwen_hip_decoder_create: {last_error()}")
+
+    @classmethod
+    def from_checkpoint(cls, model_dir, device=0, kv_capacity=1024):
+        """Create a decoder with the shape and weights of a safetensors checkpoint."""
+        h = lib().qwen_hip_decoder_create_from_checkpoint(os.fsencode(model_dir), device, kv_capacity)
+        if not h:
+            raise RuntimeError(f"qwen_hip_decoder_create_from_checkpoint: {last_error()}")
+        self = cls.__new__(cls)
+        self.h = h
+        self.cfg = HipConfig.from_address(lib().qwen_hip_decoder_config(h))
+        self.cfg = HipConfig(*[getattr(self.cfg, f) for f, _ in HipConfig._fields_])
+        return self
+
+    def load_checkpoint(self, ckpt: "Checkpoint"):
+        check(lib().qwen_hip_decoder_load_checkpoint(self.h, ckpt.h), "load_checkpoint")
 
     # weights -------------------------------------------------------------
     def load_synthetic(self, seed=0, weight_std=0.02, norm_std=0.0):
@@ -273,6 +343,46 @@ class Decoder:
     def close(self):
         if getattr(self, "h", None):
             lib().qwen_hip_decoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+
+class Stream:
+    """The streaming driver over one decoder (prefix KV reuse per chunk)."""
+
+    def __init__(self, dec: Decoder):
+        self.dec = dec
+        self.h = lib().qwen_hip_stream_create(dec.h)
+        if not self.h:
+            raise RuntimeError(f"qwen_hip_stream_create: {last_error()}")
+
+    def chunk(self, rows, max_new):
+        """(tokens, reused rows) of one chunk's decoder input rows [n][hidden]."""
+        rows = np.ascontiguousarray(rows, np.float32)
+        n = rows.size // self.dec.cfg.hidden
+        out = np.zeros(max(max_new, 1), np.int32)
+        reused = C.c_int()
+        k = lib().qwen_hip_stream_chunk(self.h, _ptr(rows), n, int(max_new), _ptr(out), C.byref(reused))
+        check(k, "stream_chunk")
+        return [int(t) for t in out[:k]], reused.value
+
+    def reset(self):
+        lib().qwen_hip_stream_reset(self.h)
+
+    def stats(self):
+        tot, reu = C.c_longlong(), C.c_longlong()
+        check(lib().qwen_hip_stream_stats(self.h, C.byref(tot), C.byref(reu)), "stream_stats")
+        return tot.value, reu.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().qwen_hip_stream_destroy(self.h)
             self.h = None
 
     def __del__(self):

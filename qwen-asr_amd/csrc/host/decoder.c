@@ -830,6 +830,8 @@ int qwen_hip_decoder_generate(qwen_hip_decoder *d, int first, int n, int *out, i
 
 int qwen_hip_decoder_kv_len(const qwen_hip_decoder *d) { return d ? d->kv_len : QWEN_HIP_EINVAL; }
 
+const qwen_hip_config *qwen_hip_decoder_config(const qwen_hip_decoder *d) { return d ? &d->cfg : NULL; }
+
 int qwen_hip_decoder_set_kv_len(qwen_hip_decoder *d, int n) {
     if (!d || n < 0 || n > d->kv_len) { qk_set_err("set_kv_len: %d outside [0, kv_len]", n); return QWEN_HIP_EINVAL; }
     QK_TRY(use_device(d));

@@ -1,0 +1,137 @@
+"""Checkpoint upload and the streaming driver on the GPU.
+
+* A decoder created from a safetensors checkpoint computes exactly what a
+  decoder given the same arrays through load_layer computes (same bytes on
+  the device: logits equal bit for bit).
+* Streaming with prefix KV reuse (qwen_hip_stream_chunk, the reference's
+  qwen_asr.c:1747-1829) gives the tokens a from-scratch prefill of every chunk
+  gives, except where the top-2 logit margin is a near-tie (the reused and the
+  fresh prefill sum in different orders), the analogue of the reference's
+  reuse-vs-fresh regression check (asr_regression.py:484-493); the reused
+  prefix is exactly the rows that did not change.
+"""
+import numpy as np
+import pytest
+
+from ckpt_util import write_checkpoint
+
+pytestmark = pytest.mark.gpu
+TIE = 1e-3
+
+
+def test_checkpoint_decoder_equals_load_layer(P, qa, gpu, tmp_path):
+    m = P.SynthModel(P.CFG_TINY, seed=6, norm_std=0.1)
+    write_checkpoint(m, str(tmp_path), shards=2, norm_bf16=False)
+    a = qa.Decoder.from_checkpoint(str(tmp_path), 0, 256)
+    b = qa.Decoder(qa.config_from(m.cfg), 0, 256)
+    b.load_model(m)
+    assert (a.cfg.hidden, a.cfg.layers, a.cfg.vocab) == (m.cfg.hidden, m.cfg.layers, m.cfg.vocab)
+    rows, _ = P.prompt_rows(m, 30, 4, seed=2)
+    out = []
+    for d in (a, b):
+        d.set_keep_logits(True)
+        d.prefill(rows[:-1])
+        t = d.forward(rows[-1])
+        lg = [d.read_logits()]
+        toks = [t]
+        for _ in range(6):
+            t = d.forward_token(t)
+            toks.append(t)
+            lg.append(d.read_logits())
+        out.append((toks, np.array(lg)))
+    assert out[0][0] == out[1][0]
+    assert np.array_equal(out[0][1], out[1][1])
+    a.close()
+    b.close()
+
+
+@pytest.fixture(scope="module")
+def dec06(qa, gpu):
+    cfg = qa.preset(0)
+    d = qa.Decoder(cfg, 0, 2048)
+    d.load_synthetic(0, 0.02, 0.0)
+    yield d
+    d.close()
+
+
+def chunk_rows(qa, cfg, emb, head, audio, c, carried):
+    """template head + audio of chunks 0..c + suffix ids + carried text tokens"""
+    e = lambda ids: qa.bf16_to_f32(emb[np.asarray(ids, np.int64)]).reshape(-1, cfg.hidden)
+    parts = [head] + audio[:c + 1] + [e([151644, 77091, 198])]
+    if carried:
+        parts.append(e(carried))
+    return np.ascontiguousarray(np.concatenate(parts), np.float32)
+
+
+def test_stream_reuse_matches_fresh_prefill(qa, dec06):
+    d = dec06
+    cfg = qa.preset(0)
+    emb = qa.synth_bf16(cfg.vocab * cfg.hidden, 0, qa.SYNTH_EMBED).reshape(cfg.vocab, cfg.hidden)
+    head, _, _ = qa.prompt_rows(cfg, 0, 9, emb=emb)
+    audio = [qa.prompt_rows(cfg, 26, 0, audio_chunk=c, emb=emb)[0] for c in range(5)]
+    max_new, rollback = 12, 5
+
+    def run(reuse):
+        st = qa.Stream(d)
+        d.set_kv_len(0)
+        toks, reused, carried = [], [], []
+        for c in range(len(audio)):
+            if not reuse:
+                st.reset()
+            rows = chunk_rows(qa, cfg, emb, head, audio, c, carried)
+            t, r = st.chunk(rows, max_new)
+            toks.append(t)
+            reused.append(r)
+            carried = (carried + t)[:-rollback] if len(carried + t) > rollback else []
+        stats = st.stats()
+        st.close()
+        return toks, reused, stats
+
+    tr, rr, (tot, reu) = run(True)
+    tf, rf, _ = run(False)
+    # chunk c > 0 reuses the template head and the audio of chunks < c
+    assert rr[0] == 0 and all(rr[c] == 9 + 26 * c for c in range(1, len(audio))), rr
+    assert all(r == 0 for r in rf)
+    assert reu == sum(rr) and tot > reu
+    for c in range(len(audio)):
+        assert len(tr[c]) == max_new and len(tf[c]) == max_new
+    if tr != tf:
+        # the first difference must be a near-tie: replay the fresh path there with logits
+        c = next(k for k in range(len(tr)) if tr[k] != tf[k])
+        i = next(k for k in range(max_new) if tr[c][k] != tf[c][k])
+        carried = []
+        for k in range(c):
+            carried = (carried + tf[k])[:-rollback] if len(carried + tf[k]) > rollback else []
+        rows = chunk_rows(qa, cfg, emb, head, audio, c, carried)
+        d.set_kv_len(0)
+        d.set_keep_logits(True)
+        d.prefill(rows[:-1])
+        t = d.forward(rows[-1])
+        for k in range(i):
+            t = d.forward_token(tf[c][k])
+        lg = d.read_logits()
+        d.set_keep_logits(False)
+        s = np.sort(lg)
+        assert s[-1] - s[-2] < TIE, f"chunk {c} token {i}: {tr[c][i]} vs {tf[c][i]}, margin {s[-1] - s[-2]:.2e}"
+    print(f"streaming: {len(audio)} chunks, reused {rr}, identical to fresh prefill: {tr == tf}")
+
+
+def test_stream_token_accounting(qa, dec06):
+    """KV length after a chunk = prefill rows + 1 + kept tokens (every kept
+    token is forwarded, as the reference's loop forwards each appended one);
+    max_new = 0 still forwards the last row."""
+    d = dec06
+    cfg = qa.preset(0)
+    rows, _, _ = qa.prompt_rows(cfg, 20, 6, seed=9)
+    st = qa.Stream(d)
+    d.set_kv_len(0)
+    t, r = st.chunk(rows, 0)
+    assert t == [] and r == 0 and d.kv_len() == len(rows)
+    t, r = st.chunk(rows, 1)
+    assert len(t) == 1 and r == len(rows) - 1 and d.kv_len() == len(rows) + 1
+    t2, r = st.chunk(rows, 7)
+    assert t2[0] == t[0] and len(t2) == 7 and d.kv_len() == len(rows) + 7
+    # the same chunk again reuses every prefill row and reproduces the tokens
+    t3, r = st.chunk(rows, 7)
+    assert t3 == t2 and r == len(rows) - 1
+    st.close()
