@@ -621,7 +621,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
     {
         const PxSplit sp(a.pos0, r);
         wq.load(Wq(0), H, wave, lane);
-        wo.load(Wo(0), PX_QD, wave, lane);
+        if (!DEEP) wo.load(Wo(0), PX_QD, wave, lane);
         px_kv_dma<AB>(kvb[wave], Kc(0), Vc(0), gl, sp.s0 + gid, NG, sp.cend, sp.active);
     }
 
@@ -653,6 +653,9 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     for (int i = 0; i < 16 / NCW; i++) px_put_local(dst + SlabQ::row(wave, i, 0), y[i], T);
                 }
             }
+            // 0.6B spreads its prefetches so no hand-over waits behind more than ~32 KB per CU:
+            // W_o here, W_f after attention, W_d and the next W_q once the O / F hand-overs landed
+            if (DEEP) wo.load(Wo(l), PX_QD, wave, lane);
             // operands of the norm/RoPE step
             float rc = 0.f, rs = 0.f, nw1 = 0.f, nw2 = 0.f;
             if (wave < 3) {
@@ -770,6 +773,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             px_sync();
             px_sync();
             if (S.abort_) return;
+            if (DEEP) wd.load(Wd(l), I, wave, lane);
             if (tid < 256) {
                 // online merge over chunks of 8 splits; a chunk's LDS reads are
                 // issued together (one latency per chunk, not per split)
@@ -813,18 +817,14 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     for (int i = 0; i < SO / 2 / NCW; i++) px_put_global(dst + SlabO::row(wave, i, lane), y[i], T + 2u);
                 }
             }
-            if (DEEP) {
-                wd.load(Wd(l), I, wave, lane);
-                wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
-            } else {
-                wf.load(Wf(l), H, wave, lane);
-            }
+            if (!DEEP) wf.load(Wf(l), H, wave, lane);
             mark(7);
 
             // ---- F: gate|up rows of the group + SwiGLU (qwen_asr_decoder.c:463-466) ----
             px_sync();
             px_sync();
             if (S.abort_) return;
+            if (DEEP) wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
             {
                 float y[RF / NCW];
                 wf.dot(S.xn, y, lane);
@@ -836,9 +836,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                         px_put_local(dst + SlabF::row(wave, i, 0) / 2, swiglu1(y[i], y[i + 1]), T + 4u);
                 }
             }
-            if (DEEP) {
-                wo.load(Wo(l + 1 < L ? l + 1 : 0), PX_QD, wave, lane);
-            } else {
+            if (!DEEP) {
                 wd.load(Wd(l), I, wave, lane);
                 wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
             }
