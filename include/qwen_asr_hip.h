@@ -39,6 +39,7 @@ extern "C" {
 #define QWEN_HIP_VOCAB_SIZE        151936
 #define QWEN_HIP_TOKEN_ENDOFTEXT   151643
 #define QWEN_HIP_TOKEN_IM_END      151645
+#define QWEN_HIP_TOKEN_ASR_TEXT    151704      /* <asr_text>, qwen_asr.h:36 */
 #define QWEN_HIP_MAX_LAYERS        28          /* QWEN_MAX_DEC_LAYERS, qwen_asr.h:27 */
 #define QWEN_HIP_HEAD_DIM          128         /* the only head size the kernels build for */
 
@@ -255,6 +256,27 @@ int qwen_hip_stream_chunk(qwen_hip_stream *st, const float *rows, int n_rows, in
 /* prefill rows seen and reused so far (the reference's prefill_total_tokens /
  * prefill_reused_tokens, :1768-1769) */
 int qwen_hip_stream_stats(const qwen_hip_stream *st, long long *rows_total, long long *rows_reused);
+
+/* ------------------------------------------------------------------------
+ * Token ids -> text: the decode half of the reference tokenizer
+ * (qwen_tokenizer_load / qwen_tokenizer_decode, qwen_asr_tokenizer.c:500-609,
+ * byte-level table :25-47, key decoding :70-121) and the transcript assembly
+ * of the greedy loop (qwen_asr.c:729-754).  Host only.
+ * ------------------------------------------------------------------------ */
+typedef struct qwen_hip_vocab qwen_hip_vocab;
+/* vocab.json (byte-level BPE string -> id); NULL on failure. */
+qwen_hip_vocab *qwen_hip_vocab_load(const char *vocab_json_path);
+void qwen_hip_vocab_free(qwen_hip_vocab *v);
+/* max id + 1 */
+int qwen_hip_vocab_size(const qwen_hip_vocab *v);
+/* the bytes of one token ("" for ids absent from the file, as the reference) */
+const char *qwen_hip_vocab_piece(const qwen_hip_vocab *v, int token_id);
+/* Text of a generated token sequence as the reference's loop builds it:
+ * stop at <|endoftext|> / <|im_end|>, emit pieces only after <asr_text>
+ * (or from the start when past_asr_text != 0, the forced-language / carried-
+ * text case).  Writes at most cap-1 bytes + NUL; returns the full length. */
+long qwen_hip_vocab_transcript(const qwen_hip_vocab *v, const int *tokens, int n, int past_asr_text, char *out,
+                               size_t cap);
 
 /* ------------------------------------------------------------------------
  * Op-level ABI: the qwen_asr_kernels.h operators on device pointers.

@@ -82,6 +82,11 @@ SIGNATURES = [
     ("qwen_hip_stream_reset", None, [_vp]),
     ("qwen_hip_stream_chunk", _i, [_vp, _vp, _i, _i, _vp, _vp]),
     ("qwen_hip_stream_stats", _i, [_vp, _vp, _vp]),
+    ("qwen_hip_vocab_load", _vp, [C.c_char_p]),
+    ("qwen_hip_vocab_free", None, [_vp]),
+    ("qwen_hip_vocab_size", _i, [_vp]),
+    ("qwen_hip_vocab_piece", C.c_char_p, [_vp, _i]),
+    ("qwen_hip_vocab_transcript", C.c_long, [_vp, _vp, _i, _i, C.c_char_p, C.c_size_t]),
     ("qwen_hip_add_inplace", _i, [_vp, _vp, _i, _vp]),
     ("qwen_hip_rms_norm", _i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     ("qwen_hip_rms_norm_per_head", _i, [_vp, _vp, _i, _i, _i, _f, _vp]),
@@ -191,6 +196,41 @@ def prompt_rows(cfg, n_audio, n_ids, seed=0, audio_chunk=0, token_set=0, emb=Non
 
 
 ST_F32, ST_F16, ST_BF16, ST_OTHER = 0, 1, 2, -1
+
+
+class Vocab:
+    """vocab.json for token -> text (host only)."""
+
+    def __init__(self, path):
+        self.h = lib().qwen_hip_vocab_load(os.fsencode(path))
+        if not self.h:
+            raise RuntimeError(f"qwen_hip_vocab_load: {last_error()}")
+
+    def __len__(self):
+        return lib().qwen_hip_vocab_size(self.h)
+
+    def piece(self, token):
+        return lib().qwen_hip_vocab_piece(self.h, int(token))
+
+    def transcript(self, tokens, past_asr_text=False):
+        """bytes of the text the reference's loop assembles from `tokens`"""
+        t = np.ascontiguousarray(tokens, np.int32)
+        n = lib().qwen_hip_vocab_transcript(self.h, _ptr(t), t.size, int(past_asr_text), None, 0)
+        check(n if n < 0 else 0, "vocab_transcript")
+        buf = C.create_string_buffer(n + 1)
+        lib().qwen_hip_vocab_transcript(self.h, _ptr(t), t.size, int(past_asr_text), buf, n + 1)
+        return buf.raw[:n]
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().qwen_hip_vocab_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Checkpoint:
