@@ -243,6 +243,56 @@ __device__ __forceinline__ void px_fold(const float (&q)[2][8], float4 k0, float
     }
 }
 
+// px_fold for NB positions at once: the NB scores of a head are independent
+// dot products, then one max / rescale and an exp-weighted sum, so the online
+// softmax pays one dependent update per batch instead of one per position.
+// in[i] false: position i is skipped (its k/v may be anything finite).
+template <int NB>
+__device__ __forceinline__ void px_fold_n(const float (&q)[2][8], const float4 (&k)[NB][2], const float4 (&v)[NB][2],
+                                          const bool (&in)[NB], float scale, float (&m)[2], float (&l)[2],
+                                          float (&o)[2][8]) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float sc[NB];
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const float kv[8] = {k[i][0].x, k[i][0].y, k[i][0].z, k[i][0].w, k[i][1].x, k[i][1].y, k[i][1].z, k[i][1].w};
+            float d = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) d = fmaf(q[h][j], kv[j], d);
+            sc[i] = d;
+        }
+#pragma unroll
+        for (int i = 0; i < NB; i++) sc[i] = group_sum<16>(sc[i]);
+        float mn = m[h];
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            sc[i] = in[i] ? sc[i] * scale : -INFINITY;
+            mn = fmaxf(mn, sc[i]);
+        }
+        // mn == m[h] covers the batch with no position in and the start (m = -inf)
+        const float corr = (mn == m[h]) ? 1.0f : __expf(m[h] - mn);
+        float p[NB], ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            p[i] = in[i] ? __expf(sc[i] - mn) : 0.0f;
+            ps += p[i];
+        }
+        l[h] = fmaf(l[h], corr, ps);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float acc = o[h][j] * corr;
+#pragma unroll
+            for (int i = 0; i < NB; i++) {
+                const float vj = j < 4 ? (&v[i][0].x)[j] : (&v[i][1].x)[j - 4];
+                acc = fmaf(p[i], vj, acc);
+            }
+            o[h][j] = acc;
+        }
+        m[h] = mn;
+    }
+}
+
 // The split of positions [0, pos] a block of the group works on.
 struct PxSplit {
     int nsplit, s0, s1, cend;
@@ -715,18 +765,27 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     for (int j = 0; j < 8; j++) o[h][j] = 0.f;
                 // the first AB positions of each group were DMA'd into LDS by this wave
                 px_wait_loads();
+                {
+                    float4 kk[AB][2], vv[AB][2];
+                    bool in[AB];
 #pragma unroll
-                for (int j = 0; j < AB; j++)
-                    if (sp.s0 + gid + NG * j < sp.cend)
-                        px_fold(q, px_u2f(kvb[wave][j][0][lane]), px_u2f(kvb[wave][j][1][lane]),
-                                px_u2f(kvb[wave][j][2][lane]), px_u2f(kvb[wave][j][3][lane]), a.scale, m, lsum, o);
+                    for (int j = 0; j < AB; j++) {
+                        in[j] = sp.s0 + gid + NG * j < sp.cend;
+                        kk[j][0] = px_u2f(kvb[wave][j][0][lane]);
+                        kk[j][1] = px_u2f(kvb[wave][j][1][lane]);
+                        vv[j][0] = px_u2f(kvb[wave][j][2][lane]);
+                        vv[j][1] = px_u2f(kvb[wave][j][3][lane]);
+                    }
+                    px_fold_n<AB>(q, kk, vv, in, a.scale, m, lsum, o);
+                }
                 // longer splits continue in register batches
                 for (int pb = sp.s0 + gid + NG * AB; pb < sp.cend; pb += NG * AB) {
                     PxKv<AB> kv;
                     kv.load(kcl, vcl, gl, pb, NG, sp.cend);
+                    bool in[AB];
 #pragma unroll
-                    for (int j = 0; j < AB; j++)
-                        if (pb + NG * j < sp.cend) px_fold(q, kv.k[j][0], kv.k[j][1], kv.v[j][0], kv.v[j][1], a.scale, m, lsum, o);
+                    for (int j = 0; j < AB; j++) in[j] = pb + NG * j < sp.cend;
+                    px_fold_n<AB>(q, kv.k, kv.v, in, a.scale, m, lsum, o);
                 }
                 if (sp.last && gid == 0) {   // position pos: this step's k/v
                     const float4 *kn = reinterpret_cast<const float4 *>(&S.kr[gl * 8]);
