@@ -92,7 +92,7 @@ __device__ __forceinline__ void px_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n
 // dst[i] = value.  PER words per lane in flight per pass.  False on timeout or
 // when another block raised an error.
 template <int PER, typename Addr>
-__device__ bool px_poll(Addr addr, int n, unsigned tag, float *dst, unsigned *err, int lane) {
+__device__ bool px_poll(Addr addr, int n, unsigned tag, float *dst, unsigned *err, int lane, float *ssq = nullptr) {
     for (int base = 0; base < n; base += 64 * PER) {
         for (unsigned spin = 1;; spin++) {
             u64 w[PER];
@@ -108,7 +108,11 @@ __device__ bool px_poll(Addr addr, int n, unsigned tag, float *dst, unsigned *er
 #pragma unroll
                 for (int j = 0; j < PER; j++) {
                     const int i = base + j * 64 + lane;
-                    if (i < n) dst[i] = __uint_as_float((unsigned)w[j]);
+                    if (i < n) {
+                        const float v = __uint_as_float((unsigned)w[j]);
+                        dst[i] = v;
+                        if (ssq) *ssq = fmaf(v, v, *ssq);   // this lane's share of sum(x^2), in px_rmsnorm's order
+                    }
                 }
                 break;
             }
@@ -360,7 +364,7 @@ __device__ __forceinline__ const char *px_layer(const qk_persist_args &a, int l)
 // ---------------------------------------------------------------------------
 template <int H, int I, int NCW>
 __device__ bool px_x_update(const qk_persist_args &a, PxShared<H, I, NCW> &S, const u64 *yp, unsigned ty, u64 *xl,
-                            unsigned tx, int lane, unsigned long long *tr_hop = nullptr) {
+                            unsigned tx, int lane, float &ssq, unsigned long long *tr_hop = nullptr) {
     constexpr int SO = PxShared<H, I, NCW>::SO;
     const int r = S.r;
     // this block's slice of the 8 split-K partials
@@ -375,19 +379,26 @@ __device__ bool px_x_update(const qk_persist_args &a, PxShared<H, I, NCW> &S, co
     }
     // the XCD's whole new residual
     auto whole = [&](int i) { return xl + i; };
-    return px_poll<(H / 64 < 16 ? H / 64 : 16)>(whole, H, tx, S.xs, a.err, lane);
+    ssq = 0.0f;
+    return px_poll<(H / 64 < 16 ? H / 64 : 16)>(whole, H, tx, S.xs, a.err, lane, &ssq);
 }
 
 // xn = rms_norm(xs) * w (qwen_rms_norm, qwen_asr_kernels.c:750-809); w was
 // DMA'd into LDS by px_load_norm and has landed (the caller's polls waited
 // for every load of this wave).
+// ssq_lane >= 0: this lane's share of sum(x^2) already accumulated (by the
+// poll that wrote xs, same elements in the same order); < 0: compute it here.
 template <int H, int I, int NCW>
-__device__ void px_rmsnorm(const qk_persist_args &a, PxShared<H, I, NCW> &S, const float *w, int lane) {
-    float ss = 0.0f;
+__device__ void px_rmsnorm(const qk_persist_args &a, PxShared<H, I, NCW> &S, const float *w, int lane,
+                           float ssq_lane = -1.0f) {
+    float ss = ssq_lane;
+    if (ss < 0.0f) {
+        ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < H / 64; j++) {
-        const float v = S.xs[j * 64 + lane];
-        ss = fmaf(v, v, ss);
+        for (int j = 0; j < H / 64; j++) {
+            const float v = S.xs[j * 64 + lane];
+            ss = fmaf(v, v, ss);
+        }
     }
     ss = wave_sum(ss);
     const float rinv = 1.0f / sqrtf(ss / (float)H + a.eps);
@@ -442,6 +453,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             const int par = l & 1;
             const char *lb = px_layer<H>(a, l);
             bool ok = true;
+            float ssq = -1.0f;
             // ---- Q: input (embedding / x_in) or x += down partials; input norm ----
             px_load_norm<H>((const float *)(lb + a.off_nin), S.nw, lane);
             px_sync();
@@ -464,11 +476,11 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             } else {
                 const int pp = (l - 1) & 1;
                 ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T - QK_PX_TPL + 5u, a.xlb + (pp * WG + g) * H,
-                                            T - QK_PX_TPL + 6u, lane, tr ? tr + QK_PX_TRACE_XU + 2 * l : nullptr);
+                                            T - QK_PX_TPL + 6u, lane, ssq, tr ? tr + QK_PX_TRACE_XU + 2 * l : nullptr);
             }
             if (ok) {
                 px_wait_loads();
-                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane);
+                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane, l == 0 ? -1.0f : ssq);
             }
             mark(10 * l + 1);
             if (lane == 0) S.abort_ = !ok;
@@ -511,10 +523,10 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             px_sync();
             mark(10 * l + 6);
             ok = px_x_update<H, I, NCW>(a, S, a.xo + (par * WG) * H, T + 2u, a.xla + (par * WG + g) * H, T + 3u, lane,
-                                        tr ? tr + QK_PX_TRACE_XU + 2 * l + 1 : nullptr);
+                                        ssq, tr ? tr + QK_PX_TRACE_XU + 2 * l + 1 : nullptr);
             if (ok) {
                 px_wait_loads();
-                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane);
+                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane, ssq);
             }
             mark(10 * l + 7);
             if (lane == 0) S.abort_ = !ok;
@@ -541,11 +553,12 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             px_load_norm<H>(a.fnorm, S.nw, lane);
             px_sync();
             mark(10 * L + 0);
+            float ssq = -1.0f;
             bool ok = px_x_update<H, I, NCW>(a, S, a.xd + (pp * WG) * H, T + 5u, a.xlb + (pp * WG + g) * H, T + 6u, lane,
-                                             tr ? tr + QK_PX_TRACE_XU + 2 * L : nullptr);
+                                             ssq, tr ? tr + QK_PX_TRACE_XU + 2 * L : nullptr);
             if (ok) {
                 px_wait_loads();
-                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane);
+                px_rmsnorm<H, I, NCW>(a, S, S.nw, lane, ssq);
                 if (b == 0 && a.hidden_out)
                     for (int i = lane; i < H; i += 64) a.hidden_out[i] = S.xn[i];
             }
