@@ -47,14 +47,26 @@ __device__ __forceinline__ f32x4 mfma_f32_4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// max / sum over lanes l, l^16, l^32, l^48 (the four lanes holding one
+// query's scores) with row swaps at VALU latency (no LDS crossbar)
 __device__ __forceinline__ float xor_max16_32(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, QK_WAVE));
-    return fmaxf(v, __shfl_xor(v, 32, QK_WAVE));
+    float a = v, b = v;
+    swap16(a, b);
+    v = fmaxf(a, b);
+    a = v;
+    b = v;
+    swap32(a, b);
+    return fmaxf(a, b);
 }
 
 __device__ __forceinline__ float xor_sum16_32(float v) {
-    v += __shfl_xor(v, 16, QK_WAVE);
-    return v + __shfl_xor(v, 32, QK_WAVE);
+    float a = v, b = v;
+    swap16(a, b);
+    v = a + b;
+    a = v;
+    b = v;
+    swap32(a, b);
+    return a + b;
 }
 
 // The next K/V tile, held in registers while the current one is consumed.
@@ -164,20 +176,19 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
         for (int qt = 0; qt < 2; qt++)
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) s[qt][kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        // consecutive MFMAs go to the 4 independent (qt, kt) accumulators
 #pragma unroll
         for (int b = 0; b < 8; b++) {
             float4 kf[2];
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) kf[kt] = *reinterpret_cast<const float4 *>(&sK[16 * kt + ql][16 * b + 4 * kq]);
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++)
+            for (int c = 0; c < 4; c++)
 #pragma unroll
-                for (int qt = 0; qt < 2; qt++) {
-                    s[qt][kt] = mfma_f32_4(kf[kt].x, q[qt][b].x, s[qt][kt]);
-                    s[qt][kt] = mfma_f32_4(kf[kt].y, q[qt][b].y, s[qt][kt]);
-                    s[qt][kt] = mfma_f32_4(kf[kt].z, q[qt][b].z, s[qt][kt]);
-                    s[qt][kt] = mfma_f32_4(kf[kt].w, q[qt][b].w, s[qt][kt]);
-                }
+                for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                    for (int qt = 0; qt < 2; qt++)
+                        s[qt][kt] = mfma_f32_4((&kf[kt].x)[c], (&q[qt][b].x)[c], s[qt][kt]);
         }
 
         // online softmax (causal mask: key <= q_offset + query; keys past ks1 belong elsewhere)
@@ -208,23 +219,29 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
             sum = xor_sum16_32(sum);
             l[qt] = fmaf(l[qt], corr, sum);
             m[qt] = mn;
+            if (!__all(corr == 1.0f)) {          // the running max moved for some query of the wave
 #pragma unroll
-            for (int dt = 0; dt < 8; dt++) o[qt][dt] *= corr;
+                for (int dt = 0; dt < 8; dt++) o[qt][dt] *= corr;
+            }
         }
 
         // O^T[d][query] += V^T[d][key] P^T[key][query]
+        // consecutive MFMAs go to 8 independent (qt, dt) accumulators
 #pragma unroll
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int dt = 0; dt < 8; dt++) {
-                const float4 vf = *reinterpret_cast<const float4 *>(&sVt[16 * dt + ql][16 * kt + 4 * kq]);
+            for (int dh = 0; dh < 8; dh += 4) {
+                float4 vf[4];
 #pragma unroll
-                for (int qt = 0; qt < 2; qt++) {
-                    o[qt][dt] = mfma_f32_4(vf.x, p[qt][kt][0], o[qt][dt]);
-                    o[qt][dt] = mfma_f32_4(vf.y, p[qt][kt][1], o[qt][dt]);
-                    o[qt][dt] = mfma_f32_4(vf.z, p[qt][kt][2], o[qt][dt]);
-                    o[qt][dt] = mfma_f32_4(vf.w, p[qt][kt][3], o[qt][dt]);
-                }
+                for (int d = 0; d < 4; d++)
+                    vf[d] = *reinterpret_cast<const float4 *>(&sVt[16 * (dh + d) + ql][16 * kt + 4 * kq]);
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+#pragma unroll
+                    for (int d = 0; d < 4; d++)
+#pragma unroll
+                        for (int qt = 0; qt < 2; qt++)
+                            o[qt][dh + d] = mfma_f32_4((&vf[d].x)[c], p[qt][kt][c], o[qt][dh + d]);
             }
     }
     if (!wave_on) return;
