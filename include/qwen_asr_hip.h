@@ -258,6 +258,66 @@ int qwen_hip_stream_chunk(qwen_hip_stream *st, const float *rows, int n_rows, in
 int qwen_hip_stream_stats(const qwen_hip_stream *st, long long *rows_total, long long *rows_reused);
 
 /* ------------------------------------------------------------------------
+ * Audio encoder: qwen_encoder_load / qwen_encoder_forward (reference
+ * qwen_asr_encoder.c:67-372) on the fp32 matrix cores.  mel [128][frames] ->
+ * [tokens][output_dim] rows, the input the decoder's prefill consumes.
+ * ------------------------------------------------------------------------ */
+#define QWEN_HIP_ENC_MAX_LAYERS 24        /* QWEN_MAX_ENC_LAYERS, qwen_asr.h:26 */
+
+/* The encoder fields of qwen_config_t (qwen_asr.h:48-57) */
+typedef struct {
+    int d_model;         /* 896 (0.6B) or 1024 (1.7B) */
+    int layers;          /* 18 or 24 */
+    int heads;           /* 14 or 16 */
+    int head_dim;        /* 64 */
+    int ffn_dim;         /* 3584 or 4096 */
+    int output_dim;      /* 1024 or 2048 (the decoder's hidden) */
+    int chunk_size;      /* mel frames per stem chunk: 100 */
+    int n_window_infer;  /* 800: attention windows of n_window_infer / chunk_size chunks */
+} qwen_hip_enc_config;
+
+/* the reference's two presets (detect_config, qwen_asr.c:135-191) */
+void qwen_hip_enc_config_preset(qwen_hip_enc_config *cfg, int model_b);
+
+/* Host weights, fp32 as qwen_enc_layer_t / qwen_encoder_t hold them after
+ * loading (qwen_asr.h:75-125); matrices row-major [out][in]. */
+typedef struct {
+    const float *wq, *bq, *wk, *bk, *wv, *bv, *wo, *bo;   /* [d][d], [d] */
+    const float *ln1_w, *ln1_b;                           /* self_attn_layer_norm [d] */
+    const float *fc1_w, *fc1_b, *fc2_w, *fc2_b;           /* [ffn][d], [ffn], [d][ffn], [d] */
+    const float *ln2_w, *ln2_b;                           /* final_layer_norm [d] */
+} qwen_hip_enc_layer_weights;
+
+typedef struct {
+    const float *conv1_w, *conv1_b;      /* [480][1][3][3], [480] */
+    const float *conv2_w, *conv2_b;      /* [480][480][3][3], [480] */
+    const float *conv3_w, *conv3_b;
+    const float *conv_out_w;             /* [d][480*16] */
+    const float *ln_post_w, *ln_post_b;  /* [d] */
+    const float *proj1_w, *proj1_b;      /* [d][d], [d] */
+    const float *proj2_w, *proj2_b;      /* [output_dim][d], [output_dim] */
+} qwen_hip_enc_stem_weights;
+
+typedef struct qwen_hip_encoder qwen_hip_encoder;
+qwen_hip_encoder *qwen_hip_encoder_create(const qwen_hip_enc_config *cfg, int device);
+void qwen_hip_encoder_destroy(qwen_hip_encoder *enc);
+int qwen_hip_encoder_load_layer(qwen_hip_encoder *enc, int layer, const qwen_hip_enc_layer_weights *w);
+int qwen_hip_encoder_load_stem(qwen_hip_encoder *enc, const qwen_hip_enc_stem_weights *w);
+/* seeded synthetic encoder (qwen_synth ids QWEN_SYNTH_ENC): bf16 N(0, wstd)
+ * matrices widened to fp32 (conv1: N(0, 10 wstd)), fp32 biases N(0, wstd),
+ * LayerNorm weights 1 + N(0, 0.1), LayerNorm biases N(0, 0.02) */
+int qwen_hip_encoder_load_synthetic(qwen_hip_encoder *enc, uint64_t seed, double wstd);
+/* tokens the encoder produces for mel_frames frames (:193-214) */
+int qwen_hip_encoder_tokens(const qwen_hip_enc_config *cfg, int mel_frames);
+/* qwen_encoder_forward: mel (host) [128][mel_frames] -> out (host)
+ * [tokens][output_dim]; returns tokens, negative on error. */
+int qwen_hip_encoder_forward(qwen_hip_encoder *enc, const float *mel, int mel_frames, float *out);
+/* Device in, device out: *d_out points at the encoder's own output buffer
+ * (valid until the next call), ready for qwen_hip_decoder_prefill_device. */
+int qwen_hip_encoder_forward_device(qwen_hip_encoder *enc, const float *d_mel, int mel_frames, const float **d_out);
+hipStream_t qwen_hip_encoder_stream(const qwen_hip_encoder *enc);
+
+/* ------------------------------------------------------------------------
  * Token ids -> text: the decode half of the reference tokenizer
  * (qwen_tokenizer_load / qwen_tokenizer_decode, qwen_asr_tokenizer.c:500-609,
  * byte-level table :25-47, key decoding :70-121) and the transcript assembly

@@ -24,6 +24,21 @@ enum {
     QWEN_SYNTH_QNORM, QWEN_SYNTH_KNORM, QWEN_SYNTH_INNORM, QWEN_SYNTH_POSTNORM
 };
 #define QWEN_SYNTH_AUDIO(chunk) (500000u + (uint64_t)(chunk))
+/* Tensor ids for an audio encoder: layer l < 30, the stem / projections as
+ * "layer" 30; the mel input of a workload. */
+#define QWEN_SYNTH_ENC(l, f)    (700000u + 32u * (uint64_t)(l) + (uint64_t)(f))
+#define QWEN_SYNTH_ENC_STEM     30u
+#define QWEN_SYNTH_MEL(set)     (750000u + (uint64_t)(set))
+enum {
+    QWEN_SYNTH_E_WQ = 0, QWEN_SYNTH_E_BQ, QWEN_SYNTH_E_WK, QWEN_SYNTH_E_BK, QWEN_SYNTH_E_WV, QWEN_SYNTH_E_BV,
+    QWEN_SYNTH_E_WO, QWEN_SYNTH_E_BO, QWEN_SYNTH_E_LN1W, QWEN_SYNTH_E_LN1B, QWEN_SYNTH_E_FC1W, QWEN_SYNTH_E_FC1B,
+    QWEN_SYNTH_E_FC2W, QWEN_SYNTH_E_FC2B, QWEN_SYNTH_E_LN2W, QWEN_SYNTH_E_LN2B
+};
+enum {
+    QWEN_SYNTH_S_CONV1W = 0, QWEN_SYNTH_S_CONV1B, QWEN_SYNTH_S_CONV2W, QWEN_SYNTH_S_CONV2B, QWEN_SYNTH_S_CONV3W,
+    QWEN_SYNTH_S_CONV3B, QWEN_SYNTH_S_CONVOUT, QWEN_SYNTH_S_LNPW, QWEN_SYNTH_S_LNPB, QWEN_SYNTH_S_P1W,
+    QWEN_SYNTH_S_P1B, QWEN_SYNTH_S_P2W, QWEN_SYNTH_S_P2B
+};
 #define QWEN_SYNTH_TOKENS(set)  (600000u + (uint64_t)(set))
 
 uint64_t qwen_synth_key(uint64_t seed, uint64_t tensor_id);

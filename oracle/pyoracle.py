@@ -356,3 +356,102 @@ def prompt_rows(model: SynthModel, n_audio, n_ids, seed=0, audio_chunk=0, token_
     rows = np.concatenate([np.array(head, np.float32).reshape(-1, c.hidden), audio,
                            np.array(tail, np.float32).reshape(-1, c.hidden)], axis=0)
     return np.ascontiguousarray(rows, np.float32), ids
+
+
+# ---------------------------------------------------------------------------
+# Audio encoder (reference qwen_asr_encoder.c) -- synthetic weights and the
+# compiled reference's forward pass.
+# ---------------------------------------------------------------------------
+ENC_FIELDS = ("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "ln1_w", "ln1_b",
+              "fc1_w", "fc1_b", "fc2_w", "fc2_b", "ln2_w", "ln2_b")
+STEM_FIELDS = ("conv1_w", "conv1_b", "conv2_w", "conv2_b", "conv3_w", "conv3_b", "conv_out_w",
+               "ln_post_w", "ln_post_b", "proj1_w", "proj1_b", "proj2_w", "proj2_b")
+
+
+def synth_enc_id(layer, field):
+    return 700000 + 32 * layer + field
+
+
+def synth_mel_id(s):
+    return 750000 + s
+
+
+class SynthEncoder:
+    """The seeded synthetic encoder of qwen_hip_encoder_load_synthetic, as host
+    fp32 arrays: bf16 N(0, wstd) matrices widened (conv1 N(0, 10 wstd)), fp32
+    biases N(0, wstd), LayerNorm weights N(1, 0.1) and biases N(0, 0.02)."""
+
+    def __init__(self, cfg, seed=0, wstd=0.02):
+        d, f, o = cfg.d_model, cfg.ffn_dim, cfg.output_dim
+        mat = lambda n, tid, std: bf16_to_f32(synth_bf16(n, seed, tid, std)).astype(np.float32)
+        vec = lambda n, tid, mean, std: synth_f32(n, seed, tid, std, mean)
+        self.cfg = cfg
+        self.layers = []
+        for l in range(cfg.layers):
+            i = lambda k: synth_enc_id(l, k)
+            self.layers.append([
+                mat(d * d, i(0), wstd).reshape(d, d), vec(d, i(1), 0, wstd),
+                mat(d * d, i(2), wstd).reshape(d, d), vec(d, i(3), 0, wstd),
+                mat(d * d, i(4), wstd).reshape(d, d), vec(d, i(5), 0, wstd),
+                mat(d * d, i(6), wstd).reshape(d, d), vec(d, i(7), 0, wstd),
+                vec(d, i(8), 1.0, 0.1), vec(d, i(9), 0, 0.02),
+                mat(f * d, i(10), wstd).reshape(f, d), vec(f, i(11), 0, wstd),
+                mat(d * f, i(12), wstd).reshape(d, f), vec(d, i(13), 0, wstd),
+                vec(d, i(14), 1.0, 0.1), vec(d, i(15), 0, 0.02)])
+        s = lambda k: synth_enc_id(30, k)
+        self.stem = [mat(480 * 9, s(0), wstd * 10), vec(480, s(1), 0, wstd),
+                     mat(480 * 4320, s(2), wstd), vec(480, s(3), 0, wstd),
+                     mat(480 * 4320, s(4), wstd), vec(480, s(5), 0, wstd),
+                     mat(d * 7680, s(6), wstd).reshape(d, 7680), vec(d, s(7), 1.0, 0.1), vec(d, s(8), 0, 0.02),
+                     mat(d * d, s(9), wstd).reshape(d, d), vec(d, s(10), 0, wstd),
+                     mat(o * d, s(11), wstd).reshape(o, d), vec(o, s(12), 0, wstd)]
+
+
+def synth_mel(frames, seed=0, s=0):
+    return synth_f32(128 * frames, seed, synth_mel_id(s)).reshape(128, frames)
+
+
+class RefEncoder:
+    """qwen_encoder_forward of the reference (oracle/_ref), on a SynthEncoder's arrays."""
+
+    def __init__(self, model: SynthEncoder):
+        lib = ref_lib()
+        if lib is None:
+            raise RuntimeError("oracle/_ref is not built")
+        lib.ref_enc_create.restype = C.c_void_p
+        lib.ref_enc_create.argtypes = [C.c_int] * 8
+        lib.ref_enc_set_layer.argtypes = [C.c_void_p, C.c_int] + [_f32p] * 16
+        lib.ref_enc_set_stem.argtypes = [C.c_void_p] + [_f32p] * 13
+        lib.ref_enc_forward.argtypes = [C.c_void_p, _f32p, C.c_int, _f32p, C.c_long]
+        lib.ref_enc_time.argtypes = [C.c_void_p, _f32p, C.c_int, _f32p, C.c_long]
+        lib.ref_enc_time.restype = C.c_double
+        lib.ref_enc_destroy.argtypes = [C.c_void_p]
+        self.lib, self.model, c = lib, model, model.cfg
+        self.h = lib.ref_enc_create(c.d_model, c.layers, c.heads, c.head_dim, c.ffn_dim, c.output_dim,
+                                    c.chunk_size, c.n_window_infer)
+        self._keep = []
+        for l, arrs in enumerate(model.layers):
+            arrs = [np.ascontiguousarray(a, np.float32) for a in arrs]
+            self._keep += arrs
+            assert lib.ref_enc_set_layer(self.h, l, *arrs) == 0
+        arrs = [np.ascontiguousarray(a, np.float32) for a in model.stem]
+        self._keep += arrs
+        lib.ref_enc_set_stem(self.h, *arrs)
+
+    def forward(self, mel, tokens):
+        mel = np.ascontiguousarray(mel, np.float32)
+        out = np.empty((tokens, self.model.cfg.output_dim), np.float32)
+        T = self.lib.ref_enc_forward(self.h, mel, mel.shape[1], out, out.size)
+        assert T == tokens, (T, tokens)
+        return out
+
+    def time(self, mel, tokens):
+        mel = np.ascontiguousarray(mel, np.float32)
+        out = np.empty((tokens, self.model.cfg.output_dim), np.float32)
+        return self.lib.ref_enc_time(self.h, mel, mel.shape[1], out, out.size)
+
+    def __del__(self):
+        try:
+            self.lib.ref_enc_destroy(self.h)
+        except Exception:
+            pass

@@ -171,3 +171,74 @@ void ref_destroy(void *mp) {
     free(ctx);
     free(m);
 }
+
+/* ------------------------------------------------------------------------
+ * The reference's audio encoder (qwen_encoder_forward, qwen_asr_encoder.c:
+ * 171-372).  qwen_encoder_load (:67-168) reads safetensors; here the
+ * qwen_encoder_t fields point at caller-owned fp32 buffers instead (the
+ * loader's own output format: bf16 matrices widened to fp32).
+ * ------------------------------------------------------------------------ */
+void *ref_enc_create(int d_model, int layers, int heads, int head_dim, int ffn, int out_dim, int chunk,
+                     int n_window_infer) {
+    if (layers > QWEN_MAX_ENC_LAYERS) return NULL;
+    qwen_ctx_t *ctx = (qwen_ctx_t *)calloc(1, sizeof(qwen_ctx_t));
+    if (!ctx) return NULL;
+    qwen_config_t *c = &ctx->config;
+    c->enc_d_model = d_model;
+    c->enc_layers = layers;
+    c->enc_heads = heads;
+    c->enc_head_dim = head_dim;
+    c->enc_ffn_dim = ffn;
+    c->enc_output_dim = out_dim;
+    c->enc_chunk_size = chunk;
+    c->enc_n_window = chunk / 2;
+    c->enc_n_window_infer = n_window_infer;
+    c->enc_conv_proj_dim = QWEN_CONV_HIDDEN * 16;
+    return ctx;
+}
+
+int ref_enc_set_layer(void *p, int l, float *wq, float *bq, float *wk, float *bk, float *wv, float *bv, float *wo,
+                      float *bo, float *ln1w, float *ln1b, float *fc1w, float *fc1b, float *fc2w, float *fc2b,
+                      float *ln2w, float *ln2b) {
+    qwen_ctx_t *ctx = (qwen_ctx_t *)p;
+    if (l < 0 || l >= ctx->config.enc_layers) return -1;
+    qwen_enc_layer_t *y = &ctx->encoder.layers[l];
+    y->wq_weight = wq; y->wq_bias = bq; y->wk_weight = wk; y->wk_bias = bk;
+    y->wv_weight = wv; y->wv_bias = bv; y->wo_weight = wo; y->wo_bias = bo;
+    y->attn_norm_weight = ln1w; y->attn_norm_bias = ln1b;
+    y->fc1_weight = fc1w; y->fc1_bias = fc1b; y->fc2_weight = fc2w; y->fc2_bias = fc2b;
+    y->ffn_norm_weight = ln2w; y->ffn_norm_bias = ln2b;
+    return 0;
+}
+
+int ref_enc_set_stem(void *p, float *c1w, float *c1b, float *c2w, float *c2b, float *c3w, float *c3b, float *cow,
+                     float *lnpw, float *lnpb, float *p1w, float *p1b, float *p2w, float *p2b) {
+    qwen_encoder_t *e = &((qwen_ctx_t *)p)->encoder;
+    e->conv1_weight = c1w; e->conv1_bias = c1b; e->conv2_weight = c2w; e->conv2_bias = c2b;
+    e->conv3_weight = c3w; e->conv3_bias = c3b; e->conv_out_weight = cow;
+    e->ln_post_weight = lnpw; e->ln_post_bias = lnpb;
+    e->proj1_weight = p1w; e->proj1_bias = p1b; e->proj2_weight = p2w; e->proj2_bias = p2b;
+    return 0;
+}
+
+/* mel [128][frames] -> out [tokens][out_dim] (cap floats); returns tokens, -1 on failure */
+int ref_enc_forward(void *p, const float *mel, int frames, float *out, long cap) {
+    qwen_ctx_t *ctx = (qwen_ctx_t *)p;
+    int T = 0;
+    float *o = qwen_encoder_forward(ctx, mel, frames, &T);
+    if (!o) return -1;
+    if ((long)T * ctx->config.enc_output_dim > cap) { free(o); return -1; }
+    memcpy(out, o, (size_t)T * ctx->config.enc_output_dim * sizeof(float));
+    free(o);
+    return T;
+}
+
+double ref_enc_time(void *p, const float *mel, int frames, float *out, long cap) {
+    struct timespec a, b;
+    clock_gettime(CLOCK_MONOTONIC, &a);
+    int T = ref_enc_forward(p, mel, frames, out, cap);
+    clock_gettime(CLOCK_MONOTONIC, &b);
+    return T < 0 ? -1.0 : (b.tv_sec - a.tv_sec) + 1e-9 * (b.tv_nsec - a.tv_nsec);
+}
+
+void ref_enc_destroy(void *p) { free(p); }

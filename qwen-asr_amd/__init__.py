@@ -82,6 +82,16 @@ SIGNATURES = [
     ("qwen_hip_stream_reset", None, [_vp]),
     ("qwen_hip_stream_chunk", _i, [_vp, _vp, _i, _i, _vp, _vp]),
     ("qwen_hip_stream_stats", _i, [_vp, _vp, _vp]),
+    ("qwen_hip_enc_config_preset", None, [_vp, _i]),
+    ("qwen_hip_encoder_create", _vp, [_vp, _i]),
+    ("qwen_hip_encoder_destroy", None, [_vp]),
+    ("qwen_hip_encoder_load_layer", _i, [_vp, _i, _vp]),
+    ("qwen_hip_encoder_load_stem", _i, [_vp, _vp]),
+    ("qwen_hip_encoder_load_synthetic", _i, [_vp, _u64, _d]),
+    ("qwen_hip_encoder_tokens", _i, [_vp, _i]),
+    ("qwen_hip_encoder_forward", _i, [_vp, _vp, _i, _vp]),
+    ("qwen_hip_encoder_forward_device", _i, [_vp, _vp, _i, _vp]),
+    ("qwen_hip_encoder_stream", _vp, [_vp]),
     ("qwen_hip_vocab_load", _vp, [C.c_char_p]),
     ("qwen_hip_vocab_free", None, [_vp]),
     ("qwen_hip_vocab_size", _i, [_vp]),
@@ -196,6 +206,84 @@ def prompt_rows(cfg, n_audio, n_ids, seed=0, audio_chunk=0, token_set=0, emb=Non
 
 
 ST_F32, ST_F16, ST_BF16, ST_OTHER = 0, 1, 2, -1
+
+
+class EncConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("d_model", "layers", "heads", "head_dim", "ffn_dim", "output_dim",
+                                       "chunk_size", "n_window_infer")]
+
+
+class EncLayerWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "ln1_w", "ln1_b",
+                                          "fc1_w", "fc1_b", "fc2_w", "fc2_b", "ln2_w", "ln2_b")]
+
+
+class EncStemWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("conv1_w", "conv1_b", "conv2_w", "conv2_b", "conv3_w", "conv3_b",
+                                          "conv_out_w", "ln_post_w", "ln_post_b", "proj1_w", "proj1_b",
+                                          "proj2_w", "proj2_b")]
+
+
+def enc_preset(model_b):
+    cfg = EncConfig()
+    lib().qwen_hip_enc_config_preset(C.byref(cfg), int(model_b))
+    return cfg
+
+
+class Encoder:
+    """The audio encoder on one GPU (mel [128][frames] -> rows [tokens][output_dim])."""
+
+    def __init__(self, cfg: EncConfig, device=0):
+        self.cfg = cfg
+        self.h = lib().qwen_hip_encoder_create(C.byref(cfg), device)
+        if not self.h:
+            raise RuntimeError(f"qwen_hip_encoder_create: {last_error()}")
+
+    def load_synthetic(self, seed=0, wstd=0.02):
+        check(lib().qwen_hip_encoder_load_synthetic(self.h, seed, wstd), "encoder_load_synthetic")
+
+    def load_layer(self, l, arrays):
+        """arrays: the 16 fp32 arrays of EncLayerWeights in field order"""
+        arrs = [np.ascontiguousarray(a, np.float32) for a in arrays]
+        w = EncLayerWeights(*[a.ctypes.data for a in arrs])
+        check(lib().qwen_hip_encoder_load_layer(self.h, l, C.byref(w)), f"encoder_load_layer {l}")
+
+    def load_stem(self, arrays):
+        arrs = [np.ascontiguousarray(a, np.float32) for a in arrays]
+        w = EncStemWeights(*[a.ctypes.data for a in arrs])
+        check(lib().qwen_hip_encoder_load_stem(self.h, C.byref(w)), "encoder_load_stem")
+
+    def tokens(self, frames):
+        return lib().qwen_hip_encoder_tokens(C.byref(self.cfg), int(frames))
+
+    def forward(self, mel):
+        mel = np.ascontiguousarray(mel, np.float32)
+        frames = mel.shape[1]
+        out = np.empty((self.tokens(frames), self.cfg.output_dim), np.float32)
+        T = lib().qwen_hip_encoder_forward(self.h, _ptr(mel), frames, _ptr(out))
+        check(T if T < 0 else 0, "encoder_forward")
+        return out[:T]
+
+    def forward_device(self, d_mel_ptr, frames):
+        """(tokens, device pointer of the [tokens][output_dim] rows)"""
+        p = C.c_void_p()
+        T = lib().qwen_hip_encoder_forward_device(self.h, C.c_void_p(d_mel_ptr), int(frames), C.byref(p))
+        check(T if T < 0 else 0, "encoder_forward_device")
+        return T, p.value
+
+    def stream(self):
+        return lib().qwen_hip_encoder_stream(self.h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().qwen_hip_encoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Vocab:

@@ -1,0 +1,316 @@
+// encoder.hip - kernels of the audio encoder (reference qwen_asr_encoder.c:
+// Conv2D stem -> conv_out projection + sinusoidal positions -> pre-LayerNorm
+// transformer layers with windowed bidirectional attention -> ln_post,
+// proj1 + GELU, proj2).
+//
+// Every matrix product runs on the fp32 matrix cores (v_mfma_f32_16x16x4_f32):
+// the reference computes the encoder in fp32 on weights widened from bf16
+// (load_bf16_as_f32, qwen_asr_encoder.c:43-65), so products stay exact fp32
+// and only the summation order differs.
+//
+//   enc_im2col   Conv2D(3x3, stride 2, pad 1) patches of all chunks at once:
+//                row n = (chunk, oh, ow), column k = (ic, ki, kj)
+//                (the reference's im2col, qwen_asr_kernels.c:566-590)
+//   enc_gemm     C[M][N] = A[M][K] . B[N][K]^T with the encoder epilogues:
+//                bias along M or N, GELU, residual add, positional table add,
+//                zeroing of the padded columns of a partial last chunk
+//   enc_stem_rows conv3 output [480][chunk][16][w] -> token rows [t][480*16]
+//                (qwen_asr_encoder.c:281-290)
+//   enc_layernorm  (x - mean) * inv_std * w + b, two-pass mean / variance
+//                (qwen_layer_norm, qwen_asr_kernels.c:640-748)
+//   enc_attention  bidirectional attention inside fixed token windows
+//                (qwen_bidirectional_attention, qwen_asr_kernels.c:1003-1048)
+#include "common.h"
+#include "qk_kernels.h"
+#include "qwen_asr_hip.h"
+
+#include <math.h>
+
+__device__ __forceinline__ f32x4 enc_mfma(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// GELU, tanh form (qwen_gelu, qwen_asr_kernels.c:886-893)
+__device__ __forceinline__ float enc_gelu(float v) {
+    const float x3 = v * v * v;
+    const float inner = 0.7978845608028654f * (v + 0.044715f * x3);
+    return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+// ---------------------------------------------------------------------------
+// im2col of one stem layer over every chunk.  in: [c_in][chunks][h_in][w_in]
+// (conv1: the mel [128][frames], chunk c covering frames [c*cw, c*cw + cw),
+// frames past `frames` read as 0).  cols: [chunks*h_out*w_out][kpad], the
+// columns past c_in*9 zero.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void enc_im2col(const float *in, float *cols, int c_in, int chunks, int h_in,
+                                                  int w_in, int h_out, int w_out, int kpad, int mel_frames) {
+    const long rows = (long)chunks * h_out * w_out;
+    const long total = rows * kpad;
+    for (long e = blockIdx.x * 256L + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
+        const long n = e / kpad;
+        const int k = (int)(e % kpad);
+        float v = 0.0f;
+        if (k < c_in * 9) {
+            const int ic = k / 9, ki = (k % 9) / 3, kj = k % 3;
+            const int ow = (int)(n % w_out), oh = (int)((n / w_out) % h_out), c = (int)(n / ((long)w_out * h_out));
+            const int ih = 2 * oh - 1 + ki, iw = 2 * ow - 1 + kj;
+            if (ih >= 0 && ih < h_in && iw >= 0 && iw < w_in) {
+                if (mel_frames > 0) {               // conv1 reads the mel directly
+                    const int f = c * w_in + iw;
+                    if (f < mel_frames) v = in[(long)ih * mel_frames + f];
+                } else {
+                    v = in[(((long)ic * chunks + c) * h_in + ih) * w_in + iw];
+                }
+            }
+        }
+        cols[e] = v;
+    }
+}
+
+extern "C" int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int chunks, int h_in, int w_in,
+                                    int h_out, int w_out, int kpad, int mel_frames, hipStream_t s) {
+    if (!in || !cols || c_in <= 0 || chunks <= 0 || kpad < c_in * 9 || (kpad & 15)) return QWEN_HIP_EINVAL;
+    const long total = (long)chunks * h_out * w_out * kpad;
+    long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    enc_im2col<<<(int)blocks, 256, 0, s>>>(in, cols, c_in, chunks, h_in, w_in, h_out, w_out, kpad, mel_frames);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// ---------------------------------------------------------------------------
+// fp32 GEMM on v_mfma_f32_16x16x4_f32.  Block tile 64 x 64, 4 waves of 32 x 32
+// (2 x 2 MFMA tiles), K walked 16 at a time through LDS with the next tile's
+// loads in flight.  Within a 16-wide k block lane l supplies k = 4 (l >> 4) + c
+// at k-step c for both operands (each lane reads one float4 per row).
+// ---------------------------------------------------------------------------
+#define EG_T 64
+#define EG_K 16
+#define EG_LD (EG_K + 4)
+
+__global__ __launch_bounds__(256) void enc_gemm(qk_enc_gemm_args a) {
+    __shared__ __attribute__((aligned(16))) float sA[EG_T][EG_LD];
+    __shared__ __attribute__((aligned(16))) float sB[EG_T][EG_LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * EG_T, n0 = blockIdx.x * EG_T;
+    const int lr = tid >> 2, lk = (tid & 3) * 4;      // loader: row lr, k lk .. lk+3 of the tile
+
+    float4 ra, rb;
+    auto gload = [&](int k0) {
+        const int gm = m0 + lr, gn = n0 + lr, gk = k0 + lk;
+        ra = (gm < a.M && gk < a.K) ? *reinterpret_cast<const float4 *>(a.A + (long)gm * a.lda + gk)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+        rb = (gn < a.N && gk < a.K) ? *reinterpret_cast<const float4 *>(a.B + (long)gn * a.ldb + gk)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    gload(0);
+    for (int k0 = 0; k0 < a.K; k0 += EG_K) {
+        __syncthreads();
+        *reinterpret_cast<float4 *>(&sA[lr][lk]) = ra;
+        *reinterpret_cast<float4 *>(&sB[lr][lk]) = rb;
+        __syncthreads();
+        if (k0 + EG_K < a.K) gload(k0 + EG_K);
+        float4 af[2], bf[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const float4 *>(&sA[wm * 32 + i * 16 + (lane & 15)][4 * (lane >> 4)]);
+#pragma unroll
+        for (int j = 0; j < 2; j++) bf[j] = *reinterpret_cast<const float4 *>(&sB[wn * 32 + j * 16 + (lane & 15)][4 * (lane >> 4)]);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j] = enc_mfma((&af[i].x)[c], (&bf[j].x)[c], acc[i][j]);
+    }
+
+    // D[4 (l >> 4) + r][l & 15] of each 16 x 16 tile: rows m, column n
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+                if (m >= a.M || n >= a.N) continue;
+                float v = acc[i][j][r];
+                if (a.bias_m) v += a.bias_m[m];
+                if (a.bias_n) v += a.bias_n[n];
+                if (a.pe) v += a.pe[(long)(m % a.pe_rows) * a.N + n];
+                if (a.gelu) v = enc_gelu(v);
+                if (a.col_w > 0) {
+                    // stem output column n = (chunk, oh, ow): the last chunk's columns past its
+                    // valid width are the zero padding the reference's next convolution sees
+                    const int ow = n % a.col_w, c = n / (a.col_w * a.col_h);
+                    if (c == a.col_chunks - 1 && ow >= a.col_valid) v = 0.0f;
+                }
+                float *y = a.C + (long)m * a.ldc + n;
+                if (a.add) v += *y;                    // residual (qwen_add_inplace after the projection)
+                *y = v;
+            }
+        }
+    }
+}
+
+extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
+    if (!a || !a->A || !a->B || !a->C || a->M <= 0 || a->N <= 0 || a->K <= 0 || (a->K & 3) || (a->lda & 3) ||
+        (a->ldb & 3) || a->lda < a->K || a->ldb < a->K || a->ldc < a->N || (a->pe && a->pe_rows <= 0))
+        return QWEN_HIP_EINVAL;
+    dim3 grid((a->N + EG_T - 1) / EG_T, (a->M + EG_T - 1) / EG_T);
+    enc_gemm<<<grid, 256, 0, s>>>(*a);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// conv3 output [480][chunks][16][w] -> rows [token][480*16], token = chunk*w + t for
+// t < the chunk's token count (qwen_asr_encoder.c:281-290: column ch*16 + f)
+__global__ __launch_bounds__(256) void enc_stem_rows(const float *c3, float *rows, int chunks, int w, int h,
+                                                     int ch_n, int tokens) {
+    const int D = ch_n * h;
+    const long total = (long)tokens * D;
+    for (long e = blockIdx.x * 256L + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
+        const int tok = (int)(e / D), col = (int)(e % D);
+        const int ch = col / h, f = col % h;
+        const int c = tok / w, t = tok % w;
+        rows[e] = c3[(((long)ch * chunks + c) * h + f) * w + t];
+    }
+}
+
+extern "C" int qk_enc_stem_rows_launch(const float *c3, float *rows, int chunks, int w, int h, int ch_n, int tokens,
+                                       hipStream_t s) {
+    if (!c3 || !rows || tokens <= 0 || tokens > chunks * w) return QWEN_HIP_EINVAL;
+    long blocks = ((long)tokens * ch_n * h + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    enc_stem_rows<<<(int)blocks, 256, 0, s>>>(c3, rows, chunks, w, h, ch_n, tokens);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm, one block per row (qwen_layer_norm: mean, then mean of squared
+// deviations, then (x - mean) * inv_std * w + b).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void enc_layernorm(const float *x, const float *w, const float *b, float *out,
+                                                     int D, float eps) {
+    __shared__ float red[4];
+    const float *xr = x + (long)blockIdx.x * D;
+    float *orow = out + (long)blockIdx.x * D;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < D; i += 256) s += xr[i];
+    s = wave_sum(s);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)D;
+    __syncthreads();
+    float v = 0.0f;
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float d = xr[i] - mean;
+        v = fmaf(d, d, v);
+    }
+    v = wave_sum(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    const float var = (red[0] + red[1] + red[2] + red[3]) / (float)D;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    for (int i = threadIdx.x; i < D; i += 256) orow[i] = (xr[i] - mean) * inv_std * w[i] + b[i];
+}
+
+extern "C" int qk_enc_layernorm_launch(const float *x, const float *w, const float *b, float *out, int rows, int D,
+                                       float eps, hipStream_t s) {
+    if (!x || !w || !b || !out || rows <= 0 || D <= 0) return QWEN_HIP_EINVAL;
+    enc_layernorm<<<rows, 256, 0, s>>>(x, w, b, out, D, eps);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
+// ---------------------------------------------------------------------------
+// Windowed bidirectional attention, head_dim 64.  Block = (64 query rows, head);
+// four lanes per query row (16 dims each), online softmax over the keys of
+// the row's window [ws, we); K/V rows of the windows the block touches are
+// staged in LDS 32 at a time.  qkv: [T][3 * H * 64] (q | k | v per token).
+// ---------------------------------------------------------------------------
+#define EA_ROWS 64
+#define EA_TILE 32
+
+__global__ __launch_bounds__(256) void enc_attention(const float *qkv, float *out, int T, int H, int win, float scale) {
+    constexpr int hd = 64;
+    __shared__ float4 sk[EA_TILE][hd / 4];
+    __shared__ float4 sv[EA_TILE][hd / 4];
+    const int h = blockIdx.y;
+    const int qi = blockIdx.x * EA_ROWS + (threadIdx.x >> 2);
+    const int quarter = threadIdx.x & 3;
+    const long stride = 3L * H * hd;
+    const bool valid = qi < T;
+    const int q0 = blockIdx.x * EA_ROWS;
+    const int q1 = min(T, q0 + EA_ROWS) - 1;
+    const int kb0 = (q0 / win) * win, kb1 = min(T, (q1 / win + 1) * win);   // union of the rows' windows
+    const int ws = valid ? (qi / win) * win : 0, we = valid ? min(T, ws + win) : 0;
+
+    float4 q[4], o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        q[j] = valid ? *reinterpret_cast<const float4 *>(qkv + (long)qi * stride + h * hd + quarter * 16 + 4 * j)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        o[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float m = -1e30f, l = 0.0f;                       // the reference's max_score start
+    for (int t0 = kb0; t0 < kb1; t0 += EA_TILE) {
+        const int nk = min(EA_TILE, kb1 - t0);
+        __syncthreads();
+        for (int e = threadIdx.x; e < EA_TILE * hd / 4; e += 256) {
+            const int r = e / (hd / 4), c = e % (hd / 4);
+            if (r < nk) {
+                const float *row = qkv + (long)(t0 + r) * stride + h * hd;
+                sk[r][c] = *reinterpret_cast<const float4 *>(row + H * hd + c * 4);
+                sv[r][c] = *reinterpret_cast<const float4 *>(row + 2 * H * hd + c * 4);
+            }
+        }
+        __syncthreads();
+        for (int j = 0; j < nk; j++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float4 kk = sk[j][quarter * 4 + c];
+                d = fmaf(q[c].x, kk.x, d);
+                d = fmaf(q[c].y, kk.y, d);
+                d = fmaf(q[c].z, kk.z, d);
+                d = fmaf(q[c].w, kk.w, d);
+            }
+            d = group_sum<4>(d);
+            const int key = t0 + j;
+            if (key >= ws && key < we) {
+                const float sc = d * scale;
+                const float mn = fmaxf(m, sc);
+                const float corr = __expf(m - mn), pw = __expf(sc - mn);
+                l = fmaf(l, corr, pw);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float4 vv = sv[j][quarter * 4 + c];
+                    o[c].x = fmaf(o[c].x, corr, pw * vv.x);
+                    o[c].y = fmaf(o[c].y, corr, pw * vv.y);
+                    o[c].z = fmaf(o[c].z, corr, pw * vv.z);
+                    o[c].w = fmaf(o[c].w, corr, pw * vv.w);
+                }
+                m = mn;
+            }
+        }
+    }
+    if (!valid) return;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float4 *op = reinterpret_cast<float4 *>(out + (long)qi * H * hd + h * hd + quarter * 16);
+#pragma unroll
+    for (int c = 0; c < 4; c++) op[c] = make_float4(o[c].x * inv, o[c].y * inv, o[c].z * inv, o[c].w * inv);
+}
+
+extern "C" int qk_enc_attention_launch(const float *qkv, float *out, int T, int H, int hd, int win, float scale,
+                                       hipStream_t s) {
+    if (!qkv || !out || T <= 0 || H <= 0 || hd != 64 || win <= 0) return QWEN_HIP_EINVAL;
+    dim3 grid((T + EA_ROWS - 1) / EA_ROWS, H);
+    enc_attention<<<grid, 256, 0, s>>>(qkv, out, T, H, win, scale);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}

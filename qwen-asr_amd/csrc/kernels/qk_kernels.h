@@ -238,6 +238,28 @@ int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W
 int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, float *y, uint16_t *out_hi,
                           uint16_t *out_lo, hipStream_t s);
 
+/* ---- audio encoder (fp32 matrix cores) --------------------------------- */
+/* C[M][N] (=, +=) A[M][K] . B[N][K]^T (+ bias_m[m] | bias_n[n]) (+ pe[m % pe_rows][n])
+ * (GELU); K and the leading dimensions multiples of 4.  col_w > 0: stem
+ * output, column n = (chunk, oh, ow) with col_h x col_w per chunk; the last
+ * chunk's columns with ow >= col_valid are written as 0. */
+typedef struct {
+    const float *A, *B;
+    float *C;
+    int M, N, K, lda, ldb, ldc;
+    const float *bias_m, *bias_n, *pe;
+    int pe_rows, gelu, add;
+    int col_w, col_h, col_chunks, col_valid;
+} qk_enc_gemm_args;
+int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s);
+int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int chunks, int h_in, int w_in, int h_out,
+                         int w_out, int kpad, int mel_frames, hipStream_t s);
+int qk_enc_stem_rows_launch(const float *c3, float *rows, int chunks, int w, int h, int ch_n, int tokens,
+                            hipStream_t s);
+int qk_enc_layernorm_launch(const float *x, const float *w, const float *b, float *out, int rows, int D, float eps,
+                            hipStream_t s);
+int qk_enc_attention_launch(const float *qkv, float *out, int T, int H, int hd, int win, float scale, hipStream_t s);
+
 /* ---- elementwise (op-level ABI) --------------------------------------- */
 int qk_add_launch(float *a, const float *b, long n, hipStream_t s);
 int qk_rms_norm_launch(float *out, const float *x, const float *w, int S, int D,

@@ -1,0 +1,114 @@
+"""The audio encoder (qwen_hip_encoder_*) against the reference's encoder
+(qwen_encoder_forward, qwen_asr_encoder.c:171-372): the committed fixtures
+tests/golden/enc_*.npz hold the compiled reference's output on seeded
+weights and mel (tests/golden/make_enc_golden.py; test_encoder_oracle.py
+re-derives one of them on the CPU).
+
+Both compute in fp32 (the products of the fp32 matrix cores are exact fp32
+products); sums run in another order, tanhf / expf of two libms differ by
+ulps, and 2 layers of LayerNorm / attention / GELU amplify that: the bar is
+|gpu - ref| <= 1e-4 + 1e-3 |ref| elementwise.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+ATOL, RTOL = 1e-4, 1e-3
+
+
+def fixture(name):
+    return np.load(os.path.join(GOLD, name + ".npz"))
+
+
+def build(qa, P, g):
+    cfg = qa.EncConfig(*[int(v) for v in g["cfg"]])
+    m = P.SynthEncoder(cfg, seed=int(g["seed"]))
+    from golden.make_enc_golden import weight_checksum
+    assert abs(weight_checksum(m) - float(g["weight_sum"])) <= 1e-9 * abs(float(g["weight_sum"]))
+    mel = P.synth_mel(int(g["frames"]), int(g["seed"]), int(g["mel_set"]))
+    assert float(np.float64(mel).sum()) == float(g["mel_sum"])
+    return cfg, m, mel
+
+
+def load(qa, cfg, m):
+    e = qa.Encoder(cfg, 0)
+    for l, arrs in enumerate(m.layers):
+        e.load_layer(l, arrs)
+    e.load_stem(m.stem)
+    return e
+
+
+@pytest.mark.parametrize("name", ["enc_tiny", "enc_06b2"])
+def test_encoder_matches_reference(P, qa, gpu, name):
+    g = fixture(name)
+    cfg, m, mel = build(qa, P, g)
+    e = load(qa, cfg, m)
+    out = e.forward(mel)
+    ref = g["out"]
+    assert out.shape == ref.shape
+    err = np.abs(out - ref)
+    print(f"{name}: {out.shape[0]} tokens, max |d| {err.max():.2e}, max rel {float((err / (np.abs(ref) + 1e-6)).max()):.2e}")
+    assert np.all(err <= ATOL + RTOL * np.abs(ref)), float((err - RTOL * np.abs(ref)).max())
+    e.close()
+
+
+def d2h(ptr, shape):
+    """copy a device buffer (raw pointer) to a new host array"""
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    out = np.empty(shape, np.float32)
+    assert hip.hipMemcpy(out.ctypes.data, C.c_void_p(ptr), out.nbytes, 2) == 0   # hipMemcpyDeviceToHost
+    return out
+
+
+def test_encoder_synthetic_loader_and_device_path(P, qa, gpu):
+    """load_synthetic (C recipe) == the same weights through load_layer/load_stem,
+    bit for bit; forward_device == forward; repeated calls with other lengths
+    (buffers regrown, partial chunks of every size class)"""
+    cfg = qa.EncConfig(128, 2, 2, 64, 256, 96, 100, 200)
+    m = P.SynthEncoder(cfg, seed=5)
+    a = load(qa, cfg, m)
+    b = qa.Encoder(cfg, 0)
+    b.load_synthetic(5, 0.02)
+    for frames in (320, 99, 1, 400):
+        mel = P.synth_mel(frames, 5, 3)
+        oa = a.forward(mel)
+        ob = b.forward(mel)
+        assert oa.shape[0] == a.tokens(frames)
+        assert np.array_equal(oa, ob), frames
+        dm = gpu.from_numpy(np.ascontiguousarray(mel)).to("cuda")
+        gpu.cuda.synchronize()
+        T, p = b.forward_device(dm.data_ptr(), frames)
+        assert np.array_equal(d2h(p, (T, cfg.output_dim)), ob), frames
+    a.close()
+    b.close()
+
+
+def test_encoder_rows_feed_the_decoder(P, qa, gpu):
+    """encoder output (0.6B widths: 1024 = the decoder's hidden) straight into
+    the decoder's device prefill gives what the host path gives"""
+    cfg = qa.enc_preset(0)
+    cfg.layers = 2
+    e = qa.Encoder(cfg, 0)
+    e.load_synthetic(0, 0.02)
+    mel = P.synth_mel(300, 0, 4)
+    rows = e.forward(mel)
+    dm = gpu.from_numpy(np.ascontiguousarray(mel)).to("cuda")
+    gpu.cuda.synchronize()
+    T, p = e.forward_device(dm.data_ptr(), 300)
+    dcfg = qa.preset(0)
+    d = qa.Decoder(dcfg, 0, 512)
+    d.load_synthetic(0, 0.02, 0.0)
+    d.set_engine(0)
+    d.prefill(rows[:-1])
+    t_host = d.forward(rows[-1])
+    d.set_kv_len(0)
+    d.prefill_device(p, T - 1)
+    t_dev = d.forward(rows[-1])
+    assert T == rows.shape[0] and t_dev == t_host
+    d.close()
+    e.close()
