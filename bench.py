@@ -43,6 +43,9 @@ WORKLOADS = {
                desc="C3 Qwen3-ASR-1.7B decoder: 1500 audio rows + 16 ids, prefill 1515, greedy decode"),
     "c4": dict(model_b=0, n_audio=8192, n_ids=0, steps=512,
                desc="C4 0.6B long context: prefill 8191 audio rows, greedy decode over up to 8.7k positions"),
+    "enc": dict(model_b=0, n_audio=0, n_ids=0, steps=20,
+                desc="Qwen3-ASR-0.6B audio encoder: 30 s of synthetic mel (3000 frames, 30 chunks -> 390 "
+                     "tokens), conv stem + 18 layers + projection, fp32"),
     "c5": dict(model_b=0, n_audio=26, n_ids=9,
                desc="C5 0.6B streaming: 60 chunks x (roll back 5 tokens, prefill 5 token + 26 audio rows, "
                     "24 greedy forwards), KV window capped at 1024 positions"),
@@ -211,6 +214,94 @@ def run_streaming(qa, d, cfg, chunks):
     return out, times
 
 
+ENC_FRAMES, ENC_CPU_FRAMES = 3000, 200
+FP32_MFMA_PEAK_TFS = 157.3
+
+
+def enc_flops(c, frames):
+    """Algorithmic flops of one encoder forward (2 per multiply-add): conv
+    stem as GEMMs (conv1 K = 9), conv_out, per layer the Q/K/V/O, FFN and
+    windowed attention products, ln_post projections.  Full chunks only."""
+    cw = c.chunk_size
+    conv = lambda w: (w + 2 - 3) // 2 + 1
+    w1, w2, w3 = conv(cw), conv(conv(cw)), conv(conv(conv(cw)))
+    chunks = frames // cw
+    T = chunks * w3
+    d, f, o = c.d_model, c.ffn_dim, c.output_dim
+    fl = 2 * 480 * 9 * chunks * 64 * w1 + 2 * 480 * 4320 * chunks * (32 * w2 + 16 * w3)
+    fl += 2 * T * d * 7680
+    win = w3 * (c.n_window_infer // cw)
+    att = sum(min(win, T - s) ** 2 for s in range(0, T, win)) * 4 * d
+    fl += c.layers * (2 * T * (4 * d * d + 2 * d * f) + att)
+    fl += 2 * T * d * (d + o)
+    return fl, T
+
+
+def run_encoder(qa, args, wl):
+    """Encoder workload: one step = one forward of 30 s of mel resident in HBM
+    (qwen_hip_encoder_forward_device), timed with HIP events on the encoder's
+    stream; CPU baseline = the reference encoder (oracle/_ref) on 2 s of the
+    same mel with the same weights."""
+    import numpy as np
+    import torch
+    c = qa.enc_preset(wl["model_b"])
+    K, W = args.steps or wl["steps"], args.warmup
+    e = qa.Encoder(c, 0)
+    t0 = time.time()
+    e.load_synthetic(0, 0.02)
+    mel_h = qa.synth_mel(ENC_FRAMES, 0, 0)
+    mel = torch.from_numpy(mel_h).cuda()
+    log(f"[gpu] enc: weights generated+uploaded in {time.time() - t0:.1f}s; {ENC_FRAMES} mel frames")
+    for _ in range(W):
+        T, _ = e.forward_device(mel.data_ptr(), ENC_FRAMES)
+    s = torch.cuda.ExternalStream(e.stream())
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(s)
+    for _ in range(K):
+        T, _ = e.forward_device(mel.data_ptr(), ENC_FRAMES)
+    ev1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    fl, T_ = enc_flops(c, ENC_FRAMES)
+    assert T == T_, (T, T_)
+    audio_s = ENC_FRAMES / 100.0
+    tfs = fl / (gpu_ms / K * 1e-3) / 1e12
+    log(f"[gpu] enc: {K} forwards, {gpu_ms / K:.3f} ms GPU per forward ({wall / K * 1e3:.3f} ms wall), "
+        f"{fl / 1e9:.1f} GFLOP -> {tfs:.1f} TFLOP/s")
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pyoracle as P
+        if P.ref_available():
+            threads = min(os.cpu_count() or 1, 16)
+            t0 = time.time()
+            m = P.SynthEncoder(c, seed=0)
+            r = P.RefEncoder(m, threads=threads)
+            log(f"[cpu] encoder weights generated in {time.time() - t0:.1f}s; {ENC_CPU_FRAMES} frames on "
+                f"{threads} threads")
+            n_tok = e.tokens(ENC_CPU_FRAMES)
+            tc = r.time(mel_h[:, :ENC_CPU_FRAMES], n_tok)
+            log(f"[cpu] reference encoder: {tc:.2f}s for {ENC_CPU_FRAMES / 100:.0f} s of audio")
+            cpu = {"value": round(ENC_CPU_FRAMES / 100.0 / tc, 4), "unit": "audio-s/s", "cores": threads,
+                   "kind": "reference",
+                   "sample": f"reference encoder (oracle/_ref, no BLAS) on the first {ENC_CPU_FRAMES} frames "
+                             f"({ENC_CPU_FRAMES // 100} s) of the same mel, same weights"}
+    print(json.dumps({
+        "metric": "encoder audio seconds per second (0.6B, 30 s input)",
+        "value": round(audio_s / (gpu_ms / K * 1e-3), 2), "unit": "audio-s/s", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": round(gpu_ms / K, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": wl["desc"], "tokens": T, "weights": "synthetic N(0,0.02), seed 0"},
+        "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": FP32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                     "frac": round(tfs / FP32_MFMA_PEAK_TFS, 4), "traffic": None,
+                     "kernel": "encoder forward (all launches; enc_gemm dominant)",
+                     "flops_per_launch": fl, "launch_us": round(gpu_ms / K * 1e3, 2)},
+        "wall_ms_per_step": round(wall / K * 1e3, 4), "cpu_baseline": cpu}), flush=True)
+
+
 def cpu_baseline(wl, rows, first_token, threads, decode_steps):
     """Reference decoder (oracle/_ref) on this host: prefill of the same rows
     and `decode_steps` greedy forwards from the same first token."""
@@ -296,6 +387,9 @@ def main():
                          "frac": big["frac"], "traffic": None,
                          "kernel": f"gemv {big['rows']}x{big['cols']} (largest shape)"},
             "per_shape": rows, "cpu_baseline": cpu}), flush=True)
+        return
+    if args.workload == "enc":
+        run_encoder(qa, args, wl)
         return
     if args.workload == "c5":
         d = qa.Decoder(cfg, 0, C5_CAP + 64)

@@ -316,6 +316,14 @@ int qwen_hip_encoder_forward(qwen_hip_encoder *enc, const float *mel, int mel_fr
  * (valid until the next call), ready for qwen_hip_decoder_prefill_device. */
 int qwen_hip_encoder_forward_device(qwen_hip_encoder *enc, const float *d_mel, int mel_frames, const float **d_out);
 hipStream_t qwen_hip_encoder_stream(const qwen_hip_encoder *enc);
+const qwen_hip_enc_config *qwen_hip_encoder_config(const qwen_hip_encoder *enc);
+/* Encoder from a checkpoint (thinker.audio_tower.*, qwen_encoder_load,
+ * qwen_asr_encoder.c:67-168): shape from the tensor shapes (d_model from
+ * conv_out rows, ffn from fc1 rows, output_dim from proj2 rows, layers
+ * counted, 64-wide heads); F32 or BF16 tensors widened to fp32. */
+int qwen_hip_checkpoint_enc_config(const qwen_hip_checkpoint *ck, qwen_hip_enc_config *cfg);
+int qwen_hip_encoder_load_checkpoint(qwen_hip_encoder *enc, const qwen_hip_checkpoint *ck);
+qwen_hip_encoder *qwen_hip_encoder_create_from_checkpoint(const char *model_dir, int device);
 
 /* ------------------------------------------------------------------------
  * Token ids -> text: the decode half of the reference tokenizer

@@ -414,10 +414,13 @@ def synth_mel(frames, seed=0, s=0):
 class RefEncoder:
     """qwen_encoder_forward of the reference (oracle/_ref), on a SynthEncoder's arrays."""
 
-    def __init__(self, model: SynthEncoder):
+    def __init__(self, model: SynthEncoder, threads=0):
         lib = ref_lib()
         if lib is None:
             raise RuntimeError("oracle/_ref is not built")
+        if threads:
+            lib.ref_set_threads.argtypes = [C.c_int]
+            lib.ref_set_threads(threads)
         lib.ref_enc_create.restype = C.c_void_p
         lib.ref_enc_create.argtypes = [C.c_int] * 8
         lib.ref_enc_set_layer.argtypes = [C.c_void_p, C.c_int] + [_f32p] * 16

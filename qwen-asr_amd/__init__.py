@@ -92,6 +92,10 @@ SIGNATURES = [
     ("qwen_hip_encoder_forward", _i, [_vp, _vp, _i, _vp]),
     ("qwen_hip_encoder_forward_device", _i, [_vp, _vp, _i, _vp]),
     ("qwen_hip_encoder_stream", _vp, [_vp]),
+    ("qwen_hip_encoder_config", _vp, [_vp]),
+    ("qwen_hip_checkpoint_enc_config", _i, [_vp, _vp]),
+    ("qwen_hip_encoder_load_checkpoint", _i, [_vp, _vp]),
+    ("qwen_hip_encoder_create_from_checkpoint", _vp, [C.c_char_p, _i]),
     ("qwen_hip_vocab_load", _vp, [C.c_char_p]),
     ("qwen_hip_vocab_free", None, [_vp]),
     ("qwen_hip_vocab_size", _i, [_vp]),
@@ -187,6 +191,11 @@ def synth_tokens(n, seed, tensor_id, n_ids=151643):
     return out
 
 
+def synth_mel(frames, seed=0, s=0):
+    """seeded N(0,1) log-mel [128][frames] (tensor id 750000 + s)"""
+    return synth_f32(128 * frames, seed, 750000 + s).reshape(128, frames)
+
+
 def bf16_to_f32(a):
     return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
@@ -238,6 +247,17 @@ class Encoder:
         self.h = lib().qwen_hip_encoder_create(C.byref(cfg), device)
         if not self.h:
             raise RuntimeError(f"qwen_hip_encoder_create: {last_error()}")
+
+    @classmethod
+    def from_checkpoint(cls, model_dir, device=0):
+        h = lib().qwen_hip_encoder_create_from_checkpoint(os.fsencode(model_dir), device)
+        if not h:
+            raise RuntimeError(f"qwen_hip_encoder_create_from_checkpoint: {last_error()}")
+        self = cls.__new__(cls)
+        self.h = h
+        c = EncConfig.from_address(lib().qwen_hip_encoder_config(h))
+        self.cfg = EncConfig(*[getattr(c, f) for f, _ in EncConfig._fields_])
+        return self
 
     def load_synthetic(self, seed=0, wstd=0.02):
         check(lib().qwen_hip_encoder_load_synthetic(self.h, seed, wstd), "encoder_load_synthetic")
@@ -335,6 +355,11 @@ class Checkpoint:
     def config(self):
         cfg = HipConfig()
         check(lib().qwen_hip_checkpoint_config(self.h, C.byref(cfg)), "checkpoint_config")
+        return cfg
+
+    def enc_config(self):
+        cfg = EncConfig()
+        check(lib().qwen_hip_checkpoint_enc_config(self.h, C.byref(cfg)), "checkpoint_enc_config")
         return cfg
 
     def tensor(self, name):

@@ -42,6 +42,7 @@ struct qwen_hip_encoder {
     /* activations, sized for cap_chunks chunks */
     int cap_chunks;
     float *mel, *cols, *c1, *c2, *c3, *rows, *x, *xn, *qkv, *att, *mid, *out;
+    float *gws;   /* split-K partials of the GEMMs (QK_ENC_GEMM_WS_ELEMS floats) */
 };
 
 static int dmalloc(void **p, size_t n) {
@@ -86,7 +87,7 @@ static int check_cfg(const qwen_hip_enc_config *c) {
 static void act_free(qwen_hip_encoder *e) {
     void **b[] = {(void **)&e->mel, (void **)&e->cols, (void **)&e->c1, (void **)&e->c2, (void **)&e->c3,
                   (void **)&e->rows, (void **)&e->x, (void **)&e->xn, (void **)&e->qkv, (void **)&e->att,
-                  (void **)&e->mid, (void **)&e->out};
+                  (void **)&e->mid, (void **)&e->out, (void **)&e->gws};
     for (size_t i = 0; i < sizeof(b) / sizeof(b[0]); i++) dfree(b[i]);
     e->cap_chunks = 0;
 }
@@ -318,6 +319,7 @@ static int reserve(qwen_hip_encoder *e, int chunks, int tokens) {
     if (!rc) rc = dmalloc((void **)&e->att, T * d * 4);
     if (!rc) rc = dmalloc((void **)&e->mid, T * (size_t)(c->ffn_dim > (int)d ? c->ffn_dim : (int)d) * 4);
     if (!rc) rc = dmalloc((void **)&e->out, T * (size_t)c->output_dim * 4);
+    if (!rc) rc = dmalloc((void **)&e->gws, (size_t)QK_ENC_GEMM_WS_ELEMS * 4);
     if (rc) { act_free(e); return rc; }
     e->cap_chunks = chunks;
     return 0;
@@ -326,7 +328,8 @@ static int reserve(qwen_hip_encoder *e, int chunks, int tokens) {
 static int gemm(qwen_hip_encoder *e, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
                 int N, int K, const float *bias_m, const float *bias_n, int gelu, int add) {
     qk_enc_gemm_args g = {.A = A, .B = B, .C = C, .M = M, .N = N, .K = K, .lda = lda, .ldb = ldb, .ldc = ldc,
-                          .bias_m = bias_m, .bias_n = bias_n, .gelu = gelu, .add = add};
+                          .bias_m = bias_m, .bias_n = bias_n, .gelu = gelu, .add = add,
+                          .ws = e->gws, .ws_elems = QK_ENC_GEMM_WS_ELEMS};
     return qk_enc_gemm_launch(&g, e->stream);
 }
 
@@ -358,7 +361,8 @@ static int run(qwen_hip_encoder *e, int mel_frames, int *tokens_out) {
     QK_TRY(qk_enc_stem_rows_launch(e->c3, e->rows, chunks, w3, 16, ENC_CH, T, e->stream));
     {
         qk_enc_gemm_args g = {.A = e->rows, .B = e->cow, .C = e->x, .M = T, .N = d, .K = ENC_CH * 16,
-                              .lda = ENC_CH * 16, .ldb = ENC_CH * 16, .ldc = d, .pe = e->pe, .pe_rows = w3};
+                              .lda = ENC_CH * 16, .ldb = ENC_CH * 16, .ldc = d, .pe = e->pe, .pe_rows = w3,
+                              .ws = e->gws, .ws_elems = QK_ENC_GEMM_WS_ELEMS};
         QK_TRY(qk_enc_gemm_launch(&g, e->stream));
     }
     const int win = w3 * (c->n_window_infer / cw);
@@ -418,3 +422,5 @@ int qwen_hip_encoder_forward_device(qwen_hip_encoder *e, const float *d_mel, int
 }
 
 hipStream_t qwen_hip_encoder_stream(const qwen_hip_encoder *e) { return e ? e->stream : NULL; }
+
+const qwen_hip_enc_config *qwen_hip_encoder_config(const qwen_hip_encoder *e) { return e ? &e->cfg : NULL; }

@@ -428,3 +428,138 @@ qwen_hip_decoder *qwen_hip_decoder_create_from_checkpoint(const char *model_dir,
     qwen_hip_checkpoint_close(ck);
     return d;
 }
+
+/* ---- the audio encoder (thinker.audio_tower.*; qwen_encoder_load,
+ * qwen_asr_encoder.c:67-168, and the encoder part of detect_config) ------- */
+#define ENAME(buf, fmt, ...) snprintf(buf, sizeof(buf), "thinker.audio_tower." fmt, __VA_ARGS__)
+
+int qwen_hip_checkpoint_enc_config(const qwen_hip_checkpoint *ck, qwen_hip_enc_config *cfg) {
+    if (!ck || !cfg) return QWEN_HIP_EINVAL;
+    const st_tensor *co = find(ck, "thinker.audio_tower.conv_out.weight");
+    const st_tensor *fc = find(ck, "thinker.audio_tower.layers.0.fc1.weight");
+    const st_tensor *p2 = find(ck, "thinker.audio_tower.proj2.weight");
+    if (!co || !fc || !p2 || co->ndim != 2 || fc->ndim != 2 || p2->ndim != 2) {
+        qk_set_err("checkpoint: no audio encoder (thinker.audio_tower.conv_out / layers.0.fc1 / proj2)");
+        return QWEN_HIP_EINVAL;
+    }
+    char n[ST_NAME];
+    int layers = 0;
+    for (; layers < QWEN_HIP_ENC_MAX_LAYERS; layers++) {
+        ENAME(n, "layers.%d.self_attn.q_proj.weight", layers);
+        if (!find(ck, n)) break;
+    }
+    memset(cfg, 0, sizeof(*cfg));
+    cfg->d_model = (int)co->shape[0];
+    cfg->head_dim = 64;
+    cfg->heads = cfg->d_model / 64;
+    cfg->ffn_dim = (int)fc->shape[0];
+    cfg->output_dim = (int)p2->shape[0];
+    cfg->layers = layers;
+    cfg->chunk_size = 100;
+    cfg->n_window_infer = 800;
+    return 0;
+}
+
+/* any F32 / BF16 tensor of exactly n elements, widened into a new fp32 buffer */
+static float *f32_of(const qwen_hip_checkpoint *ck, const char *name, long long n) {
+    const st_tensor *t = find(ck, name);
+    if (!t) { qk_set_err("checkpoint: missing %s", name); return NULL; }
+    long long numel = 1;
+    for (int i = 0; i < t->ndim; i++) numel *= t->shape[i];
+    if (numel != n || (t->dtype != QWEN_HIP_ST_F32 && t->dtype != QWEN_HIP_ST_BF16)) {
+        qk_set_err("checkpoint: %s must be F32 or BF16 with %lld elements", name, n);
+        return NULL;
+    }
+    float *out = (float *)malloc((size_t)n * sizeof(float));
+    if (!out) { qk_set_err("checkpoint: out of host memory"); return NULL; }
+    const char *p = (const char *)ck->map[t->shard] + ck->data_off[t->shard] + t->begin;
+    if (t->dtype == QWEN_HIP_ST_F32) {
+        memcpy(out, p, (size_t)n * 4);
+    } else {
+        for (long long i = 0; i < n; i++) {
+            uint16_t b;
+            memcpy(&b, p + 2 * i, 2);
+            const uint32_t u = (uint32_t)b << 16;
+            memcpy(&out[i], &u, 4);
+        }
+    }
+    return out;
+}
+
+int qwen_hip_encoder_load_checkpoint(qwen_hip_encoder *e, const qwen_hip_checkpoint *ck) {
+    if (!e || !ck) return QWEN_HIP_EINVAL;
+    qwen_hip_enc_config c;
+    QK_TRY(qwen_hip_checkpoint_enc_config(ck, &c));
+    /* the encoder's own shape must match what it was created with */
+    const qwen_hip_enc_config *ec = qwen_hip_encoder_config(e);
+    if (c.d_model != ec->d_model || c.layers != ec->layers || c.ffn_dim != ec->ffn_dim ||
+        c.output_dim != ec->output_dim) {
+        qk_set_err("checkpoint: encoder shape differs from the encoder's configuration");
+        return QWEN_HIP_EINVAL;
+    }
+    const long long d = c.d_model, f = c.ffn_dim, o = c.output_dim;
+    char n[ST_NAME];
+    int rc = 0;
+    for (int l = 0; l < c.layers && !rc; l++) {
+        static const char *names[16] = {"self_attn.q_proj.weight", "self_attn.q_proj.bias", "self_attn.k_proj.weight",
+                                        "self_attn.k_proj.bias", "self_attn.v_proj.weight", "self_attn.v_proj.bias",
+                                        "self_attn.out_proj.weight", "self_attn.out_proj.bias",
+                                        "self_attn_layer_norm.weight", "self_attn_layer_norm.bias", "fc1.weight",
+                                        "fc1.bias", "fc2.weight", "fc2.bias", "final_layer_norm.weight",
+                                        "final_layer_norm.bias"};
+        const long long sizes[16] = {d * d, d, d * d, d, d * d, d, d * d, d, d, d, f * d, f, d * f, d, d, d};
+        float *p[16] = {0};
+        int ok = 1;
+        for (int i = 0; i < 16 && ok; i++) {
+            ENAME(n, "layers.%d.%s", l, names[i]);
+            p[i] = f32_of(ck, n, sizes[i]);
+            ok = p[i] != NULL;
+        }
+        if (ok) {
+            qwen_hip_enc_layer_weights w = {p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7],
+                                            p[8], p[9], p[10], p[11], p[12], p[13], p[14], p[15]};
+            rc = qwen_hip_encoder_load_layer(e, l, &w);
+        } else {
+            rc = QWEN_HIP_EINVAL;
+        }
+        for (int i = 0; i < 16; i++) free(p[i]);
+    }
+    if (rc) return rc;
+    static const char *snames[13] = {"conv2d1.weight", "conv2d1.bias", "conv2d2.weight", "conv2d2.bias",
+                                     "conv2d3.weight", "conv2d3.bias", "conv_out.weight", "ln_post.weight",
+                                     "ln_post.bias", "proj1.weight", "proj1.bias", "proj2.weight", "proj2.bias"};
+    const long long ssizes[13] = {480 * 9, 480, 480LL * 4320, 480, 480LL * 4320, 480, d * 7680, d, d, d * d, d,
+                                  o * d, o};
+    float *p[13] = {0};
+    int ok = 1;
+    for (int i = 0; i < 13 && ok; i++) {
+        ENAME(n, "%s", snames[i]);
+        p[i] = f32_of(ck, n, ssizes[i]);
+        ok = p[i] != NULL;
+    }
+    if (ok) {
+        qwen_hip_enc_stem_weights w = {p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10], p[11], p[12]};
+        rc = qwen_hip_encoder_load_stem(e, &w);
+    } else {
+        rc = QWEN_HIP_EINVAL;
+    }
+    for (int i = 0; i < 13; i++) free(p[i]);
+    return rc;
+}
+
+qwen_hip_encoder *qwen_hip_encoder_create_from_checkpoint(const char *model_dir, int device) {
+    qwen_hip_checkpoint *ck = qwen_hip_checkpoint_open(model_dir);
+    if (!ck) return NULL;
+    qwen_hip_enc_config c;
+    qwen_hip_encoder *e = NULL;
+    if (qwen_hip_checkpoint_enc_config(ck, &c) == 0) e = qwen_hip_encoder_create(&c, device);
+    if (e && qwen_hip_encoder_load_checkpoint(e, ck) != 0) {
+        char msg[512];
+        snprintf(msg, sizeof(msg), "%s", qwen_hip_last_error());
+        qwen_hip_encoder_destroy(e);
+        qk_set_err("%s", msg);
+        e = NULL;
+    }
+    qwen_hip_checkpoint_close(ck);
+    return e;
+}

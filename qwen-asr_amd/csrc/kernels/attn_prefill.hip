@@ -47,28 +47,6 @@ __device__ __forceinline__ f32x4 mfma_f32_4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// max / sum over lanes l, l^16, l^32, l^48 (the four lanes holding one
-// query's scores) with row swaps at VALU latency (no LDS crossbar)
-__device__ __forceinline__ float xor_max16_32(float v) {
-    float a = v, b = v;
-    swap16(a, b);
-    v = fmaxf(a, b);
-    a = v;
-    b = v;
-    swap32(a, b);
-    return fmaxf(a, b);
-}
-
-__device__ __forceinline__ float xor_sum16_32(float v) {
-    float a = v, b = v;
-    swap16(a, b);
-    v = a + b;
-    a = v;
-    b = v;
-    swap32(a, b);
-    return a + b;
-}
-
 // The next K/V tile, held in registers while the current one is consumed.
 struct PfStage {
     float4 k[4];     // K rows: float4 (tid + 256 i): key (.. >> 5), dims 4 (.. & 31)

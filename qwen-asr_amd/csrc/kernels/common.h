@@ -113,6 +113,28 @@ __device__ __forceinline__ float group_max(float v) {
 
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
+// max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four row groups of an
+// MFMA 16 x 16 result that share a column) with row swaps at VALU latency
+__device__ __forceinline__ float xor_max16_32(float v) {
+    float a = v, b = v;
+    swap16(a, b);
+    v = fmaxf(a, b);
+    a = v;
+    b = v;
+    swap32(a, b);
+    return fmaxf(a, b);
+}
+
+__device__ __forceinline__ float xor_sum16_32(float v) {
+    float a = v, b = v;
+    swap16(a, b);
+    v = a + b;
+    a = v;
+    b = v;
+    swap32(a, b);
+    return a + b;
+}
+
 // Argmax order: larger value wins, lower index wins an exact tie.  This is
 // the reference's strict '>' over increasing row index (qwen_asr_kernels_avx.c
 // :223-226) and the in-order combine of per-thread winners

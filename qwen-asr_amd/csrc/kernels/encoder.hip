@@ -88,6 +88,22 @@ extern "C" int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int 
 #define EG_K 16
 #define EG_LD (EG_K + 4)
 
+// the encoder epilogues on element (m, n) of C (y points at it)
+__device__ __forceinline__ void enc_epilogue(const qk_enc_gemm_args &a, int m, int n, float v, float *y) {
+    if (a.bias_m) v += a.bias_m[m];
+    if (a.bias_n) v += a.bias_n[n];
+    if (a.pe) v += a.pe[(long)(m % a.pe_rows) * a.N + n];
+    if (a.gelu) v = enc_gelu(v);
+    if (a.col_w > 0) {
+        // stem output column n = (chunk, oh, ow): the last chunk's columns past its
+        // valid width are the zero padding the reference's next convolution sees
+        const int ow = n % a.col_w, c = n / (a.col_w * a.col_h);
+        if (c == a.col_chunks - 1 && ow >= a.col_valid) v = 0.0f;
+    }
+    if (a.add) v += *y;                    // residual (qwen_add_inplace after the projection)
+    *y = v;
+}
+
 __global__ __launch_bounds__(256) void enc_gemm(qk_enc_gemm_args a) {
     __shared__ __attribute__((aligned(16))) float sA[EG_T][EG_LD];
     __shared__ __attribute__((aligned(16))) float sB[EG_T][EG_LD];
@@ -110,13 +126,16 @@ __global__ __launch_bounds__(256) void enc_gemm(qk_enc_gemm_args a) {
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    gload(0);
-    for (int k0 = 0; k0 < a.K; k0 += EG_K) {
+    // K slice of this block: [kb, ke); kc is a multiple of EG_K, so every
+    // 16-wide step but the last one of the whole product lies inside K
+    const int kb = blockIdx.z * a.kc, ke = min(a.K, kb + a.kc);
+    gload(kb);
+    for (int k0 = kb; k0 < ke; k0 += EG_K) {
         __syncthreads();
         *reinterpret_cast<float4 *>(&sA[lr][lk]) = ra;
         *reinterpret_cast<float4 *>(&sB[lr][lk]) = rb;
         __syncthreads();
-        if (k0 + EG_K < a.K) gload(k0 + EG_K);
+        if (k0 + EG_K < ke) gload(k0 + EG_K);
         float4 af[2], bf[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const float4 *>(&sA[wm * 32 + i * 16 + (lane & 15)][4 * (lane >> 4)]);
@@ -131,6 +150,7 @@ __global__ __launch_bounds__(256) void enc_gemm(qk_enc_gemm_args a) {
     }
 
     // D[4 (l >> 4) + r][l & 15] of each 16 x 16 tile: rows m, column n
+    float *part = a.split > 1 ? a.ws + (long)blockIdx.z * a.M * a.N : nullptr;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
 #pragma unroll
@@ -140,22 +160,23 @@ __global__ __launch_bounds__(256) void enc_gemm(qk_enc_gemm_args a) {
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
                 if (m >= a.M || n >= a.N) continue;
-                float v = acc[i][j][r];
-                if (a.bias_m) v += a.bias_m[m];
-                if (a.bias_n) v += a.bias_n[n];
-                if (a.pe) v += a.pe[(long)(m % a.pe_rows) * a.N + n];
-                if (a.gelu) v = enc_gelu(v);
-                if (a.col_w > 0) {
-                    // stem output column n = (chunk, oh, ow): the last chunk's columns past its
-                    // valid width are the zero padding the reference's next convolution sees
-                    const int ow = n % a.col_w, c = n / (a.col_w * a.col_h);
-                    if (c == a.col_chunks - 1 && ow >= a.col_valid) v = 0.0f;
-                }
-                float *y = a.C + (long)m * a.ldc + n;
-                if (a.add) v += *y;                    // residual (qwen_add_inplace after the projection)
-                *y = v;
+                if (part)
+                    part[(long)m * a.N + n] = acc[i][j][r];
+                else
+                    enc_epilogue(a, m, n, acc[i][j][r], a.C + (long)m * a.ldc + n);
             }
         }
+    }
+}
+
+// split-K: C = epilogue(sum of the slices' partials, slice 0 first)
+__global__ __launch_bounds__(256) void enc_gemm_reduce(qk_enc_gemm_args a) {
+    const long MN = (long)a.M * a.N;
+    for (long e = blockIdx.x * 256L + threadIdx.x; e < MN; e += (long)gridDim.x * 256) {
+        float v = a.ws[e];
+        for (int z = 1; z < a.split; z++) v += a.ws[z * MN + e];
+        const int m = (int)(e / a.N), n = (int)(e % a.N);
+        enc_epilogue(a, m, n, v, a.C + (long)m * a.ldc + n);
     }
 }
 
@@ -163,8 +184,24 @@ extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
     if (!a || !a->A || !a->B || !a->C || a->M <= 0 || a->N <= 0 || a->K <= 0 || (a->K & 3) || (a->lda & 3) ||
         (a->ldb & 3) || a->lda < a->K || a->ldb < a->K || a->ldc < a->N || (a->pe && a->pe_rows <= 0))
         return QWEN_HIP_EINVAL;
-    dim3 grid((a->N + EG_T - 1) / EG_T, (a->M + EG_T - 1) / EG_T);
-    enc_gemm<<<grid, 256, 0, s>>>(*a);
+    qk_enc_gemm_args g = *a;
+    const long tiles = (long)((a->N + EG_T - 1) / EG_T) * ((a->M + EG_T - 1) / EG_T);
+    // slices so that the grid holds ~2 blocks per CU, each slice >= 128 deep
+    int split = a->ws ? (int)(480 / tiles) : 1;
+    if (split > 8) split = 8;
+    if (split > a->K / 128) split = a->K / 128;
+    if (split < 1) split = 1;
+    g.kc = ((a->K + split - 1) / split + EG_K - 1) / EG_K * EG_K;
+    g.split = (a->K + g.kc - 1) / g.kc;
+    if (g.split > 1 && (long)g.split * a->M * a->N > a->ws_elems) g.kc = a->K, g.split = 1;
+    if (g.split == 1) g.kc = a->K;
+    dim3 grid((a->N + EG_T - 1) / EG_T, (a->M + EG_T - 1) / EG_T, g.split);
+    enc_gemm<<<grid, 256, 0, s>>>(g);
+    if (g.split > 1) {
+        long blocks = ((long)a->M * a->N + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        enc_gemm_reduce<<<(int)blocks, 256, 0, s>>>(g);
+    }
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 
@@ -229,88 +266,99 @@ extern "C" int qk_enc_layernorm_launch(const float *x, const float *w, const flo
 }
 
 // ---------------------------------------------------------------------------
-// Windowed bidirectional attention, head_dim 64.  Block = (64 query rows, head);
-// four lanes per query row (16 dims each), online softmax over the keys of
-// the row's window [ws, we); K/V rows of the windows the block touches are
-// staged in LDS 32 at a time.  qkv: [T][3 * H * 64] (q | k | v per token).
+// Windowed bidirectional attention, head_dim 64, on the fp32 matrix cores.
+// Block = one wave: 16 queries of one window, one head.  S^T = K Q^T and
+// O^T += V^T P^T on v_mfma_f32_16x16x4_f32: lane l holds query l & 15, keys
+// (first product) and dims (second) 4 (l >> 4) + r of each 16-row tile, so
+// the scores come out in the register layout the second product takes as
+// its B operand.  Online softmax over blocks of 64 keys of the window
+// [ws, we); K and V are read straight from qkv [T][3 H 64] (q | k | v).
 // ---------------------------------------------------------------------------
-#define EA_ROWS 64
-#define EA_TILE 32
+#define EA_Q 16
+#define EA_KB 64
 
-__global__ __launch_bounds__(256) void enc_attention(const float *qkv, float *out, int T, int H, int win, float scale) {
+__global__ __launch_bounds__(64) void enc_attention(const float *qkv, float *out, int T, int H, int win, float scale) {
     constexpr int hd = 64;
-    __shared__ float4 sk[EA_TILE][hd / 4];
-    __shared__ float4 sv[EA_TILE][hd / 4];
-    const int h = blockIdx.y;
-    const int qi = blockIdx.x * EA_ROWS + (threadIdx.x >> 2);
-    const int quarter = threadIdx.x & 3;
+    const int lane = threadIdx.x, h = blockIdx.y;
+    const int lq = lane & 15, lg = lane >> 4;
+    const int tpw = (win + EA_Q - 1) / EA_Q;
+    const int ws = (blockIdx.x / tpw) * win, we = min(T, ws + win);
+    const int q0 = ws + (blockIdx.x % tpw) * EA_Q;
+    if (q0 >= we) return;                              // whole block: a short last window
     const long stride = 3L * H * hd;
-    const bool valid = qi < T;
-    const int q0 = blockIdx.x * EA_ROWS;
-    const int q1 = min(T, q0 + EA_ROWS) - 1;
-    const int kb0 = (q0 / win) * win, kb1 = min(T, (q1 / win + 1) * win);   // union of the rows' windows
-    const int ws = valid ? (qi / win) * win : 0, we = valid ? min(T, ws + win) : 0;
+    const int qi = q0 + lq;
+    const float *qrow = qkv + (long)min(qi, T - 1) * stride + h * hd;
+    const float *kbase = qkv + (long)H * hd + h * hd, *vbase = qkv + 2L * H * hd + h * hd;
 
-    float4 q[4], o[4];
+    float4 q[4];                                       // Q^T operand: dims 16 kb + 4 lg + c
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        q[j] = valid ? *reinterpret_cast<const float4 *>(qkv + (long)qi * stride + h * hd + quarter * 16 + 4 * j)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-        o[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    float m = -1e30f, l = 0.0f;                       // the reference's max_score start
-    for (int t0 = kb0; t0 < kb1; t0 += EA_TILE) {
-        const int nk = min(EA_TILE, kb1 - t0);
-        __syncthreads();
-        for (int e = threadIdx.x; e < EA_TILE * hd / 4; e += 256) {
-            const int r = e / (hd / 4), c = e % (hd / 4);
-            if (r < nk) {
-                const float *row = qkv + (long)(t0 + r) * stride + h * hd;
-                sk[r][c] = *reinterpret_cast<const float4 *>(row + H * hd + c * 4);
-                sv[r][c] = *reinterpret_cast<const float4 *>(row + 2 * H * hd + c * 4);
+    for (int kb = 0; kb < 4; kb++) q[kb] = *reinterpret_cast<const float4 *>(qrow + 16 * kb + 4 * lg);
+    f32x4 o[4];                                        // O^T[16 dt + 4 lg + r][query lq]
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m = -1e30f, l = 0.0f;                        // the reference's max_score start
+
+    for (int k0 = ws; k0 < we; k0 += EA_KB) {
+        float p[4][4];                                 // key k0 + 16 t + 4 lg + r
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float *krow = kbase + (long)min(k0 + 16 * t + lq, T - 1) * stride;
+            f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const float4 kk = *reinterpret_cast<const float4 *>(krow + 16 * kb + 4 * lg);
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc = enc_mfma((&kk.x)[c], (&q[kb].x)[c], acc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                p[t][r] = k0 + 16 * t + 4 * lg + r < we ? acc[r] * scale : -INFINITY;
+                mx = fmaxf(mx, p[t][r]);
             }
         }
-        __syncthreads();
-        for (int j = 0; j < nk; j++) {
-            float d = 0.0f;
+        mx = xor_max16_32(mx);
+        const float mn = fmaxf(m, mx);
+        const float corr = __expf(m - mn);
+        float sum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                p[t][r] = __expf(p[t][r] - mn);
+                sum += p[t][r];
+            }
+        l = fmaf(l, corr, sum);                        // this lane's keys; lane groups summed at the end
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) o[dt] *= corr;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            if (k0 + 16 * t >= we) break;              // uniform: the tile holds no key of the window
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const float4 kk = sk[j][quarter * 4 + c];
-                d = fmaf(q[c].x, kk.x, d);
-                d = fmaf(q[c].y, kk.y, d);
-                d = fmaf(q[c].z, kk.z, d);
-                d = fmaf(q[c].w, kk.w, d);
-            }
-            d = group_sum<4>(d);
-            const int key = t0 + j;
-            if (key >= ws && key < we) {
-                const float sc = d * scale;
-                const float mn = fmaxf(m, sc);
-                const float corr = __expf(m - mn), pw = __expf(sc - mn);
-                l = fmaf(l, corr, pw);
+                const float *vrow = vbase + (long)min(k0 + 16 * t + 4 * lg + c, T - 1) * stride;
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const float4 vv = sv[j][quarter * 4 + c];
-                    o[c].x = fmaf(o[c].x, corr, pw * vv.x);
-                    o[c].y = fmaf(o[c].y, corr, pw * vv.y);
-                    o[c].z = fmaf(o[c].z, corr, pw * vv.z);
-                    o[c].w = fmaf(o[c].w, corr, pw * vv.w);
-                }
-                m = mn;
+                for (int dt = 0; dt < 4; dt++) o[dt] = enc_mfma(vrow[16 * dt + lq], p[t][c], o[dt]);
             }
         }
     }
-    if (!valid) return;
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    float4 *op = reinterpret_cast<float4 *>(out + (long)qi * H * hd + h * hd + quarter * 16);
+    l = xor_sum16_32(l);
+    if (qi >= we) return;
+    const float inv = 1.0f / l;
+    float *orow = out + (long)qi * H * hd + h * hd + 4 * lg;
 #pragma unroll
-    for (int c = 0; c < 4; c++) op[c] = make_float4(o[c].x * inv, o[c].y * inv, o[c].z * inv, o[c].w * inv);
+    for (int dt = 0; dt < 4; dt++)
+        *reinterpret_cast<float4 *>(orow + 16 * dt) =
+            make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
 }
 
 extern "C" int qk_enc_attention_launch(const float *qkv, float *out, int T, int H, int hd, int win, float scale,
                                        hipStream_t s) {
     if (!qkv || !out || T <= 0 || H <= 0 || hd != 64 || win <= 0) return QWEN_HIP_EINVAL;
-    dim3 grid((T + EA_ROWS - 1) / EA_ROWS, H);
-    enc_attention<<<grid, 256, 0, s>>>(qkv, out, T, H, win, scale);
+    const long nwin = (T + win - 1) / win, tpw = (win + EA_Q - 1) / EA_Q;
+    if (nwin * tpw > 0x7fffffffL) return QWEN_HIP_EINVAL;
+    dim3 grid((unsigned)(nwin * tpw), H);
+    enc_attention<<<grid, 64, 0, s>>>(qkv, out, T, H, win, scale);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }

@@ -242,7 +242,11 @@ int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, fl
 /* C[M][N] (=, +=) A[M][K] . B[N][K]^T (+ bias_m[m] | bias_n[n]) (+ pe[m % pe_rows][n])
  * (GELU); K and the leading dimensions multiples of 4.  col_w > 0: stem
  * output, column n = (chunk, oh, ow) with col_h x col_w per chunk; the last
- * chunk's columns with ow >= col_valid are written as 0. */
+ * chunk's columns with ow >= col_valid are written as 0.  ws: optional
+ * workspace of ws_elems floats; when the tile grid is too small to fill the
+ * chip, K is split over up to 8 slices whose raw partials go to ws and are
+ * summed in slice order by a second kernel that applies the epilogue
+ * (deterministic).  kc / split are set by the launcher. */
 typedef struct {
     const float *A, *B;
     float *C;
@@ -250,7 +254,11 @@ typedef struct {
     const float *bias_m, *bias_n, *pe;
     int pe_rows, gelu, add;
     int col_w, col_h, col_chunks, col_valid;
+    float *ws;
+    long ws_elems;
+    int kc, split;
 } qk_enc_gemm_args;
+#define QK_ENC_GEMM_WS_ELEMS (512L * 64 * 64)   /* enough for every split the launcher picks */
 int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s);
 int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int chunks, int h_in, int w_in, int h_out,
                          int w_out, int kpad, int mel_frames, hipStream_t s);

@@ -48,3 +48,38 @@ def write_checkpoint(model, path, shards=1, norm_bf16=False, extra=None):
         save_file(part, os.path.join(path, f"model-{k + 1:05d}-of-{shards:05d}.safetensors"),
                   metadata={"format": "pt"})
     return names
+
+
+ENC_LAYER_NAMES = ("self_attn.q_proj.weight", "self_attn.q_proj.bias", "self_attn.k_proj.weight",
+                   "self_attn.k_proj.bias", "self_attn.v_proj.weight", "self_attn.v_proj.bias",
+                   "self_attn.out_proj.weight", "self_attn.out_proj.bias", "self_attn_layer_norm.weight",
+                   "self_attn_layer_norm.bias", "fc1.weight", "fc1.bias", "fc2.weight", "fc2.bias",
+                   "final_layer_norm.weight", "final_layer_norm.bias")
+ENC_STEM_NAMES = ("conv2d1.weight", "conv2d1.bias", "conv2d2.weight", "conv2d2.bias", "conv2d3.weight",
+                  "conv2d3.bias", "conv_out.weight", "ln_post.weight", "ln_post.bias", "proj1.weight",
+                  "proj1.bias", "proj2.weight", "proj2.bias")
+ENC_STEM_SHAPES = {"conv2d1.weight": (480, 1, 3, 3), "conv2d2.weight": (480, 480, 3, 3),
+                   "conv2d3.weight": (480, 480, 3, 3)}
+
+
+def enc_tensors(enc):
+    """thinker.audio_tower.* of the encoder loader (qwen_asr_encoder.c:67-168)
+    from a pyoracle.SynthEncoder: matrices as BF16 (the synthetic ones are
+    bf16 values, so exact), vectors as F32."""
+    def put(t, name, a):
+        a = np.ascontiguousarray(a, np.float32)
+        if a.ndim >= 2:
+            bits = (a.view(np.uint32) >> 16).astype(np.uint16)
+            t[name] = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+        else:
+            t[name] = torch.from_numpy(a)
+
+    t = {}
+    for l, arrs in enumerate(enc.layers):
+        for name, a in zip(ENC_LAYER_NAMES, arrs):
+            put(t, f"thinker.audio_tower.layers.{l}.{name}", a)
+    for name, a in zip(ENC_STEM_NAMES, enc.stem):
+        if name in ENC_STEM_SHAPES:
+            a = np.asarray(a).reshape(ENC_STEM_SHAPES[name])
+        put(t, f"thinker.audio_tower.{name}", a)
+    return t

@@ -103,3 +103,21 @@ def test_reader_rejects_bad_files(qa, tmp_path):
     assert len(ck) == 1 and ck.tensor("a")[1] == (4,)
     with pytest.raises(RuntimeError, match="embed_tokens"):
         ck.config()
+
+
+def test_encoder_config_from_tensor_shapes(P, qa, tmp_path):
+    """qwen_hip_checkpoint_enc_config: d_model from conv_out rows, ffn from fc1
+    rows, output_dim from proj2 rows, layers counted, 64-wide heads (the
+    encoder part of the reference's detect_config); a checkpoint without an
+    audio tower is refused with a message."""
+    from safetensors.torch import save_file
+    from ckpt_util import enc_tensors
+    cfg = qa.EncConfig(128, 3, 2, 64, 256, 96, 100, 800)
+    t = enc_tensors(P.SynthEncoder(cfg, seed=2))
+    save_file(t, str(tmp_path / "model.safetensors"))
+    got = qa.Checkpoint(str(tmp_path)).enc_config()
+    assert [getattr(got, f) for f, _ in qa.EncConfig._fields_] == [128, 3, 2, 64, 256, 96, 100, 800]
+    del t["thinker.audio_tower.proj2.weight"]
+    save_file(t, str(tmp_path / "model.safetensors"))
+    with pytest.raises(RuntimeError, match="no audio encoder"):
+        qa.Checkpoint(str(tmp_path)).enc_config()

@@ -112,3 +112,28 @@ def test_encoder_rows_feed_the_decoder(P, qa, gpu):
     assert T == rows.shape[0] and t_dev == t_host
     d.close()
     e.close()
+
+
+def test_encoder_from_checkpoint(P, qa, gpu, tmp_path):
+    """thinker.audio_tower.* read from a safetensors checkpoint (BF16 matrices,
+    F32 vectors, two shards): shape taken from the tensors, chunk 100 and
+    attention window 800 frames as the reference fixes them (qwen_asr.c:182-184),
+    output bit-identical to the same weights loaded by hand with that config"""
+    import ckpt_util
+    from safetensors.torch import save_file
+    g = fixture("enc_tiny")
+    cfg, m, mel = build(qa, P, g)
+    t = ckpt_util.enc_tensors(m)
+    names = sorted(t)
+    half = len(names) // 2
+    save_file({n: t[n] for n in names[:half]}, str(tmp_path / "model-00001-of-00002.safetensors"))
+    save_file({n: t[n] for n in names[half:]}, str(tmp_path / "model-00002-of-00002.safetensors"))
+    e = qa.Encoder.from_checkpoint(str(tmp_path), 0)
+    cfg.n_window_infer = 800
+    for f, _ in qa.EncConfig._fields_:
+        assert getattr(e.cfg, f) == getattr(cfg, f), f
+    out = e.forward(mel)
+    ref_h = load(qa, cfg, m)
+    np.testing.assert_array_equal(out, ref_h.forward(mel))
+    e.close()
+    ref_h.close()
