@@ -179,6 +179,48 @@ def run_gemv_sweep(qa, threads, with_cpu):
     return out
 
 
+def run_lm_shard(qa):
+    """One GPU's share of a vocabulary-sharded LM head: the logit GEMV
+    (qwen_hip_linear_nobias_bf16, seq 1) over 1/N of the 151936 rows at the
+    real hidden sizes, cold weights (rotation over >= 1 GiB of copies), timed
+    with HIP events.  (The argmax op synchronises the host per call; the
+    persistent engine fuses the argmax into this pass.)  The exchange of the
+    N (logit, index) pairs is not part of a one-GPU run."""
+    import numpy as np
+    import torch
+    out = []
+    for K in (1024, 2048):
+        for n in (1, 8):
+            R = -(-151936 // n)
+            W = qa.synth_bf16(R * K, 0, 9200 + K + n).reshape(R, K)
+            x = qa.synth_uniform(K, 0, 9300 + K)
+            wbytes = 2 * R * K
+            copies = max(4, -(-(1 << 30) // wbytes))
+            dW0 = torch.from_numpy(W.view(np.int16)).to("cuda")
+            dWs = [dW0] + [dW0.clone() for _ in range(copies - 1)]
+            dx = torch.from_numpy(x).to("cuda")
+            dy = torch.empty(R, dtype=torch.float32, device="cuda")
+            lib = qa.lib()
+            call = lambda w: lib.qwen_hip_linear_nobias_bf16(dy.data_ptr(), dx.data_ptr(), w.data_ptr(), 1, K, R, None)
+            for i in range(copies):
+                call(dWs[i])
+            reps = max(copies * 4, 64)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(reps):
+                call(dWs[i % copies])
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            gbs = (wbytes + 4 * K + 4 * R) / (us * 1e-6) / 1e9
+            log(f"[gpu] LM-head logits, 1/{n} of the vocabulary ({R} x {K}): {us:.2f} us, {gbs:.0f} GB/s")
+            out.append({"shards": n, "rows": R, "cols": K, "us": round(us, 3), "gb_s": round(gbs, 1)})
+            del dWs, dW0
+            torch.cuda.empty_cache()
+    return out
+
+
 def run_streaming(qa, d, cfg, chunks):
     """The C5 op pattern (the reference's streaming KV reuse, qwen_asr.c:1748-1829):
     a 9-row template head, then per chunk: roll the KV back by the last 5
@@ -377,6 +419,7 @@ def main():
                    "kind": "reference",
                    "sample": "the reference's qwen_linear_nobias_bf16 (oracle/_ref, seq 1 threaded matvec) on "
                              "each shape, >= 0.5 s per shape; value = all shapes' bytes / summed time"}
+        shard = run_lm_shard(qa)
         print(json.dumps({
             "metric": "bf16 GEMV GB/s (C2 sweep)", "value": round(tot_b / (tot_us * 1e-6) / 1e9, 1),
             "unit": "GB/s", "n_gpus": 1, "steps": len(rows), "warmup": 1,
@@ -386,7 +429,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": big["gb_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": big["frac"], "traffic": None,
                          "kernel": f"gemv {big['rows']}x{big['cols']} (largest shape)"},
-            "per_shape": rows, "cpu_baseline": cpu}), flush=True)
+            "per_shape": rows, "lm_head_shard_share": shard, "cpu_baseline": cpu}), flush=True)
         return
     if args.workload == "enc":
         run_encoder(qa, args, wl)

@@ -261,16 +261,37 @@ __global__ __launch_bounds__(64) void attn_prefill_merge(qk_attn_args a) {
     const int n = (kend_tile + a.chunk - 1) / a.chunk;
     const size_t stride = (size_t)a.seq_q * a.heads * QK_PF_PART;
     const float *p0 = a.part + ((size_t)qi * a.heads + h) * QK_PF_PART;
+    // batches of 8 splits: the loads of a batch are issued together, the sums
+    // still run in split order
+    constexpr int MB = 8;
     float M = PF_MINIT;
-    for (int s = 0; s < n; s++) M = fmaxf(M, p0[s * stride + hd]);
+    for (int s0 = 0; s0 < n; s0 += MB) {
+        float mv[MB];
+#pragma unroll
+        for (int j = 0; j < MB; j++) mv[j] = s0 + j < n ? p0[(s0 + j) * stride + hd] : PF_MINIT;
+#pragma unroll
+        for (int j = 0; j < MB; j++) M = fmaxf(M, mv[j]);
+    }
     float L = 0.0f, ox = 0.0f, oy = 0.0f;
-    for (int s = 0; s < n; s++) {
-        const float *p = p0 + s * stride;
-        const float w = __expf(p[hd] - M);
-        L = fmaf(p[hd + 1], w, L);
-        const float2 v = *reinterpret_cast<const float2 *>(p + 2 * lane);
-        ox = fmaf(v.x, w, ox);
-        oy = fmaf(v.y, w, oy);
+    for (int s0 = 0; s0 < n; s0 += MB) {
+        float mv[MB], lv[MB];
+        float2 v[MB];
+#pragma unroll
+        for (int j = 0; j < MB; j++) {
+            const bool in = s0 + j < n;
+            const float *p = p0 + (in ? s0 + j : 0) * stride;
+            mv[j] = p[hd];
+            lv[j] = p[hd + 1];
+            v[j] = *reinterpret_cast<const float2 *>(p + 2 * lane);
+        }
+#pragma unroll
+        for (int j = 0; j < MB; j++) {
+            // a split past n adds lv * 0 and v * 0 (finite values of split 0): no change
+            const float w = s0 + j < n ? __expf(mv[j] - M) : 0.0f;
+            L = fmaf(lv[j], w, L);
+            ox = fmaf(v[j].x, w, ox);
+            oy = fmaf(v[j].y, w, oy);
+        }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     const size_t base = (size_t)qi * a.heads * hd + h * hd + 2 * lane;

@@ -113,6 +113,36 @@ __device__ __forceinline__ float group_max(float v) {
 
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
+// p[0] + p[stride] + ... + p[(n - 1) stride], 1 <= n <= N, added left to
+// right as a plain loop would; the n loads are issued together, so summing n
+// split-K partials costs one memory latency instead of n.
+template <int N>
+__device__ __forceinline__ float sum_splits(const float *p, int n, long stride) {
+    float v[N];
+#pragma unroll
+    for (int s = 0; s < N; s++) v[s] = s < n ? p[s * stride] : 0.0f;
+    float acc = v[0];
+#pragma unroll
+    for (int s = 1; s < N; s++)
+        if (s < n) acc += v[s];
+    return acc;
+}
+
+template <int N>
+__device__ __forceinline__ float2 sum_splits2(const float2 *p, int n, long stride) {
+    float2 v[N];
+#pragma unroll
+    for (int s = 0; s < N; s++) v[s] = s < n ? p[s * stride] : make_float2(0.0f, 0.0f);
+    float2 acc = v[0];
+#pragma unroll
+    for (int s = 1; s < N; s++)
+        if (s < n) {
+            acc.x += v[s].x;
+            acc.y += v[s].y;
+        }
+    return acc;
+}
+
 // max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four row groups of an
 // MFMA 16 x 16 result that share a column) with row swaps at VALU latency
 __device__ __forceinline__ float xor_max16_32(float v) {

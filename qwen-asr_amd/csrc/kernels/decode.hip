@@ -357,9 +357,7 @@ extern "C" int qk_argmax_finish_launch(const float *cand_val, const int *cand_id
 // ---------------------------------------------------------------------------
 // Element i of the projection row: the sum of its nsum split-K partials.
 __device__ __forceinline__ float qkv_at(const float *p, int nsum, long pstride) {
-    float v = p[0];
-    for (int s = 1; s < nsum; s++) v += p[s * pstride];
-    return v;
+    return sum_splits<QK_GEMM_MAX_SPLIT>(p, nsum, pstride);
 }
 
 __global__ __launch_bounds__(64) void rope_append(qk_rope_append_args a) {
@@ -401,7 +399,9 @@ __global__ __launch_bounds__(64) void rope_append(qk_rope_append_args a) {
 }
 
 extern "C" int qk_rope_append_launch(const qk_rope_append_args *a, hipStream_t s) {
-    if (!a || a->S <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads) return QWEN_HIP_EINVAL;
+    if (!a || a->S <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads ||
+        a->nsum > QK_GEMM_MAX_SPLIT)
+        return QWEN_HIP_EINVAL;
     dim3 grid(a->heads + a->kv_heads, a->S);
     rope_append<<<grid, 64, 0, s>>>(*a);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;

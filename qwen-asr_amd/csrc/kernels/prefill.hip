@@ -19,6 +19,20 @@ __device__ __forceinline__ void split2(float v, uint16_t &hi, uint16_t &lo) {
     lo = f32_to_bf16_rne(v - bf16_to_f32(hi));
 }
 
+// sum over the NW waves of a block (red: NW floats of LDS)
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; i++) s += red[i];
+    return s;
+}
+
 __device__ __forceinline__ float block_sum256(float v, float *red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     v = wave_sum(v);
@@ -35,30 +49,31 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
 // projection that produced it, summed in split order), which is the
 // residual add of qwen_asr_decoder.c:318 / :331.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void rmsnorm_split(float *x, const float *part, int nsum, long pstride,
-                                                     const float *w, int D, float eps, uint16_t *hi, uint16_t *lo) {
-    __shared__ float red[4];
+// 1024 threads per row: each thread's split partials are one batch of loads
+// (D = 1024: one element per thread), so the row costs one memory latency.
+#define RN_THREADS 1024
+__global__ __launch_bounds__(RN_THREADS) void rmsnorm_split(float *x, const float *part, int nsum, long pstride,
+                                                            const float *w, int D, float eps, uint16_t *hi,
+                                                            uint16_t *lo) {
+    __shared__ float red[RN_THREADS / 64];
     float *xr = x + (size_t)blockIdx.x * D;
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < D; i += 256) {
+    for (int i = threadIdx.x; i < D; i += RN_THREADS) {
         float v = xr[i];
         if (nsum) {
-            const float *pr = part + (size_t)blockIdx.x * D + i;
-            float add = pr[0];
-            for (int sp = 1; sp < nsum; sp++) add += pr[sp * pstride];
-            v += add;
+            v += sum_splits<QK_GEMM_MAX_SPLIT>(part + (size_t)blockIdx.x * D + i, nsum, pstride);
             xr[i] = v;
         }
         ss = fmaf(v, v, ss);
     }
     float rinv = 1.0f;
     if (w) {
-        ss = block_sum256(ss, red);
+        ss = block_sum<RN_THREADS / 64>(ss, red);
         rinv = 1.0f / sqrtf(ss / (float)D + eps);
     }
     if (!hi) return;
     uint16_t *h = hi + (size_t)blockIdx.x * D, *l = lo + (size_t)blockIdx.x * D;
-    for (int i = threadIdx.x; i < D; i += 256) {      // each thread re-reads only what it wrote
+    for (int i = threadIdx.x; i < D; i += RN_THREADS) {   // each thread re-reads only what it wrote
         const float v = w ? (xr[i] * w[i]) * rinv : xr[i];
         split2(v, h[i], l[i]);
     }
@@ -66,9 +81,10 @@ __global__ __launch_bounds__(256) void rmsnorm_split(float *x, const float *part
 
 extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride, const float *w, int S,
                                        int D, float eps, uint16_t *hi, uint16_t *lo, hipStream_t s) {
-    if (S <= 0 || D <= 0 || !x || nsum < 0 || (nsum && !part) || (!hi) != (!lo) || (!hi && !nsum))
+    if (S <= 0 || D <= 0 || !x || nsum < 0 || nsum > QK_GEMM_MAX_SPLIT || (nsum && !part) || (!hi) != (!lo) ||
+        (!hi && !nsum))
         return QWEN_HIP_EINVAL;
-    rmsnorm_split<<<S, 256, 0, s>>>(x, part, nsum, pstride, w, D, eps, hi, lo);
+    rmsnorm_split<<<S, RN_THREADS, 0, s>>>(x, part, nsum, pstride, w, D, eps, hi, lo);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 
@@ -246,13 +262,7 @@ __global__ __launch_bounds__(256) void gemm_reduce(const float *part, int nsum, 
                                                    uint16_t *ohi, uint16_t *olo) {
     const long pairs = M * N / 2, pstride = M * N;
     for (long t = blockIdx.x * 256L + threadIdx.x; t < pairs; t += (long)gridDim.x * 256) {
-        const float2 *p = reinterpret_cast<const float2 *>(part) + t;
-        float2 v = p[0];
-        for (int sp = 1; sp < nsum; sp++) {
-            const float2 w = p[sp * pstride / 2];
-            v.x += w.x;
-            v.y += w.y;
-        }
+        const float2 v = sum_splits2<QK_GEMM_MAX_SPLIT>(reinterpret_cast<const float2 *>(part) + t, nsum, pstride / 2);
         if (EPI == QK_GEMM_SWIGLU) {
             split2(swiglu1(v.x, v.y), ohi[t], olo[t]);
         } else if (EPI == QK_GEMM_ADD) {
@@ -269,7 +279,7 @@ __global__ __launch_bounds__(256) void gemm_reduce(const float *part, int nsum, 
 
 extern "C" int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, float *y, uint16_t *out_hi,
                                      uint16_t *out_lo, hipStream_t s) {
-    if (!part || nsum < 1 || M <= 0 || N <= 0 || (N & 1)) return QWEN_HIP_EINVAL;
+    if (!part || nsum < 1 || nsum > QK_GEMM_MAX_SPLIT || M <= 0 || N <= 0 || (N & 1)) return QWEN_HIP_EINVAL;
     if (epi == QK_GEMM_SWIGLU ? (!out_hi || !out_lo) : !y) return QWEN_HIP_EINVAL;
     long blocks = ((long)M * N / 2 + 255) / 256;
     if (blocks > 2048) blocks = 2048;

@@ -172,6 +172,39 @@ def test_causal_attention_long_unsplit(P, qa, gpu):
     assert worst <= 0.0, worst
 
 
+@pytest.mark.parametrize("shards", [2, 8])
+def test_vocab_sharded_argmax(P, qa, gpu, shards):
+    """The LM head as it would shard over GPUs: each shard runs the argmax op
+    on its contiguous vocabulary slice, the (logit, global index) pairs are
+    combined by larger logit, then lower index; the result equals the argmax
+    over the whole vocabulary, also with exact ties placed in different
+    shards.  Logits of the slice winners come from the GEMV op on the slice."""
+    K, N = 1024, 151936
+    W = P.synth_bf16(N * K, 4, 1).reshape(N, K)
+    x = P.synth_uniform(K, 4, 2)
+    W2 = W.copy()
+    full = P.orc_lib().orc_argmax_matvec_bf16(x, W, K, N, None)
+    W2[3] = W[full]
+    W2[N - 1] = W[full]
+    dx = dev(gpu, x)
+    for Wt, want in ((W, full), (W2, 3)):
+        dW = dev(gpu, Wt.view(np.int16))
+        esz = dW.element_size()
+        best = None
+        for i in range(shards):
+            r0, r1 = N * i // shards, N * (i + 1) // shards
+            wp = ptr(dW) + r0 * K * esz
+            loc = qa.check(qa.lib().qwen_hip_argmax_matvec_bf16(ptr(dx), wp, K, r1 - r0, None))
+            dy = gpu.empty(r1 - r0, dtype=gpu.float32, device="cuda")
+            qa.check(qa.lib().qwen_hip_linear_nobias_bf16(ptr(dy), ptr(dx), wp, 1, K, r1 - r0, None), "gemv")
+            gpu.cuda.synchronize()
+            cand = (float(host(dy)[loc]), r0 + loc)
+            if best is None or cand[0] > best[0] or (cand[0] == best[0] and cand[1] < best[1]):
+                best = cand
+        assert best[1] == want, (best, want)
+        assert qa.lib().qwen_hip_argmax_matvec_bf16(ptr(dx), ptr(dW), K, N, None) == want
+
+
 def test_argmax_matvec(P, qa, gpu):
     K, N = 1024, 151936
     W = P.synth_bf16(N * K, 4, 1).reshape(N, K)
