@@ -192,6 +192,19 @@ struct PxKv {
             v[j][1] = in ? px_ldf4(vb, o + 16u) : z;
         }
     }
+    // the same rows, every load issued: positions >= end read position 0
+    // (finite: the cache is zeroed when allocated) and must not be folded
+    __device__ __forceinline__ void load_all(const float *kb, const float *vb, int gl, int p0, int stride, int end) {
+#pragma unroll
+        for (int j = 0; j < AB; j++) {
+            const int p = p0 + stride * j;
+            const unsigned o = (unsigned)((p < end ? p : 0) * 128 + gl * 8) * 4u;
+            k[j][0] = px_ldf4(kb, o);
+            k[j][1] = px_ldf4(kb, o + 16u);
+            v[j][0] = px_ldf4(vb, o);
+            v[j][1] = px_ldf4(vb, o + 16u);
+        }
+    }
 };
 
 // Issue the first K/V batch of a split straight into LDS (no registers held
@@ -791,14 +804,35 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     }
                     px_fold_n<AB>(q, kk, vv, in, a.scale, m, lsum, o);
                 }
-                // longer splits continue in register batches
-                for (int pb = sp.s0 + gid + NG * AB; pb < sp.cend; pb += NG * AB) {
-                    PxKv<AB> kv;
-                    kv.load(kcl, vcl, gl, pb, NG, sp.cend);
-                    bool in[AB];
+                // longer splits continue in register batches.  0.6B: two per pass,
+                // both batches' loads issued together, so the second one's memory
+                // latency passes during the first one's fold (block-uniform loop;
+                // a second batch wholly past the split is loaded from position 0,
+                // which stays in L2, and skipped).  1.7B (fewer registers per
+                // wave): one batch at a time.
+                if (!DEEP) {
+                    for (int pb = sp.s0 + gid + NG * AB; pb < sp.cend; pb += NG * AB) {
+                        PxKv<AB> kv;
+                        kv.load(kcl, vcl, gl, pb, NG, sp.cend);
+                        bool in[AB];
 #pragma unroll
-                    for (int j = 0; j < AB; j++) in[j] = pb + NG * j < sp.cend;
-                    px_fold_n<AB>(q, kv.k, kv.v, in, a.scale, m, lsum, o);
+                        for (int j = 0; j < AB; j++) in[j] = pb + NG * j < sp.cend;
+                        px_fold_n<AB>(q, kv.k, kv.v, in, a.scale, m, lsum, o);
+                    }
+                }
+                for (int b0 = sp.s0 + NG * AB; DEEP && b0 < sp.cend; b0 += 2 * NG * AB) {
+                    const int b1 = b0 + NG * AB;
+                    PxKv<AB> k0, k1;
+                    k0.load_all(kcl, vcl, gl, b0 + gid, NG, sp.cend);
+                    k1.load_all(kcl, vcl, gl, b1 + gid, NG, sp.cend);
+                    bool in0[AB], in1[AB];
+#pragma unroll
+                    for (int j = 0; j < AB; j++) {
+                        in0[j] = b0 + gid + NG * j < sp.cend;
+                        in1[j] = b1 + gid + NG * j < sp.cend;
+                    }
+                    px_fold_n<AB>(q, k0.k, k0.v, in0, a.scale, m, lsum, o);
+                    if (b1 < sp.cend) px_fold_n<AB>(q, k1.k, k1.v, in1, a.scale, m, lsum, o);
                 }
                 if (sp.last && gid == 0) {   // position pos: this step's k/v
                     const float4 *kn = reinterpret_cast<const float4 *>(&S.kr[gl * 8]);

@@ -91,7 +91,7 @@ extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, lo
 // ---------------------------------------------------------------------------
 // GEMM on v_mfma_f32_16x16x32_bf16.  Block tile BM x BN = (WGM TM 16) x
 // (WGN TN 16): 4 waves in a WGM x WGN grid, each TM x TN MFMA tiles of 16x16.
-// K is walked 64 at a time through two LDS buffers: the next tile's global
+// K is walked QK_BK (64) at a time through two LDS buffers: the next tile's global
 // loads are in flight (in registers) while the current one feeds the MFMAs,
 // then land in the other buffer; one barrier per k tile.  Operand fragments:
 // lane l supplies row (l & 15) and the 8 consecutive k values [8 (l >> 4), +8)
@@ -113,7 +113,8 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
                                                  float *y, uint16_t *ohi, uint16_t *olo) {
     static_assert(WGM * WGN == 4, "4 waves");
     constexpr int BM = WGM * TM * 16, BN = WGN * TN * 16;
-    constexpr int ACH = BM * (QK_BK / 8), BCH = BN * (QK_BK / 8);   // 16-byte chunks per tile
+    constexpr int CPR = QK_BK / 8;                                   // 16-byte chunks per row
+    constexpr int ACH = BM * CPR, BCH = BN * CPR;                    // 16-byte chunks per tile
     constexpr int APT = (ACH + 255) / 256, BPT = (BCH + 255) / 256;
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][2][BM][QK_LDK];   // [buffer][hi, lo]
     __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN][QK_LDK];
@@ -126,14 +127,14 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
     auto gload = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < APT; i++) {
-            const int c = tid + 256 * i, r = c >> 3, gm = m0 + r, gk = k0 + (c & 7) * 8;
+            const int c = tid + 256 * i, r = c / CPR, gm = m0 + r, gk = k0 + (c % CPR) * 8;
             const bool ok = (ACH % 256 == 0 || c < ACH) && gm < M && gk < ke;
             ra[0][i] = ok ? *reinterpret_cast<const uint4 *>(ahi + (size_t)gm * K + gk) : make_uint4(0u, 0u, 0u, 0u);
             ra[1][i] = ok ? *reinterpret_cast<const uint4 *>(alo + (size_t)gm * K + gk) : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int i = 0; i < BPT; i++) {
-            const int c = tid + 256 * i, r = c >> 3, gn = n0 + r, gk = k0 + (c & 7) * 8;
+            const int c = tid + 256 * i, r = c / CPR, gn = n0 + r, gk = k0 + (c % CPR) * 8;
             const bool ok = (BCH % 256 == 0 || c < BCH) && gn < N && gk < ke;
             rb[i] = ok ? ld_stream16(W + (size_t)gn * K + gk) : make_uint4(0u, 0u, 0u, 0u);
         }
@@ -143,14 +144,14 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
         for (int i = 0; i < APT; i++) {
             const int c = tid + 256 * i;
             if (ACH % 256 == 0 || c < ACH) {
-                *reinterpret_cast<uint4 *>(&sA[buf][0][c >> 3][(c & 7) * 8]) = ra[0][i];
-                *reinterpret_cast<uint4 *>(&sA[buf][1][c >> 3][(c & 7) * 8]) = ra[1][i];
+                *reinterpret_cast<uint4 *>(&sA[buf][0][c / CPR][(c % CPR) * 8]) = ra[0][i];
+                *reinterpret_cast<uint4 *>(&sA[buf][1][c / CPR][(c % CPR) * 8]) = ra[1][i];
             }
         }
 #pragma unroll
         for (int i = 0; i < BPT; i++) {
             const int c = tid + 256 * i;
-            if (BCH % 256 == 0 || c < BCH) *reinterpret_cast<uint4 *>(&sB[buf][c >> 3][(c & 7) * 8]) = rb[i];
+            if (BCH % 256 == 0 || c < BCH) *reinterpret_cast<uint4 *>(&sB[buf][c / CPR][(c % CPR) * 8]) = rb[i];
         }
     };
 
