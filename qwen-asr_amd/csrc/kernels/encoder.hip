@@ -43,38 +43,62 @@ __device__ __forceinline__ float enc_gelu(float v) {
 // frames past `frames` read as 0).  cols: [chunks*h_out*w_out][kpad], the
 // columns past c_in*9 zero.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void enc_im2col(const float *in, float *cols, int c_in, int chunks, int h_in,
-                                                  int w_in, int h_out, int w_out, int kpad, int mel_frames) {
-    const long rows = (long)chunks * h_out * w_out;
-    const long total = rows * kpad;
-    for (long e = blockIdx.x * 256L + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
-        const long n = e / kpad;
-        const int k = (int)(e % kpad);
+// conv1 (one input channel, the mel read in place): thread = (row, k), 256 / kpad
+// rows per block, 32-bit index math
+__global__ __launch_bounds__(256) void enc_im2col_mel(const float *mel, float *cols, int rows, int h_in, int w_in,
+                                                      int h_out, int w_out, int kpad, int mel_frames) {
+    const int rpb = 256 / kpad, r = threadIdx.x / kpad, k = threadIdx.x % kpad;
+    for (int n0 = blockIdx.x * rpb; n0 < rows; n0 += gridDim.x * rpb) {
+        const int n = n0 + r;
+        if (r >= rpb || n >= rows) continue;
+        const int ow = n % w_out, t = n / w_out, oh = t % h_out, c = t / h_out;
         float v = 0.0f;
-        if (k < c_in * 9) {
-            const int ic = k / 9, ki = (k % 9) / 3, kj = k % 3;
-            const int ow = (int)(n % w_out), oh = (int)((n / w_out) % h_out), c = (int)(n / ((long)w_out * h_out));
-            const int ih = 2 * oh - 1 + ki, iw = 2 * ow - 1 + kj;
-            if (ih >= 0 && ih < h_in && iw >= 0 && iw < w_in) {
-                if (mel_frames > 0) {               // conv1 reads the mel directly
-                    const int f = c * w_in + iw;
-                    if (f < mel_frames) v = in[(long)ih * mel_frames + f];
-                } else {
-                    v = in[(((long)ic * chunks + c) * h_in + ih) * w_in + iw];
-                }
-            }
+        if (k < 9) {
+            const int ih = 2 * oh - 1 + k / 3, iw = 2 * ow - 1 + k % 3;
+            const int f = c * w_in + iw;
+            if (ih >= 0 && ih < h_in && iw >= 0 && iw < w_in && f < mel_frames) v = mel[(long)ih * mel_frames + f];
         }
-        cols[e] = v;
+        cols[(long)n * kpad + k] = v;
+    }
+}
+
+// conv2 / conv3: one block per column row n = (chunk, oh, ow), decoded once;
+// threads along k (consecutive taps of one input row are adjacent in memory),
+// 32-bit index math (k / 9 and k % 9 by a constant)
+__global__ __launch_bounds__(256) void enc_im2col(const float *in, float *cols, int c_in, int chunks, int rows,
+                                                  int h_in, int w_in, int h_out, int w_out, int kpad) {
+    for (int n = blockIdx.x; n < rows; n += gridDim.x) {
+        const int ow = n % w_out, t = n / w_out, oh = t % h_out, c = t / h_out;
+        const int ih0 = 2 * oh - 1, iw0 = 2 * ow - 1;
+        const long plane = (long)chunks * h_in * w_in;
+        const float *src = in + (long)c * h_in * w_in;
+        float *dst = cols + (long)n * kpad;
+        for (int k = threadIdx.x; k < kpad; k += 256) {
+            float v = 0.0f;
+            if (k < c_in * 9) {
+                const int ic = k / 9, tap = k - 9 * ic;
+                const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
+                if (ih >= 0 && ih < h_in && iw >= 0 && iw < w_in) v = src[ic * plane + ih * w_in + iw];
+            }
+            dst[k] = v;
+        }
     }
 }
 
 extern "C" int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int chunks, int h_in, int w_in,
                                     int h_out, int w_out, int kpad, int mel_frames, hipStream_t s) {
     if (!in || !cols || c_in <= 0 || chunks <= 0 || kpad < c_in * 9 || (kpad & 15)) return QWEN_HIP_EINVAL;
-    const long total = (long)chunks * h_out * w_out * kpad;
-    long blocks = (total + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    enc_im2col<<<(int)blocks, 256, 0, s>>>(in, cols, c_in, chunks, h_in, w_in, h_out, w_out, kpad, mel_frames);
+    const long rows = (long)chunks * h_out * w_out;
+    if (rows > 0x7fffffffL) return QWEN_HIP_EINVAL;
+    if (mel_frames > 0) {
+        if (c_in != 1 || kpad > 256 || 256 % kpad) return QWEN_HIP_EINVAL;
+        const long rpb = 256 / kpad, blocks = (rows + rpb - 1) / rpb;
+        enc_im2col_mel<<<(int)(blocks < 65536 ? blocks : 65536), 256, 0, s>>>(in, cols, (int)rows, h_in, w_in, h_out,
+                                                                              w_out, kpad, mel_frames);
+    } else {
+        enc_im2col<<<(int)(rows < 65536 ? rows : 65536), 256, 0, s>>>(in, cols, c_in, chunks, (int)rows, h_in, w_in,
+                                                                     h_out, w_out, kpad);
+    }
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 
@@ -187,7 +211,7 @@ extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
     qk_enc_gemm_args g = *a;
     const long tiles = (long)((a->N + EG_T - 1) / EG_T) * ((a->M + EG_T - 1) / EG_T);
     // slices so that the grid holds ~2 blocks per CU, each slice >= 128 deep
-    int split = a->ws ? (int)(480 / tiles) : 1;
+    int split = a->ws ? (int)((512 + tiles - 1) / tiles) : 1;
     if (split > 8) split = 8;
     if (split > a->K / 128) split = a->K / 128;
     if (split < 1) split = 1;
