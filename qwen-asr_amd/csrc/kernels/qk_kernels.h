@@ -258,7 +258,7 @@ typedef struct {
     long ws_elems;
     int kc, split;
 } qk_enc_gemm_args;
-#define QK_ENC_GEMM_WS_ELEMS (512L * 64 * 64)   /* enough for every split the launcher picks */
+#define QK_ENC_GEMM_WS_ELEMS (1024L * 64 * 64)  /* split * M * N <= (512 + tiles) * 4096 for every split the launcher picks */
 int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s);
 int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int chunks, int h_in, int w_in, int h_out,
                          int w_out, int kpad, int mel_frames, hipStream_t s);
