@@ -279,7 +279,7 @@ class Encoder:
     def forward(self, mel):
         mel = np.ascontiguousarray(mel, np.float32)
         frames = mel.shape[1]
-        out = np.empty((self.tokens(frames), self.cfg.output_dim), np.float32)
+        out = np.empty((max(self.tokens(frames), 0), self.cfg.output_dim), np.float32)
         T = lib().qwen_hip_encoder_forward(self.h, _ptr(mel), frames, _ptr(out))
         check(T if T < 0 else 0, "encoder_forward")
         return out[:T]

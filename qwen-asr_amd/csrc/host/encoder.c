@@ -167,7 +167,10 @@ static int up(float **dst, const float *src, size_t n) {
 }
 
 int qwen_hip_encoder_load_layer(qwen_hip_encoder *e, int l, const qwen_hip_enc_layer_weights *w) {
-    if (!e || !w || l < 0 || l >= e->cfg.layers) return QWEN_HIP_EINVAL;
+    if (!e || !w || l < 0 || l >= e->cfg.layers) {
+        qk_set_err("encoder: NULL argument or layer %d outside [0, %d)", l, e ? e->cfg.layers : 0);
+        return QWEN_HIP_EINVAL;
+    }
     QK_HIP(hipSetDevice(e->device));
     const size_t d = e->cfg.d_model, f = e->cfg.ffn_dim;
     enc_layer *y = &e->L[l];

@@ -137,3 +137,31 @@ def test_encoder_from_checkpoint(P, qa, gpu, tmp_path):
     np.testing.assert_array_equal(out, ref_h.forward(mel))
     e.close()
     ref_h.close()
+
+
+def test_encoder_error_conventions(P, qa, gpu):
+    """Invalid shapes, calls before the weights are in, empty input and a
+    layer index out of range fail with a code and a message; the encoder
+    stays usable afterwards."""
+    bad = qa.EncConfig(128, 2, 3, 64, 256, 96, 100, 200)          # heads * 64 != d_model
+    assert not qa.lib().qwen_hip_encoder_create(C.byref(bad), 0)
+    assert "encoder configuration" in qa.last_error()
+    cfg = qa.EncConfig(128, 2, 2, 64, 256, 96, 100, 200)
+    e = qa.Encoder(cfg, 0)
+    mel = P.synth_mel(120, 1, 0)
+    with pytest.raises(RuntimeError, match="not loaded"):
+        e.forward(mel)
+    m = P.SynthEncoder(cfg, seed=1)
+    e.load_stem(m.stem)
+    with pytest.raises(RuntimeError, match="layer 0 not loaded"):
+        e.forward(mel)
+    with pytest.raises(RuntimeError):
+        e.load_layer(cfg.layers, m.layers[0])
+    assert "outside" in qa.last_error()
+    for l, arrs in enumerate(m.layers):
+        e.load_layer(l, arrs)
+    with pytest.raises(RuntimeError, match="bad argument"):
+        e.forward(np.zeros((128, 0), np.float32))
+    ref = load(qa, cfg, m).forward(mel)
+    np.testing.assert_array_equal(e.forward(mel), ref)
+    e.close()
