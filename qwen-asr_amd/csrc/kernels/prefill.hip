@@ -229,7 +229,7 @@ static void gemm_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint
 }
 
 extern "C" void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p) {
-    p->bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+    p->bm = M <= 32 ? 32 : 64;
     const long tiles = (long)((M + p->bm - 1) / p->bm) * ((N + QK_GEMM_BN - 1) / QK_GEMM_BN);
     const int kt = (K + QK_BK - 1) / QK_BK;
     long ns = tiles >= QK_GEMM_TARGET ? 1 : (QK_GEMM_TARGET + tiles - 1) / tiles;
