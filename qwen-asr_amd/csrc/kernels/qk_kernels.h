@@ -98,7 +98,7 @@ int qk_attn_decode_launch(const qk_attn_args *a, hipStream_t s);
  * QK_PF_TARGET blocks and returns the partial buffer size in floats (0 when
  * nsplit == 1). */
 #define QK_PF_PART 130              /* o[128], m, l */
-#define QK_PF_TARGET 384
+#define QK_PF_TARGET 768
 size_t qk_attn_prefill_plan(int seq_q, int seq_k, int q_offset, int heads, int kv_heads, int *chunk, int *nsplit);
 int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s);
 

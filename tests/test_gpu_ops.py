@@ -137,16 +137,17 @@ def test_causal_attention(P, qa, gpu, sq, sk, q_off):
     np.testing.assert_allclose(host(dout), exp, atol=3e-5, rtol=1e-4)
 
 
-def test_causal_attention_long_unsplit(P, qa, gpu):
-    """6400 query rows: the launch plan keeps one split per query tile (each
-    block walks up to 6400 keys), the path the 8k-row prefill takes.  Checked
-    against a float64 causal softmax attention computed with torch on the
-    same device (the CPU oracle is too slow at this size)."""
+def test_causal_attention_long_walk(P, qa, gpu):
+    """6400 query rows: the launch plan cuts only the longest query tiles in
+    two, so a block walks up to ~3400 keys (the path the 8k-row prefill
+    takes) and the merge combines two splits.  Checked against a float64
+    causal softmax attention computed with torch on the same device (the CPU
+    oracle is too slow at this size)."""
     sq = sk = 6400
     nh, nkv, hd = 16, 8, 128
     chunk, nsplit = C.c_int(), C.c_int()
     qa.lib().qk_attn_prefill_plan(sq, sk, 0, nh, nkv, C.byref(chunk), C.byref(nsplit))
-    assert nsplit.value == 1, (chunk.value, nsplit.value)
+    assert chunk.value >= 3000 and nsplit.value <= 3, (chunk.value, nsplit.value)
     g = gpu.Generator(device="cuda").manual_seed(11)
     Q = gpu.randn((sq, nh * hd), generator=g, device="cuda", dtype=gpu.float32)
     K = gpu.randn((sk, nkv * hd), generator=g, device="cuda", dtype=gpu.float32)
