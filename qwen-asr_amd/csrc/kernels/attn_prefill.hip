@@ -324,6 +324,11 @@ extern "C" size_t qk_attn_prefill_plan(int seq_q, int seq_k, int q_offset, int h
     long per = (tiles * kv_heads + QK_PF_TARGET - 1) / QK_PF_TARGET;
     if (per < 1) per = 1;
     long c = per * PF_KT;
+    // no block walks more than a sixth of the longest query tile (at least 256
+    // keys): the causal triangle's longest tiles then end with the rest
+    long cap = ((kmax + 5) / 6 + PF_KT - 1) / PF_KT * PF_KT;
+    if (cap < 256) cap = 256;
+    if (c > cap) c = cap;
     if (c > kmax) c = (kmax + PF_KT - 1) / PF_KT * PF_KT;
     *chunk = (int)c;
     *nsplit = (int)((kmax + c - 1) / c);

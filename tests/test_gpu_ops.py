@@ -138,16 +138,16 @@ def test_causal_attention(P, qa, gpu, sq, sk, q_off):
 
 
 def test_causal_attention_long_walk(P, qa, gpu):
-    """6400 query rows: the launch plan cuts only the longest query tiles in
-    two, so a block walks up to ~3400 keys (the path the 8k-row prefill
-    takes) and the merge combines two splits.  Checked against a float64
-    causal softmax attention computed with torch on the same device (the CPU
-    oracle is too slow at this size)."""
+    """6400 query rows: the launch plan caps a block's walk at a sixth of the
+    longest query tile, so blocks walk up to ~1100 keys (the path the 8k-row
+    prefill takes) and the merge combines up to six splits.  Checked against a
+    float64 causal softmax attention computed with torch on the same device
+    (the CPU oracle is too slow at this size)."""
     sq = sk = 6400
     nh, nkv, hd = 16, 8, 128
     chunk, nsplit = C.c_int(), C.c_int()
     qa.lib().qk_attn_prefill_plan(sq, sk, 0, nh, nkv, C.byref(chunk), C.byref(nsplit))
-    assert chunk.value >= 3000 and nsplit.value <= 3, (chunk.value, nsplit.value)
+    assert chunk.value >= 1000 and 2 <= nsplit.value <= 8, (chunk.value, nsplit.value)
     g = gpu.Generator(device="cuda").manual_seed(11)
     Q = gpu.randn((sq, nh * hd), generator=g, device="cuda", dtype=gpu.float32)
     K = gpu.randn((sk, nkv * hd), generator=g, device="cuda", dtype=gpu.float32)
