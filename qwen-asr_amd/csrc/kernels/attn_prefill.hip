@@ -1,36 +1,40 @@
 // attn_prefill.hip - causal GQA attention over many query rows (the prefill
 // half of qwen_causal_attention, reference qwen_asr_kernels.c:1050-1141) on
-// the fp32 matrix cores of gfx950.
+// the bf16 matrix cores of gfx950, fp32-accurate.
 //
-// The products stay fp32 x fp32 with fp32 accumulation, as in the reference;
-// only the summation order differs.  v_mfma_f32_16x16x4_f32 operand layout
-// (one 16x16 block, k = 4): lane l supplies A[l & 15][l >> 4] and
-// B[l >> 4][l & 15]; the result D[4 (l >> 4) + r][l & 15], r = 0..3, lands in
-// lane l.
+// Every fp32 operand x is carried as hi = bf16(x) and lo = bf16(x - hi)
+// (together ~16 significant bits; |x - hi - lo| <= 2^-17 |x|), and each
+// product a.b is taken as hi_a.hi_b + hi_a.lo_b + lo_a.hi_b on
+// v_mfma_f32_16x16x32_bf16 with fp32 accumulation: the dropped lo.lo term and
+// the split error leave ~2^-16 relative per product, against 2^-24 for fp32
+// products, at a fifth of the matrix-core time of v_mfma_f32_16x16x4_f32.
+// Softmax statistics, exponentials and the output stay fp32.
+//
+// Operand layout of the 16x16x32 bf16 MFMA: lane l supplies A[l & 15][8 (l >> 4)
+// + i] and B[8 (l >> 4) + i][l & 15], i = 0..7; the result D[4 (l >> 4) + r][l & 15],
+// r = 0..3, lands in lane l.
 //
 // A block owns one kv head, 64 consecutive queries of both query heads that
 // share it (4 waves: head = wave & 1, queries 32 (wave >> 1) .. + 32) and one
-// split of the key range.  Per 32-key tile staged in LDS:
-//   S^T = K Q^T   A = K rows (keys), B = this wave's queries; each k-step
-//                 takes 4 dims, and over a 16-dim block lane l feeds dims
-//                 4 (l >> 4) .. + 3 in turn, so both operands are one float4
-//                 per 16 dims (the dot products are permuted sums, not
-//                 reordered terms of different queries).
+// split of the key range.  Per 32-key tile staged in LDS (K rows and V^T,
+// split into hi / lo once per block):
+//   S^T = K Q^T   A = K rows (keys), B = this wave's queries, 32 dims per
+//                 k-step; Q is split once, in registers.
 //   online softmax per query: a query's 32 scores live in the 4 lanes
-//                 l & 15 = query (keys 4 (l >> 4) + r of each 16-key half),
-//                 so the row max / sum are in-lane over 8 values plus two
-//                 cross-lane steps; the rescale factor is lane-local.
-//   O^T += V^T P^T  A = V^T (dims x keys) from a transposed LDS tile, B = the
-//                 probabilities exactly where S^T left them (k-step s uses
-//                 key 4 (l >> 4) + s of lane l).
+//                 l & 15 = query (keys 16 kt + 4 (l >> 4) + r), so the row
+//                 max / sum are in-lane over 8 values plus two cross-lane
+//                 steps; the rescale factor is lane-local.
+//   O^T += V^T P^T  B = the probabilities exactly where S^T left them: k-slot
+//                 8 (l >> 4) + i of the MFMA is key 4 (l >> 4) + i (i < 4) and
+//                 16 + 4 (l >> 4) + i - 4 (i >= 4), and A = V^T reads the same
+//                 keys, so no value crosses lanes.
 // O^T lands as lane l: dims 16 dt + 4 (l >> 4) + r of query l & 15, written
 // back as float4 per dt.
 //
-// Splits: with few query tiles the key range is cut into chunks (a multiple
-// of 32 keys) so the launch fills the chip; each split writes unnormalised
-// partials (o[128], m, l) and attn_prefill_merge combines them in split order.
-// Query tiles are dispatched longest first (causal tiles grow with the query
-// index), so long prefills end without a long single-block tail.
+// Splits: the key range is cut into chunks (a multiple of 32 keys) so the
+// launch fills the chip; each split writes unnormalised partials (o[128], m,
+// l) and attn_prefill_merge combines them in split order.  Query tiles are
+// dispatched longest first (causal tiles grow with the query index).
 #include "common.h"
 #include "qk_kernels.h"
 #include "qwen_asr_hip.h"
@@ -39,12 +43,31 @@
 
 #define PF_Q 64                   // queries per block (per query head)
 #define PF_KT 32                  // keys per LDS tile
-#define PF_KLD (QWEN_HIP_HEAD_DIM + 4)   // sK row stride: rows 4 banks apart
-#define PF_VLD (PF_KT + 4)        // sVt row stride
+#define PF_KLDB (QWEN_HIP_HEAD_DIM + 8)  // bf16 row stride of the K tiles: 272 B, fragment reads conflict free
+#define PF_VLDB (PF_KT + 4)               // bf16 row stride of the V^T tiles: 72 B
 #define PF_MINIT (-1.0e30f)       // running-max start, as the reference's -1e30 (:1069)
 
-__device__ __forceinline__ f32x4 mfma_f32_4(float a, float b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
+typedef float pf_f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 pf_bf16x4 __attribute__((ext_vector_type(4)));
+
+// x = hi + lo + O(2^-17 |x|), hi and lo bf16 (round to nearest even)
+__device__ __forceinline__ void pf_split8(pf_f32x8 x, bf16x8 &hi, bf16x8 &lo) {
+    hi = __builtin_convertvector(x, bf16x8);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, pf_f32x8), bf16x8);
+}
+
+__device__ __forceinline__ void pf_split4(float4 v, pf_bf16x4 &hi, pf_bf16x4 &lo) {
+    const pf_f32x4 x = {v.x, v.y, v.z, v.w};
+    hi = __builtin_convertvector(x, pf_bf16x4);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, pf_f32x4), pf_bf16x4);
+}
+
+// hi.hi + hi.lo + lo.hi of one 16x16x32 block
+__device__ __forceinline__ f32x4 pf_mfma3(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
 }
 
 // The next K/V tile, held in registers while the current one is consumed.
@@ -72,17 +95,31 @@ __device__ __forceinline__ void pf_load(PfStage &st, const float *kb, const floa
     }
 }
 
-__device__ __forceinline__ void pf_store(const PfStage &st, float (*sK)[PF_KLD], float (*sVt)[PF_VLD], int tid) {
+__device__ __forceinline__ void pf_store(const PfStage &st, __bf16 (*sKh)[PF_KLDB], __bf16 (*sKl)[PF_KLDB],
+                                         __bf16 (*sVh)[PF_VLDB], __bf16 (*sVl)[PF_VLDB], int tid) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int idx = tid + 256 * i;
-        *reinterpret_cast<float4 *>(&sK[idx >> 5][(idx & 31) * 4]) = st.k[i];
+        pf_bf16x4 h, l;
+        pf_split4(st.k[i], h, l);
+        *reinterpret_cast<pf_bf16x4 *>(&sKh[idx >> 5][(idx & 31) * 4]) = h;
+        *reinterpret_cast<pf_bf16x4 *>(&sKl[idx >> 5][(idx & 31) * 4]) = l;
     }
     const int d = tid & 127;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-        *reinterpret_cast<float4 *>(&sVt[d][4 * ((tid >> 7) + 2 * j)]) =
-            make_float4(st.v[4 * j], st.v[4 * j + 1], st.v[4 * j + 2], st.v[4 * j + 3]);
+    for (int j = 0; j < 4; j++) {
+        pf_bf16x4 h, l;
+        pf_split4(make_float4(st.v[4 * j], st.v[4 * j + 1], st.v[4 * j + 2], st.v[4 * j + 3]), h, l);
+        *reinterpret_cast<pf_bf16x4 *>(&sVh[d][4 * ((tid >> 7) + 2 * j)]) = h;
+        *reinterpret_cast<pf_bf16x4 *>(&sVl[d][4 * ((tid >> 7) + 2 * j)]) = l;
+    }
+}
+
+// 8 bf16 of a V^T row: keys 4 kq .. + 3 and 16 + 4 kq .. + 3 (the keys of this lane's scores)
+__device__ __forceinline__ bf16x8 pf_vrow(const __bf16 *row, int kq) {
+    const pf_bf16x4 a = *reinterpret_cast<const pf_bf16x4 *>(row + 4 * kq);
+    const pf_bf16x4 b = *reinterpret_cast<const pf_bf16x4 *>(row + 16 + 4 * kq);
+    return (bf16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
 __device__ __forceinline__ void pf_write_out(const qk_attn_args &a, size_t base, float4 v) {
@@ -101,8 +138,10 @@ __device__ __forceinline__ void pf_write_out(const qk_attn_args &a, size_t base,
 
 __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
     constexpr int hd = QWEN_HIP_HEAD_DIM;
-    __shared__ __attribute__((aligned(16))) float sK[PF_KT][PF_KLD];
-    __shared__ __attribute__((aligned(16))) float sVt[hd][PF_VLD];
+    __shared__ __attribute__((aligned(16))) __bf16 sKh[PF_KT][PF_KLDB];
+    __shared__ __attribute__((aligned(16))) __bf16 sKl[PF_KT][PF_KLDB];
+    __shared__ __attribute__((aligned(16))) __bf16 sVh[hd][PF_VLDB];
+    __shared__ __attribute__((aligned(16))) __bf16 sVl[hd][PF_VLDB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, kq = lane >> 4;
     const int nq = (a.seq_q + PF_Q - 1) / PF_Q;
@@ -121,16 +160,21 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
     const float *kb = a.k + (size_t)g * a.head_stride;
     const float *vb = a.v + (size_t)g * a.head_stride;
 
-    // this lane's query rows (16 per tile qt), dims 16 b + 4 kq .. + 3
-    float4 q[2][8];
+    // this lane's query rows (16 per tile qt), dims 32 s + 8 kq .. + 7, split once
+    bf16x8 qh[2][4], qo[2][4];
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
         const int qi = qs + 16 * qt + ql;
 #pragma unroll
-        for (int b = 0; b < 8; b++)
-            q[qt][b] = qi < a.seq_q
-                           ? *reinterpret_cast<const float4 *>(a.q + (size_t)qi * qstride + h * hd + 16 * b + 4 * kq)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s4 = 0; s4 < 4; s4++) {
+            float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+            if (qi < a.seq_q) {
+                const float *qp = a.q + (size_t)qi * qstride + h * hd + 32 * s4 + 8 * kq;
+                x0 = *reinterpret_cast<const float4 *>(qp);
+                x1 = *reinterpret_cast<const float4 *>(qp + 4);
+            }
+            pf_split8((pf_f32x8){x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w}, qh[qt][s4], qo[qt][s4]);
+        }
     }
     f32x4 o[2][8];
 #pragma unroll
@@ -143,7 +187,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
     pf_load(st, kb, vb, a.pos_stride, ks0, ks1, tid);
     for (int k0 = ks0; k0 < ks1; k0 += PF_KT) {
         __syncthreads();                                  // previous tile fully consumed
-        pf_store(st, sK, sVt, tid);
+        pf_store(st, sKh, sKl, sVh, sVl, tid);
         __syncthreads();
         if (k0 + PF_KT < ks1) pf_load(st, kb, vb, a.pos_stride, k0 + PF_KT, ks1, tid);
         if (!wave_on) continue;
@@ -154,19 +198,15 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
         for (int qt = 0; qt < 2; qt++)
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) s[qt][kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        // consecutive MFMAs go to the 4 independent (qt, kt) accumulators
 #pragma unroll
-        for (int b = 0; b < 8; b++) {
-            float4 kf[2];
+        for (int s4 = 0; s4 < 4; s4++) {
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++) kf[kt] = *reinterpret_cast<const float4 *>(&sK[16 * kt + ql][16 * b + 4 * kq]);
+            for (int kt = 0; kt < 2; kt++) {
+                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&sKh[16 * kt + ql][32 * s4 + 8 * kq]);
+                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&sKl[16 * kt + ql][32 * s4 + 8 * kq]);
 #pragma unroll
-            for (int c = 0; c < 4; c++)
-#pragma unroll
-                for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                    for (int qt = 0; qt < 2; qt++)
-                        s[qt][kt] = mfma_f32_4((&kf[kt].x)[c], (&q[qt][b].x)[c], s[qt][kt]);
+                for (int qt = 0; qt < 2; qt++) s[qt][kt] = pf_mfma3(kh, kl, qh[qt][s4], qo[qt][s4], s[qt][kt]);
+            }
         }
 
         // online softmax (causal mask: key <= q_offset + query; keys past ks1 belong elsewhere)
@@ -203,24 +243,20 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
             }
         }
 
-        // O^T[d][query] += V^T[d][key] P^T[key][query]
-        // consecutive MFMAs go to 8 independent (qt, dt) accumulators
+        // O^T[d][query] += V^T[d][key] P^T[key][query]; B = this lane's 8 probabilities
+        bf16x8 ph[2], po[2];
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
+        for (int qt = 0; qt < 2; qt++)
+            pf_split8((pf_f32x8){p[qt][0][0], p[qt][0][1], p[qt][0][2], p[qt][0][3], p[qt][1][0], p[qt][1][1],
+                                 p[qt][1][2], p[qt][1][3]},
+                      ph[qt], po[qt]);
 #pragma unroll
-            for (int dh = 0; dh < 8; dh += 4) {
-                float4 vf[4];
+        for (int dt = 0; dt < 8; dt++) {
+            const bf16x8 vh = pf_vrow(&sVh[16 * dt + ql][0], kq);
+            const bf16x8 vl = pf_vrow(&sVl[16 * dt + ql][0], kq);
 #pragma unroll
-                for (int d = 0; d < 4; d++)
-                    vf[d] = *reinterpret_cast<const float4 *>(&sVt[16 * (dh + d) + ql][16 * kt + 4 * kq]);
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-#pragma unroll
-                    for (int d = 0; d < 4; d++)
-#pragma unroll
-                        for (int qt = 0; qt < 2; qt++)
-                            o[qt][dh + d] = mfma_f32_4((&vf[d].x)[c], p[qt][kt][c], o[qt][dh + d]);
-            }
+            for (int qt = 0; qt < 2; qt++) o[qt][dt] = pf_mfma3(vh, vl, ph[qt], po[qt], o[qt][dt]);
+        }
     }
     if (!wave_on) return;
 
