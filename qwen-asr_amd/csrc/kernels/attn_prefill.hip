@@ -287,11 +287,13 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
     }
 }
 
-// One wave per (query, head): combine the splits of the query's tile in split
-// order (max, then rescaled sums), normalise, store.
-__global__ __launch_bounds__(64) void attn_prefill_merge(qk_attn_args a) {
+// One wave per (query, head), four per block: combine the splits of the
+// query's tile in split order (max, then rescaled sums), normalise, store.
+__global__ __launch_bounds__(256) void attn_prefill_merge(qk_attn_args a) {
     constexpr int hd = QWEN_HIP_HEAD_DIM;
-    const int qi = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const long u = 4L * blockIdx.x + (threadIdx.x >> 6);
+    if (u >= (long)a.seq_q * a.heads) return;        // whole wave
+    const int qi = (int)(u / a.heads), h = (int)(u % a.heads), lane = threadIdx.x & 63;
     const int t = qi / PF_Q;
     const int kend_tile = min(a.seq_k, a.q_offset + min(a.seq_q, (t + 1) * PF_Q));
     const int n = (kend_tile + a.chunk - 1) / a.chunk;
@@ -381,6 +383,7 @@ extern "C" int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s) {
     const int kmax = a->seq_k < a->q_offset + a->seq_q ? a->seq_k : a->q_offset + a->seq_q;
     if ((long)a->chunk * a->nsplit < kmax) return QWEN_HIP_EINVAL;
     attn_prefill<<<dim3(nq, a->kv_heads, a->nsplit), 256, 0, s>>>(*a);
-    if (a->nsplit > 1) attn_prefill_merge<<<dim3(a->seq_q, a->heads), 64, 0, s>>>(*a);
+    if (a->nsplit > 1)
+        attn_prefill_merge<<<(unsigned)(((long)a->seq_q * a->heads + 3) / 4), 256, 0, s>>>(*a);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }

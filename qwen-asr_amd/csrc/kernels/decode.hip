@@ -360,11 +360,16 @@ __device__ __forceinline__ float qkv_at(const float *p, int nsum, long pstride) 
     return sum_splits<QK_GEMM_MAX_SPLIT>(p, nsum, pstride);
 }
 
-__global__ __launch_bounds__(64) void rope_append(qk_rope_append_args a) {
+// One wave per (row, head) unit, four units per block: unit u = 4 block + wave,
+// head = u % (heads + kv_heads) ([0, heads) q, then k/v), row = u / (heads + kv_heads).
+__global__ __launch_bounds__(256) void rope_append(qk_rope_append_args a) {
     const int hd = QWEN_HIP_HEAD_DIM, half = hd / 2;
-    const int lane = threadIdx.x;
-    const int head = blockIdx.x;                // [0, heads) q, [heads, heads+kv_heads) k/v
-    const int srow = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int nh = a.heads + a.kv_heads;
+    const long u = 4L * blockIdx.x + (threadIdx.x >> 6);
+    if (u >= (long)nh * a.S) return;            // whole wave
+    const int head = (int)(u % nh);
+    const int srow = (int)(u / nh);
     const int start = a.pos_dev ? *a.pos_dev : a.start;
     const int p = start + srow;
     const int qd = a.heads * hd, kvd = a.kv_heads * hd;
@@ -402,8 +407,9 @@ extern "C" int qk_rope_append_launch(const qk_rope_append_args *a, hipStream_t s
     if (!a || a->S <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads ||
         a->nsum > QK_GEMM_MAX_SPLIT)
         return QWEN_HIP_EINVAL;
-    dim3 grid(a->heads + a->kv_heads, a->S);
-    rope_append<<<grid, 64, 0, s>>>(*a);
+    const long units = (long)(a->heads + a->kv_heads) * a->S;
+    if ((units + 3) / 4 > 0x7fffffffL) return QWEN_HIP_EINVAL;
+    rope_append<<<(unsigned)((units + 3) / 4), 256, 0, s>>>(*a);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 

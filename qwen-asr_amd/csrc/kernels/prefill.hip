@@ -79,12 +79,63 @@ __global__ __launch_bounds__(RN_THREADS) void rmsnorm_split(float *x, const floa
     }
 }
 
+// Tall inputs: one wave per row, four rows per block, D / 64 elements per
+// lane; partials are summed in split order and then added, as above.
+template <int DPL>
+__global__ __launch_bounds__(256) void rmsnorm_split_rows(float *x, const float *part, int nsum, long pstride,
+                                                          const float *w, int S, float eps, uint16_t *hi,
+                                                          uint16_t *lo) {
+    constexpr int D = 64 * DPL;
+    const int row = 4 * blockIdx.x + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= S) return;                                   // whole wave
+    float *xr = x + (size_t)row * D;
+    float v[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; j++) v[j] = xr[j * 64 + lane];
+    if (nsum) {
+        float ps[DPL];
+        const float *pr = part + (size_t)row * D + lane;
+#pragma unroll
+        for (int j = 0; j < DPL; j++) ps[j] = pr[j * 64];
+        for (int sp = 1; sp < nsum; sp++)
+#pragma unroll
+            for (int j = 0; j < DPL; j++) ps[j] += pr[sp * pstride + j * 64];
+#pragma unroll
+        for (int j = 0; j < DPL; j++) {
+            v[j] += ps[j];
+            xr[j * 64 + lane] = v[j];
+        }
+    }
+    float rinv = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < DPL; j++) ss = fmaf(v[j], v[j], ss);
+        ss = wave_sum(ss);
+        rinv = 1.0f / sqrtf(ss / (float)D + eps);
+    }
+    if (!hi) return;
+    uint16_t *h = hi + (size_t)row * D, *l = lo + (size_t)row * D;
+#pragma unroll
+    for (int j = 0; j < DPL; j++) {
+        const int i = j * 64 + lane;
+        split2(w ? (v[j] * w[i]) * rinv : v[j], h[i], l[i]);
+    }
+}
+
 extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride, const float *w, int S,
                                        int D, float eps, uint16_t *hi, uint16_t *lo, hipStream_t s) {
     if (S <= 0 || D <= 0 || !x || nsum < 0 || nsum > QK_GEMM_MAX_SPLIT || (nsum && !part) || (!hi) != (!lo) ||
         (!hi && !nsum))
         return QWEN_HIP_EINVAL;
-    rmsnorm_split<<<S, RN_THREADS, 0, s>>>(x, part, nsum, pstride, w, D, eps, hi, lo);
+    if (S >= 1024 && (D == 1024 || D == 2048)) {
+        // tall inputs: a wave per row keeps the grid at S / 4 blocks
+        const unsigned blocks = (unsigned)((S + 3) / 4);
+        if (D == 1024) rmsnorm_split_rows<16><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
+        else rmsnorm_split_rows<32><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
+    } else {
+        rmsnorm_split<<<S, RN_THREADS, 0, s>>>(x, part, nsum, pstride, w, D, eps, hi, lo);
+    }
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 
