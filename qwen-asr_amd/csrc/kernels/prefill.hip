@@ -142,9 +142,11 @@ extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, lo
 // ---------------------------------------------------------------------------
 // GEMM on v_mfma_f32_16x16x32_bf16.  Block tile BM x BN = (WGM TM 16) x
 // (WGN TN 16): 4 waves in a WGM x WGN grid, each TM x TN MFMA tiles of 16x16.
-// K is walked QK_BK (64) at a time through two LDS buffers: the next tile's global
-// loads are in flight (in registers) while the current one feeds the MFMAs,
-// then land in the other buffer; one barrier per k tile.  Operand fragments:
+// K is walked QK_BK (64) at a time through LDS: the next tile's global loads
+// are in flight (in registers) while the current one feeds the MFMAs, then
+// land in the other of two buffers (one barrier per k tile) or, for 128-row
+// tiles, in the single buffer after a second barrier (half the LDS, so two
+// blocks share a CU).  Operand fragments:
 // lane l supplies row (l & 15) and the 8 consecutive k values [8 (l >> 4), +8)
 // of its 32-wide k step, for both the activation tile (A) and the weight tile
 // (W rows play the B columns), so the k pairing is the same on both sides.
@@ -167,8 +169,11 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
     constexpr int CPR = QK_BK / 8;                                   // 16-byte chunks per row
     constexpr int ACH = BM * CPR, BCH = BN * CPR;                    // 16-byte chunks per tile
     constexpr int APT = (ACH + 255) / 256, BPT = (BCH + 255) / 256;
-    __shared__ __attribute__((aligned(16))) uint16_t sA[2][2][BM][QK_LDK];   // [buffer][hi, lo]
-    __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN][QK_LDK];
+    // 128-row tiles keep one LDS buffer (two barriers per k tile, ~55 KB: two
+    // blocks per CU); smaller tiles double-buffer (one barrier per k tile)
+    constexpr int NBUF = BM >= 128 ? 1 : 2;
+    __shared__ __attribute__((aligned(16))) uint16_t sA[NBUF][2][BM][QK_LDK];   // [buffer][hi, lo]
+    __shared__ __attribute__((aligned(16))) uint16_t sB[NBUF][BN][QK_LDK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
     lstore(0);
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
-        const int buf = kt & 1;
+        const int buf = NBUF == 2 ? (kt & 1) : 0;
         if (kt + 1 < nk) gload(kb + (kt + 1) * QK_BK);
 #pragma unroll
         for (int kk = 0; kk < QK_BK; kk += 32) {
@@ -238,7 +243,8 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
                 }
             }
         }
-        if (kt + 1 < nk) lstore(buf ^ 1);
+        if (NBUF == 1) __syncthreads();                   // every wave is done with the only buffer
+        if (kt + 1 < nk) lstore(NBUF == 2 ? buf ^ 1 : 0);
         __syncthreads();
     }
 
@@ -280,7 +286,7 @@ static void gemm_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint
 }
 
 extern "C" void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p) {
-    p->bm = M <= 32 ? 32 : 64;
+    p->bm = M <= 32 ? 32 : M <= 512 ? 64 : 128;
     const long tiles = (long)((M + p->bm - 1) / p->bm) * ((N + QK_GEMM_BN - 1) / QK_GEMM_BN);
     const int kt = (K + QK_BK - 1) / QK_BK;
     long ns = tiles >= QK_GEMM_TARGET ? 1 : (QK_GEMM_TARGET + tiles - 1) / tiles;
