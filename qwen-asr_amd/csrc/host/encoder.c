@@ -27,8 +27,17 @@
 #define ENC_K1 16             /* conv1 patch 1*3*3 padded to a multiple of 16 */
 #define ENC_K2 (ENC_CH * 9)   /* 4320 */
 
+/* A weight matrix on the device: a bf16 copy when every value is a bf16 value
+ * (checkpoint weights are), used by the bf16 matrix-core GEMM; otherwise the
+ * fp32 values, used by the fp32 one. */
 typedef struct {
-    float *wqkv, *bqkv, *wo, *bo, *ln1w, *ln1b, *fc1w, *fc1b, *fc2w, *fc2b, *ln2w, *ln2b;
+    float *f32;
+    uint16_t *b16;
+} enc_mat;
+
+typedef struct {
+    enc_mat wqkv, wo, fc1w, fc2w;
+    float *bqkv, *bo, *ln1w, *ln1b, *fc1b, *fc2b, *ln2w, *ln2b;
     int loaded;
 } enc_layer;
 
@@ -36,7 +45,8 @@ struct qwen_hip_encoder {
     qwen_hip_enc_config cfg;
     int device;
     hipStream_t stream;
-    float *c1w, *c1b, *c2w, *c2b, *c3w, *c3b, *cow, *lnpw, *lnpb, *p1w, *p1b, *p2w, *p2b, *pe;
+    float *c1w, *c1b, *c2b, *c3b, *lnpw, *lnpb, *p1b, *p2b, *pe;
+    enc_mat c2w, c3w, cow, p1w, p2w;
     int stem_loaded;
     enc_layer L[QWEN_HIP_ENC_MAX_LAYERS];
     /* activations, sized for cap_chunks chunks */
@@ -97,15 +107,18 @@ void qwen_hip_encoder_destroy(qwen_hip_encoder *e) {
     (void)hipSetDevice(e->device);
     (void)hipStreamSynchronize(e->stream);
     act_free(e);
-    void **w[] = {(void **)&e->c1w, (void **)&e->c1b, (void **)&e->c2w, (void **)&e->c2b, (void **)&e->c3w,
-                  (void **)&e->c3b, (void **)&e->cow, (void **)&e->lnpw, (void **)&e->lnpb, (void **)&e->p1w,
-                  (void **)&e->p1b, (void **)&e->p2w, (void **)&e->p2b, (void **)&e->pe};
+    void **w[] = {(void **)&e->c1w,     (void **)&e->c1b,     (void **)&e->c2w.f32, (void **)&e->c2w.b16,
+                  (void **)&e->c2b,     (void **)&e->c3w.f32, (void **)&e->c3w.b16, (void **)&e->c3b,
+                  (void **)&e->cow.f32, (void **)&e->cow.b16, (void **)&e->lnpw,    (void **)&e->lnpb,
+                  (void **)&e->p1w.f32, (void **)&e->p1w.b16, (void **)&e->p1b,     (void **)&e->p2w.f32,
+                  (void **)&e->p2w.b16, (void **)&e->p2b,     (void **)&e->pe};
     for (size_t i = 0; i < sizeof(w) / sizeof(w[0]); i++) dfree(w[i]);
     for (int l = 0; l < QWEN_HIP_ENC_MAX_LAYERS; l++) {
         enc_layer *y = &e->L[l];
-        void **v[] = {(void **)&y->wqkv, (void **)&y->bqkv, (void **)&y->wo, (void **)&y->bo, (void **)&y->ln1w,
-                      (void **)&y->ln1b, (void **)&y->fc1w, (void **)&y->fc1b, (void **)&y->fc2w, (void **)&y->fc2b,
-                      (void **)&y->ln2w, (void **)&y->ln2b};
+        void **v[] = {(void **)&y->wqkv.f32, (void **)&y->wqkv.b16, (void **)&y->bqkv,     (void **)&y->wo.f32,
+                      (void **)&y->wo.b16,   (void **)&y->bo,       (void **)&y->ln1w,     (void **)&y->ln1b,
+                      (void **)&y->fc1w.f32, (void **)&y->fc1w.b16, (void **)&y->fc1b,     (void **)&y->fc2w.f32,
+                      (void **)&y->fc2w.b16, (void **)&y->fc2b,     (void **)&y->ln2w,     (void **)&y->ln2b};
         for (size_t i = 0; i < sizeof(v) / sizeof(v[0]); i++) dfree(v[i]);
     }
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -159,6 +172,41 @@ qwen_hip_encoder *qwen_hip_encoder_create(const qwen_hip_enc_config *cfg, int de
     return e;
 }
 
+/* every value of src[0, n) is a bf16 value (its low 16 bits are zero) */
+static int bf16_exact(const float *src, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        uint32_t u;
+        memcpy(&u, src + i, 4);
+        if (u & 0xffffu) return 0;
+    }
+    return 1;
+}
+
+/* rows [row0, row0 + n / cols) of a weight matrix: the bf16 copy when the whole
+ * matrix (`exact`, decided by the caller) is bf16-valued, else fp32 */
+static int up_mat(enc_mat *m, size_t total, size_t off, const float *src, size_t n, int exact) {
+    if (!src) { qk_set_err("encoder weight pointer is NULL"); return QWEN_HIP_EINVAL; }
+    if (exact) {
+        if (m->f32) dfree((void **)&m->f32);
+        if (!m->b16) QK_TRY(dmalloc((void **)&m->b16, total * 2));
+        uint16_t *h = (uint16_t *)malloc(n * 2);
+        if (!h) { qk_set_err("out of host memory"); return QWEN_HIP_ENOMEM; }
+        for (size_t i = 0; i < n; i++) {
+            uint32_t u;
+            memcpy(&u, src + i, 4);
+            h[i] = (uint16_t)(u >> 16);
+        }
+        const hipError_t r = hipMemcpy(m->b16 + off, h, n * 2, hipMemcpyHostToDevice);
+        free(h);
+        if (r != hipSuccess) { qk_set_err("hipMemcpy: %s", hipGetErrorString(r)); return QWEN_HIP_EDEVICE; }
+    } else {
+        if (m->b16) dfree((void **)&m->b16);
+        if (!m->f32) QK_TRY(dmalloc((void **)&m->f32, total * 4));
+        QK_HIP(hipMemcpy(m->f32 + off, src, n * 4, hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
 static int up(float **dst, const float *src, size_t n) {
     if (!src) { qk_set_err("encoder weight pointer is NULL"); return QWEN_HIP_EINVAL; }
     if (!*dst) QK_TRY(dmalloc((void **)dst, n * sizeof(float)));
@@ -175,21 +223,22 @@ int qwen_hip_encoder_load_layer(qwen_hip_encoder *e, int l, const qwen_hip_enc_l
     const size_t d = e->cfg.d_model, f = e->cfg.ffn_dim;
     enc_layer *y = &e->L[l];
     /* Q|K|V stacked: rows [0,d) q, [d,2d) k, [2d,3d) v */
-    if (!y->wqkv) QK_TRY(dmalloc((void **)&y->wqkv, 3 * d * d * 4));
     if (!y->bqkv) QK_TRY(dmalloc((void **)&y->bqkv, 3 * d * 4));
     const float *ws[3] = {w->wq, w->wk, w->wv}, *bs[3] = {w->bq, w->bk, w->bv};
-    for (int i = 0; i < 3; i++) {
+    for (int i = 0; i < 3; i++)
         if (!ws[i] || !bs[i]) { qk_set_err("encoder layer %d: NULL q/k/v weight", l); return QWEN_HIP_EINVAL; }
-        QK_HIP(hipMemcpy(y->wqkv + i * d * d, ws[i], d * d * 4, hipMemcpyHostToDevice));
+    const int qkv_exact = bf16_exact(ws[0], d * d) && bf16_exact(ws[1], d * d) && bf16_exact(ws[2], d * d);
+    for (int i = 0; i < 3; i++) {
+        QK_TRY(up_mat(&y->wqkv, 3 * d * d, i * d * d, ws[i], d * d, qkv_exact));
         QK_HIP(hipMemcpy(y->bqkv + i * d, bs[i], d * 4, hipMemcpyHostToDevice));
     }
-    QK_TRY(up(&y->wo, w->wo, d * d));
+    QK_TRY(up_mat(&y->wo, d * d, 0, w->wo, d * d, w->wo && bf16_exact(w->wo, d * d)));
     QK_TRY(up(&y->bo, w->bo, d));
     QK_TRY(up(&y->ln1w, w->ln1_w, d));
     QK_TRY(up(&y->ln1b, w->ln1_b, d));
-    QK_TRY(up(&y->fc1w, w->fc1_w, f * d));
+    QK_TRY(up_mat(&y->fc1w, f * d, 0, w->fc1_w, f * d, w->fc1_w && bf16_exact(w->fc1_w, f * d)));
     QK_TRY(up(&y->fc1b, w->fc1_b, f));
-    QK_TRY(up(&y->fc2w, w->fc2_w, d * f));
+    QK_TRY(up_mat(&y->fc2w, d * f, 0, w->fc2_w, d * f, w->fc2_w && bf16_exact(w->fc2_w, d * f)));
     QK_TRY(up(&y->fc2b, w->fc2_b, d));
     QK_TRY(up(&y->ln2w, w->ln2_w, d));
     QK_TRY(up(&y->ln2b, w->ln2_b, d));
@@ -207,16 +256,17 @@ int qwen_hip_encoder_load_stem(qwen_hip_encoder *e, const qwen_hip_enc_stem_weig
     for (int oc = 0; oc < ENC_CH; oc++) memcpy(c1 + oc * ENC_K1, w->conv1_w + oc * 9, 9 * sizeof(float));
     QK_TRY(up(&e->c1w, c1, ENC_CH * ENC_K1));
     QK_TRY(up(&e->c1b, w->conv1_b, ENC_CH));
-    QK_TRY(up(&e->c2w, w->conv2_w, (size_t)ENC_CH * ENC_K2));
+    const size_t k2 = (size_t)ENC_CH * ENC_K2, ko = d * ENC_CH * 16;
+    QK_TRY(up_mat(&e->c2w, k2, 0, w->conv2_w, k2, w->conv2_w && bf16_exact(w->conv2_w, k2)));
     QK_TRY(up(&e->c2b, w->conv2_b, ENC_CH));
-    QK_TRY(up(&e->c3w, w->conv3_w, (size_t)ENC_CH * ENC_K2));
+    QK_TRY(up_mat(&e->c3w, k2, 0, w->conv3_w, k2, w->conv3_w && bf16_exact(w->conv3_w, k2)));
     QK_TRY(up(&e->c3b, w->conv3_b, ENC_CH));
-    QK_TRY(up(&e->cow, w->conv_out_w, d * ENC_CH * 16));
+    QK_TRY(up_mat(&e->cow, ko, 0, w->conv_out_w, ko, w->conv_out_w && bf16_exact(w->conv_out_w, ko)));
     QK_TRY(up(&e->lnpw, w->ln_post_w, d));
     QK_TRY(up(&e->lnpb, w->ln_post_b, d));
-    QK_TRY(up(&e->p1w, w->proj1_w, d * d));
+    QK_TRY(up_mat(&e->p1w, d * d, 0, w->proj1_w, d * d, w->proj1_w && bf16_exact(w->proj1_w, d * d)));
     QK_TRY(up(&e->p1b, w->proj1_b, d));
-    QK_TRY(up(&e->p2w, w->proj2_w, o * d));
+    QK_TRY(up_mat(&e->p2w, o * d, 0, w->proj2_w, o * d, w->proj2_w && bf16_exact(w->proj2_w, o * d)));
     QK_TRY(up(&e->p2b, w->proj2_b, o));
     e->stem_loaded = 1;
     return 0;
@@ -328,23 +378,25 @@ static int reserve(qwen_hip_encoder *e, int chunks, int tokens) {
     return 0;
 }
 
-static int gemm(qwen_hip_encoder *e, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
+/* C = A . W^T with the activations A [M][K] and a weight matrix W [N][K] */
+static int gemm(qwen_hip_encoder *e, const float *A, int lda, const enc_mat *W, int ldb, float *C, int ldc, int M,
                 int N, int K, const float *bias_m, const float *bias_n, int gelu, int add) {
-    qk_enc_gemm_args g = {.A = A, .B = B, .C = C, .M = M, .N = N, .K = K, .lda = lda, .ldb = ldb, .ldc = ldc,
+    qk_enc_gemm_args g = {.A = A, .B = W->f32, .C = C, .M = M, .N = N, .K = K, .lda = lda, .ldb = ldb, .ldc = ldc,
                           .bias_m = bias_m, .bias_n = bias_n, .gelu = gelu, .add = add,
-                          .ws = e->gws, .ws_elems = QK_ENC_GEMM_WS_ELEMS};
+                          .ws = e->gws, .ws_elems = QK_ENC_GEMM_WS_ELEMS, .B16 = W->b16};
     return qk_enc_gemm_launch(&g, e->stream);
 }
 
 /* one stem layer: im2col over every chunk, GEMM with bias + GELU, padding zeroed */
 static int stem_layer(qwen_hip_encoder *e, const float *in, int c_in, int chunks, int h_in, int w_in, int kpad,
-                      int mel_frames, const float *w, const float *b, float *out, int valid_last) {
+                      int mel_frames, const float *w, const uint16_t *w16, const float *b, float *out,
+                      int valid_last) {
     const int h_out = conv_out(h_in), w_out = conv_out(w_in);
     const int N = chunks * h_out * w_out;
     QK_TRY(qk_enc_im2col_launch(in, e->cols, c_in, chunks, h_in, w_in, h_out, w_out, kpad, mel_frames, e->stream));
     qk_enc_gemm_args g = {.A = w, .B = e->cols, .C = out, .M = ENC_CH, .N = N, .K = kpad, .lda = kpad,
                           .ldb = kpad, .ldc = N, .bias_m = b, .gelu = 1, .col_w = w_out, .col_h = h_out,
-                          .col_chunks = chunks, .col_valid = valid_last};
+                          .col_chunks = chunks, .col_valid = valid_last, .A16 = w16};
     return qk_enc_gemm_launch(&g, e->stream);
 }
 
@@ -356,16 +408,18 @@ static int run(qwen_hip_encoder *e, int mel_frames, int *tokens_out) {
     const int w1 = conv_out(cw), w2 = conv_out(w1), w3 = conv_out(w2);
     const int T = qwen_hip_encoder_tokens(c, mel_frames);
     /* conv stem (qwen_asr_encoder.c:237-279); the mel is [128][mel_frames] */
-    QK_TRY(stem_layer(e, e->mel, 1, chunks, ENC_MEL, cw, ENC_K1, mel_frames, e->c1w, e->c1b, e->c1, conv_out(last)));
-    QK_TRY(stem_layer(e, e->c1, ENC_CH, chunks, 64, w1, ENC_K2, 0, e->c2w, e->c2b, e->c2, conv_out(conv_out(last))));
-    QK_TRY(stem_layer(e, e->c2, ENC_CH, chunks, 32, w2, ENC_K2, 0, e->c3w, e->c3b, e->c3,
+    QK_TRY(stem_layer(e, e->mel, 1, chunks, ENC_MEL, cw, ENC_K1, mel_frames, e->c1w, NULL, e->c1b, e->c1,
+                      conv_out(last)));
+    QK_TRY(stem_layer(e, e->c1, ENC_CH, chunks, 64, w1, ENC_K2, 0, e->c2w.f32, e->c2w.b16, e->c2b, e->c2,
+                      conv_out(conv_out(last))));
+    QK_TRY(stem_layer(e, e->c2, ENC_CH, chunks, 32, w2, ENC_K2, 0, e->c3w.f32, e->c3w.b16, e->c3b, e->c3,
                       conv_out(conv_out(conv_out(last)))));
     /* [480][16][w3] per chunk -> token rows [T][7680], project, add the chunk's positions (:281-301) */
     QK_TRY(qk_enc_stem_rows_launch(e->c3, e->rows, chunks, w3, 16, ENC_CH, T, e->stream));
     {
-        qk_enc_gemm_args g = {.A = e->rows, .B = e->cow, .C = e->x, .M = T, .N = d, .K = ENC_CH * 16,
+        qk_enc_gemm_args g = {.A = e->rows, .B = e->cow.f32, .C = e->x, .M = T, .N = d, .K = ENC_CH * 16,
                               .lda = ENC_CH * 16, .ldb = ENC_CH * 16, .ldc = d, .pe = e->pe, .pe_rows = w3,
-                              .ws = e->gws, .ws_elems = QK_ENC_GEMM_WS_ELEMS};
+                              .ws = e->gws, .ws_elems = QK_ENC_GEMM_WS_ELEMS, .B16 = e->cow.b16};
         QK_TRY(qk_enc_gemm_launch(&g, e->stream));
     }
     const int win = w3 * (c->n_window_infer / cw);
@@ -374,18 +428,18 @@ static int run(qwen_hip_encoder *e, int mel_frames, int *tokens_out) {
         const enc_layer *y = &e->L[l];
         /* self-attention block (:318-338) */
         QK_TRY(qk_enc_layernorm_launch(e->x, y->ln1w, y->ln1b, e->xn, T, d, 1e-5f, e->stream));
-        QK_TRY(gemm(e, e->xn, d, y->wqkv, d, e->qkv, 3 * d, T, 3 * d, d, NULL, y->bqkv, 0, 0));
+        QK_TRY(gemm(e, e->xn, d, &y->wqkv, d, e->qkv, 3 * d, T, 3 * d, d, NULL, y->bqkv, 0, 0));
         QK_TRY(qk_enc_attention_launch(e->qkv, e->att, T, H, 64, win, scale, e->stream));
-        QK_TRY(gemm(e, e->att, d, y->wo, d, e->x, d, T, d, d, NULL, y->bo, 0, 1));
+        QK_TRY(gemm(e, e->att, d, &y->wo, d, e->x, d, T, d, d, NULL, y->bo, 0, 1));
         /* FFN block (:340-353) */
         QK_TRY(qk_enc_layernorm_launch(e->x, y->ln2w, y->ln2b, e->xn, T, d, 1e-5f, e->stream));
-        QK_TRY(gemm(e, e->xn, d, y->fc1w, d, e->mid, c->ffn_dim, T, c->ffn_dim, d, NULL, y->fc1b, 1, 0));
-        QK_TRY(gemm(e, e->mid, c->ffn_dim, y->fc2w, c->ffn_dim, e->x, d, T, d, c->ffn_dim, NULL, y->fc2b, 0, 1));
+        QK_TRY(gemm(e, e->xn, d, &y->fc1w, d, e->mid, c->ffn_dim, T, c->ffn_dim, d, NULL, y->fc1b, 1, 0));
+        QK_TRY(gemm(e, e->mid, c->ffn_dim, &y->fc2w, c->ffn_dim, e->x, d, T, d, c->ffn_dim, NULL, y->fc2b, 0, 1));
     }
     /* ln_post, proj1 + GELU, proj2 (:358-371) */
     QK_TRY(qk_enc_layernorm_launch(e->x, e->lnpw, e->lnpb, e->xn, T, d, 1e-5f, e->stream));
-    QK_TRY(gemm(e, e->xn, d, e->p1w, d, e->mid, d, T, d, d, NULL, e->p1b, 1, 0));
-    QK_TRY(gemm(e, e->mid, d, e->p2w, d, e->out, c->output_dim, T, c->output_dim, d, NULL, e->p2b, 0, 0));
+    QK_TRY(gemm(e, e->xn, d, &e->p1w, d, e->mid, d, T, d, d, NULL, e->p1b, 1, 0));
+    QK_TRY(gemm(e, e->mid, d, &e->p2w, d, e->out, c->output_dim, T, c->output_dim, d, NULL, e->p2b, 0, 0));
     *tokens_out = T;
     return 0;
 }

@@ -204,23 +204,144 @@ __global__ __launch_bounds__(256) void enc_gemm_reduce(qk_enc_gemm_args a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same product with one operand bf16 (the weights, exact) and the other
+// fp32, split on the way into LDS as hi = bf16(x), lo = bf16(x - hi):
+// x.w = hi.w + lo.w on v_mfma_f32_16x16x32_bf16 (fp32 accumulation).  Block
+// tile 64 x 64, 4 waves of 32 x 32, K 32 at a time (one MFMA k-step), the next
+// tile's loads in flight during the MFMAs.  WA: the bf16 operand is A (rows
+// M); otherwise B (rows N).  Fragments: lane l supplies row (l & 15), k
+// 8 (l >> 4) .. + 7, for both operands.
+// ---------------------------------------------------------------------------
+#define EH_K 32
+#define EH_LD (EH_K + 8)           // 80-byte rows: 16-row fragment reads conflict free
+typedef float eh_f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 eh_bf16x4 __attribute__((ext_vector_type(4)));
+
+template <bool WA>
+__global__ __launch_bounds__(256) void enc_gemm_hl(qk_enc_gemm_args a) {
+    __shared__ __attribute__((aligned(16))) __bf16 sX[2][EG_T][EH_LD];   // fp32 operand: [hi, lo]
+    __shared__ __attribute__((aligned(16))) __bf16 sW[EG_T][EH_LD];      // bf16 operand
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * EG_T, n0 = blockIdx.x * EG_T;
+    // fp32 side: rows of X = M rows of A (WA false) or N rows of B (WA true)
+    const float *X = WA ? a.B : a.A;
+    const uint16_t *W = WA ? a.A16 : a.B16;
+    const int ldx = WA ? a.ldb : a.lda, ldw = WA ? a.lda : a.ldb;
+    const int xr0 = WA ? n0 : m0, xrn = WA ? a.N : a.M;
+    const int wr0 = WA ? m0 : n0, wrn = WA ? a.M : a.N;
+    // loaders: X tile 64 x 32 fp32 = 2 float4 per thread; W tile 64 x 32 bf16 = 1 uint4 per thread
+    const int xr = tid >> 3, xk = (tid & 7) * 4;       // rows xr and xr + 32
+    const int wr = tid >> 2, wk = (tid & 3) * 8;
+
+    float4 rx[2];
+    uint4 rw;
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int g = xr0 + xr + 32 * i, gk = k0 + xk;
+            rx[i] = (g < xrn && gk < a.K) ? *reinterpret_cast<const float4 *>(X + (long)g * ldx + gk)
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const int g = wr0 + wr, gk = k0 + wk;
+        rw = (g < wrn && gk < a.K) ? *reinterpret_cast<const uint4 *>(W + (long)g * ldw + gk) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const eh_f32x4 x = {rx[i].x, rx[i].y, rx[i].z, rx[i].w};
+            const eh_bf16x4 hi = __builtin_convertvector(x, eh_bf16x4);
+            const eh_bf16x4 lo = __builtin_convertvector(x - __builtin_convertvector(hi, eh_f32x4), eh_bf16x4);
+            *reinterpret_cast<eh_bf16x4 *>(&sX[0][xr + 32 * i][xk]) = hi;
+            *reinterpret_cast<eh_bf16x4 *>(&sX[1][xr + 32 * i][xk]) = lo;
+        }
+        *reinterpret_cast<uint4 *>(&sW[wr][wk]) = rw;
+    };
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    const int kb = blockIdx.z * a.kc, ke = min(a.K, kb + a.kc);
+    gload(kb);
+    for (int k0 = kb; k0 < ke; k0 += EH_K) {
+        __syncthreads();
+        lstore();
+        __syncthreads();
+        if (k0 + EH_K < ke) gload(k0 + EH_K);
+        const int kf = 8 * (lane >> 4);
+        bf16x8 fm[2][2], fn[2][2];      // [tile][hi / lo or weight]: M-side and N-side fragments
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int rm = wm * 32 + i * 16 + (lane & 15), rn = wn * 32 + i * 16 + (lane & 15);
+            if (WA) {
+                fm[i][0] = *reinterpret_cast<const bf16x8 *>(&sW[rm][kf]);
+                fn[i][0] = *reinterpret_cast<const bf16x8 *>(&sX[0][rn][kf]);
+                fn[i][1] = *reinterpret_cast<const bf16x8 *>(&sX[1][rn][kf]);
+            } else {
+                fm[i][0] = *reinterpret_cast<const bf16x8 *>(&sX[0][rm][kf]);
+                fm[i][1] = *reinterpret_cast<const bf16x8 *>(&sX[1][rm][kf]);
+                fn[i][0] = *reinterpret_cast<const bf16x8 *>(&sW[rn][kf]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                if (WA) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fm[i][0], fn[j][0], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fm[i][0], fn[j][1], acc[i][j], 0, 0, 0);
+                } else {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fm[i][0], fn[j][0], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fm[i][1], fn[j][0], acc[i][j], 0, 0, 0);
+                }
+            }
+    }
+
+    float *part = a.split > 1 ? a.ws + (long)blockIdx.z * a.M * a.N : nullptr;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+                if (m >= a.M || n >= a.N) continue;
+                if (part)
+                    part[(long)m * a.N + n] = acc[i][j][r];
+                else
+                    enc_epilogue(a, m, n, acc[i][j][r], a.C + (long)m * a.ldc + n);
+            }
+        }
+    }
+}
+
 extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
-    if (!a || !a->A || !a->B || !a->C || a->M <= 0 || a->N <= 0 || a->K <= 0 || (a->K & 3) || (a->lda & 3) ||
-        (a->ldb & 3) || a->lda < a->K || a->ldb < a->K || a->ldc < a->N || (a->pe && a->pe_rows <= 0))
+    if (!a || (a->A16 && a->B16)) return QWEN_HIP_EINVAL;
+    const bool hl = a->A16 || a->B16;
+    if (!(a->A || a->A16) || !(a->B || a->B16) || !a->C || a->M <= 0 || a->N <= 0 || a->K <= 0 || (a->K & 3) ||
+        (a->lda & 3) || (a->ldb & 3) || a->lda < a->K || a->ldb < a->K || a->ldc < a->N || (a->pe && a->pe_rows <= 0))
         return QWEN_HIP_EINVAL;
+    if (hl && ((a->K % EH_K) || (a->A16 ? (a->lda & 7) || !a->B : (a->ldb & 7) || !a->A))) return QWEN_HIP_EINVAL;
+    const int kstep = hl ? EH_K : EG_K;
     qk_enc_gemm_args g = *a;
     const long tiles = (long)((a->N + EG_T - 1) / EG_T) * ((a->M + EG_T - 1) / EG_T);
-    // slices so that the grid holds ~2 blocks per CU, each slice >= 128 deep
-    int split = a->ws ? (int)((512 + tiles - 1) / tiles) : 1;
+    // slices so that the grid holds ~4 blocks per CU, each slice >= 128 deep
+    int split = a->ws ? (int)((1024 + tiles - 1) / tiles) : 1;
     if (split > 8) split = 8;
     if (split > a->K / 128) split = a->K / 128;
     if (split < 1) split = 1;
-    g.kc = ((a->K + split - 1) / split + EG_K - 1) / EG_K * EG_K;
+    g.kc = ((a->K + split - 1) / split + kstep - 1) / kstep * kstep;
     g.split = (a->K + g.kc - 1) / g.kc;
     if (g.split > 1 && (long)g.split * a->M * a->N > a->ws_elems) g.kc = a->K, g.split = 1;
     if (g.split == 1) g.kc = a->K;
     dim3 grid((a->N + EG_T - 1) / EG_T, (a->M + EG_T - 1) / EG_T, g.split);
-    enc_gemm<<<grid, 256, 0, s>>>(g);
+    if (a->A16) enc_gemm_hl<true><<<grid, 256, 0, s>>>(g);
+    else if (a->B16) enc_gemm_hl<false><<<grid, 256, 0, s>>>(g);
+    else enc_gemm<<<grid, 256, 0, s>>>(g);
     if (g.split > 1) {
         long blocks = ((long)a->M * a->N + 255) / 256;
         if (blocks > 4096) blocks = 4096;

@@ -257,8 +257,14 @@ typedef struct {
     float *ws;
     long ws_elems;
     int kc, split;
+    /* bf16 weights (exact copies of bf16-valued fp32 weights): when A16 (A side)
+     * or B16 (B side) is set it replaces that operand, and the product runs on
+     * the bf16 matrix cores with the other, fp32, operand split hi + lo (two
+     * MFMAs per product, ~2^-17 relative per product); K and the bf16
+     * operand's leading dimension must be multiples of 32 and 8. */
+    const uint16_t *A16, *B16;
 } qk_enc_gemm_args;
-#define QK_ENC_GEMM_WS_ELEMS (1024L * 64 * 64)  /* split * M * N <= (512 + tiles) * 4096 for every split the launcher picks */
+#define QK_ENC_GEMM_WS_ELEMS (2048L * 64 * 64)  /* split * M * N <= (1024 + tiles) * 4096 for every split the launcher picks */
 int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s);
 int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int chunks, int h_in, int w_in, int h_out,
                          int w_out, int kpad, int mel_frames, hipStream_t s);
