@@ -165,3 +165,25 @@ def test_encoder_error_conventions(P, qa, gpu):
     ref = load(qa, cfg, m).forward(mel)
     np.testing.assert_array_equal(e.forward(mel), ref)
     e.close()
+
+
+def test_encoder_fp32_weights_take_the_fp32_gemm(P, qa, gpu):
+    """A weight matrix whose values are not all bf16 values (possible through
+    the fp32 load API) keeps fp32 and runs on the fp32 GEMM, next to
+    bf16-valued ones on the bf16 GEMM; the mix matches the reference encoder
+    (oracle/_ref) on the same weights."""
+    if not P.ref_available():
+        pytest.skip("oracle/_ref not built")
+    cfg = qa.EncConfig(128, 2, 2, 64, 256, 96, 100, 200)
+    m = P.SynthEncoder(cfg, seed=9)
+    rng = np.random.default_rng(9)
+    wo = m.layers[1][6]
+    m.layers[1][6] = (wo * (1.0 + 1e-3 * rng.standard_normal(wo.shape))).astype(np.float32)   # off the bf16 grid
+    assert np.any(m.layers[1][6].view(np.uint32) & 0xFFFF)
+    mel = P.synth_mel(250, 9, 1)
+    e = load(qa, cfg, m)
+    out = e.forward(mel)
+    ref = P.RefEncoder(m).forward(mel, e.tokens(250))
+    err = np.abs(out - ref)
+    assert np.all(err <= ATOL + RTOL * np.abs(ref)), float(err.max())
+    e.close()
