@@ -218,51 +218,59 @@ __global__ __launch_bounds__(256) void enc_gemm_reduce(qk_enc_gemm_args a) {
 typedef float eh_f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 eh_bf16x4 __attribute__((ext_vector_type(4)));
 
-template <bool WA>
+template <bool WA, int TT>        // TT x TT MFMA tiles of 16 x 16 per wave: block tile 32 TT x 32 TT
 __global__ __launch_bounds__(256) void enc_gemm_hl(qk_enc_gemm_args a) {
-    __shared__ __attribute__((aligned(16))) __bf16 sX[2][EG_T][EH_LD];   // fp32 operand: [hi, lo]
-    __shared__ __attribute__((aligned(16))) __bf16 sW[EG_T][EH_LD];      // bf16 operand
+    constexpr int BT = 32 * TT;                       // block tile edge
+    constexpr int XPT = BT * EH_K / 4 / 256;          // fp32 float4 loads per thread
+    constexpr int WPT = BT * EH_K / 8 / 256;          // bf16 16-byte loads per thread
+    __shared__ __attribute__((aligned(16))) __bf16 sX[2][BT][EH_LD];   // fp32 operand: [hi, lo]
+    __shared__ __attribute__((aligned(16))) __bf16 sW[BT][EH_LD];      // bf16 operand
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * EG_T, n0 = blockIdx.x * EG_T;
+    const int m0 = blockIdx.y * BT, n0 = blockIdx.x * BT;
     // fp32 side: rows of X = M rows of A (WA false) or N rows of B (WA true)
     const float *X = WA ? a.B : a.A;
     const uint16_t *W = WA ? a.A16 : a.B16;
     const int ldx = WA ? a.ldb : a.lda, ldw = WA ? a.lda : a.ldb;
     const int xr0 = WA ? n0 : m0, xrn = WA ? a.N : a.M;
     const int wr0 = WA ? m0 : n0, wrn = WA ? a.M : a.N;
-    // loaders: X tile 64 x 32 fp32 = 2 float4 per thread; W tile 64 x 32 bf16 = 1 uint4 per thread
-    const int xr = tid >> 3, xk = (tid & 7) * 4;       // rows xr and xr + 32
+    // loaders: X rows xr + 32 i (4 floats at xk), W rows wr + 64 i (8 bf16 at wk)
+    const int xr = tid >> 3, xk = (tid & 7) * 4;
     const int wr = tid >> 2, wk = (tid & 3) * 8;
 
-    float4 rx[2];
-    uint4 rw;
+    float4 rx[XPT];
+    uint4 rw[WPT];
     auto gload = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < XPT; i++) {
             const int g = xr0 + xr + 32 * i, gk = k0 + xk;
             rx[i] = (g < xrn && gk < a.K) ? *reinterpret_cast<const float4 *>(X + (long)g * ldx + gk)
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        const int g = wr0 + wr, gk = k0 + wk;
-        rw = (g < wrn && gk < a.K) ? *reinterpret_cast<const uint4 *>(W + (long)g * ldw + gk) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int i = 0; i < WPT; i++) {
+            const int g = wr0 + wr + 64 * i, gk = k0 + wk;
+            rw[i] = (g < wrn && gk < a.K) ? *reinterpret_cast<const uint4 *>(W + (long)g * ldw + gk)
+                                          : make_uint4(0u, 0u, 0u, 0u);
+        }
     };
     auto lstore = [&]() {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < XPT; i++) {
             const eh_f32x4 x = {rx[i].x, rx[i].y, rx[i].z, rx[i].w};
             const eh_bf16x4 hi = __builtin_convertvector(x, eh_bf16x4);
             const eh_bf16x4 lo = __builtin_convertvector(x - __builtin_convertvector(hi, eh_f32x4), eh_bf16x4);
             *reinterpret_cast<eh_bf16x4 *>(&sX[0][xr + 32 * i][xk]) = hi;
             *reinterpret_cast<eh_bf16x4 *>(&sX[1][xr + 32 * i][xk]) = lo;
         }
-        *reinterpret_cast<uint4 *>(&sW[wr][wk]) = rw;
+#pragma unroll
+        for (int i = 0; i < WPT; i++) *reinterpret_cast<uint4 *>(&sW[wr + 64 * i][wk]) = rw[i];
     };
-    f32x4 acc[2][2];
+    f32x4 acc[TT][TT];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TT; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TT; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     const int kb = blockIdx.z * a.kc, ke = min(a.K, kb + a.kc);
     gload(kb);
@@ -272,10 +280,10 @@ __global__ __launch_bounds__(256) void enc_gemm_hl(qk_enc_gemm_args a) {
         __syncthreads();
         if (k0 + EH_K < ke) gload(k0 + EH_K);
         const int kf = 8 * (lane >> 4);
-        bf16x8 fm[2][2], fn[2][2];      // [tile][hi / lo or weight]: M-side and N-side fragments
+        bf16x8 fm[TT][2], fn[TT][2];    // [tile][hi / lo or weight]: M-side and N-side fragments
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int rm = wm * 32 + i * 16 + (lane & 15), rn = wn * 32 + i * 16 + (lane & 15);
+        for (int i = 0; i < TT; i++) {
+            const int rm = wm * 16 * TT + i * 16 + (lane & 15), rn = wn * 16 * TT + i * 16 + (lane & 15);
             if (WA) {
                 fm[i][0] = *reinterpret_cast<const bf16x8 *>(&sW[rm][kf]);
                 fn[i][0] = *reinterpret_cast<const bf16x8 *>(&sX[0][rn][kf]);
@@ -287,9 +295,9 @@ __global__ __launch_bounds__(256) void enc_gemm_hl(qk_enc_gemm_args a) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < TT; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
+            for (int j = 0; j < TT; j++) {
                 if (WA) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fm[i][0], fn[j][0], acc[i][j], 0, 0, 0);
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fm[i][0], fn[j][1], acc[i][j], 0, 0, 0);
@@ -302,13 +310,13 @@ __global__ __launch_bounds__(256) void enc_gemm_hl(qk_enc_gemm_args a) {
 
     float *part = a.split > 1 ? a.ws + (long)blockIdx.z * a.M * a.N : nullptr;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < TT; i++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+        for (int j = 0; j < TT; j++) {
+            const int n = n0 + wn * 16 * TT + j * 16 + (lane & 15);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+                const int m = m0 + wm * 16 * TT + i * 16 + 4 * (lane >> 4) + r;
                 if (m >= a.M || n >= a.N) continue;
                 if (part)
                     part[(long)m * a.N + n] = acc[i][j][r];
@@ -339,9 +347,19 @@ extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
     if (g.split > 1 && (long)g.split * a->M * a->N > a->ws_elems) g.kc = a->K, g.split = 1;
     if (g.split == 1) g.kc = a->K;
     dim3 grid((a->N + EG_T - 1) / EG_T, (a->M + EG_T - 1) / EG_T, g.split);
-    if (a->A16) enc_gemm_hl<true><<<grid, 256, 0, s>>>(g);
-    else if (a->B16) enc_gemm_hl<false><<<grid, 256, 0, s>>>(g);
-    else enc_gemm<<<grid, 256, 0, s>>>(g);
+    // large products (the stem convolutions) take 128 x 128 tiles: half the
+    // operand bytes per MFMA, which the per-CU load path needs at full rate
+    const bool big = hl && g.split == 1 && (long)a->M * a->N >= (1L << 22);
+    dim3 grid2((a->N + 127) / 128, (a->M + 127) / 128, 1);
+    if (a->A16) {
+        if (big) enc_gemm_hl<true, 4><<<grid2, 256, 0, s>>>(g);
+        else enc_gemm_hl<true, 2><<<grid, 256, 0, s>>>(g);
+    } else if (a->B16) {
+        if (big) enc_gemm_hl<false, 4><<<grid2, 256, 0, s>>>(g);
+        else enc_gemm_hl<false, 2><<<grid, 256, 0, s>>>(g);
+    } else {
+        enc_gemm<<<grid, 256, 0, s>>>(g);
+    }
     if (g.split > 1) {
         long blocks = ((long)a->M * a->N + 255) / 256;
         if (blocks > 4096) blocks = 4096;
