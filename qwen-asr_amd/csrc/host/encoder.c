@@ -387,6 +387,16 @@ static int gemm(qwen_hip_encoder *e, const float *A, int lda, const enc_mat *W, 
     return qk_enc_gemm_launch(&g, e->stream);
 }
 
+/* x += A . W^T + bias (the residual projections), then xn = LayerNorm(x) (w, b) */
+static int gemm_add_ln(qwen_hip_encoder *e, const float *A, int lda, const enc_mat *W, int K, const float *bias,
+                       int T, const float *lnw, const float *lnb) {
+    const int d = e->cfg.d_model;
+    qk_enc_gemm_args g = {.A = A, .B = W->f32, .C = e->x, .M = T, .N = d, .K = K, .lda = lda, .ldb = K, .ldc = d,
+                          .bias_n = bias, .add = 1, .ws = e->gws, .ws_elems = QK_ENC_GEMM_WS_ELEMS, .B16 = W->b16,
+                          .ln_w = lnw, .ln_b = lnb, .ln_out = e->xn, .ln_eps = 1e-5f};
+    return qk_enc_gemm_launch(&g, e->stream);
+}
+
 /* one stem layer: im2col over every chunk, GEMM with bias + GELU, padding zeroed */
 static int stem_layer(qwen_hip_encoder *e, const float *in, int c_in, int chunks, int h_in, int w_in, int kpad,
                       int mel_frames, const float *w, const uint16_t *w16, const float *b, float *out,
@@ -424,20 +434,20 @@ static int run(qwen_hip_encoder *e, int mel_frames, int *tokens_out) {
     }
     const int win = w3 * (c->n_window_infer / cw);
     const float scale = 1.0f / sqrtf((float)c->head_dim);
+    /* pre-LayerNorm layers (:318-353): each residual projection's split-K
+     * reduce also applies the next LayerNorm (ln2, the next layer's ln1, ln_post) */
+    QK_TRY(qk_enc_layernorm_launch(e->x, e->L[0].ln1w, e->L[0].ln1b, e->xn, T, d, 1e-5f, e->stream));
     for (int l = 0; l < c->layers; l++) {
         const enc_layer *y = &e->L[l];
-        /* self-attention block (:318-338) */
-        QK_TRY(qk_enc_layernorm_launch(e->x, y->ln1w, y->ln1b, e->xn, T, d, 1e-5f, e->stream));
         QK_TRY(gemm(e, e->xn, d, &y->wqkv, d, e->qkv, 3 * d, T, 3 * d, d, NULL, y->bqkv, 0, 0));
         QK_TRY(qk_enc_attention_launch(e->qkv, e->att, T, H, 64, win, scale, e->stream));
-        QK_TRY(gemm(e, e->att, d, &y->wo, d, e->x, d, T, d, d, NULL, y->bo, 0, 1));
-        /* FFN block (:340-353) */
-        QK_TRY(qk_enc_layernorm_launch(e->x, y->ln2w, y->ln2b, e->xn, T, d, 1e-5f, e->stream));
+        QK_TRY(gemm_add_ln(e, e->att, d, &y->wo, d, y->bo, T, y->ln2w, y->ln2b));
         QK_TRY(gemm(e, e->xn, d, &y->fc1w, d, e->mid, c->ffn_dim, T, c->ffn_dim, d, NULL, y->fc1b, 1, 0));
-        QK_TRY(gemm(e, e->mid, c->ffn_dim, &y->fc2w, c->ffn_dim, e->x, d, T, d, c->ffn_dim, NULL, y->fc2b, 0, 1));
+        const int last = l + 1 == c->layers;
+        QK_TRY(gemm_add_ln(e, e->mid, c->ffn_dim, &y->fc2w, c->ffn_dim, y->fc2b, T,
+                           last ? e->lnpw : e->L[l + 1].ln1w, last ? e->lnpb : e->L[l + 1].ln1b));
     }
-    /* ln_post, proj1 + GELU, proj2 (:358-371) */
-    QK_TRY(qk_enc_layernorm_launch(e->x, e->lnpw, e->lnpb, e->xn, T, d, 1e-5f, e->stream));
+    /* proj1 + GELU, proj2 on the ln_post rows (:358-371) */
     QK_TRY(gemm(e, e->xn, d, &e->p1w, d, e->mid, d, T, d, d, NULL, e->p1b, 1, 0));
     QK_TRY(gemm(e, e->mid, d, &e->p2w, d, e->out, c->output_dim, T, c->output_dim, d, NULL, e->p2b, 0, 0));
     *tokens_out = T;

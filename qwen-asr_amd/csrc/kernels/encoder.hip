@@ -327,6 +327,59 @@ __global__ __launch_bounds__(256) void enc_gemm_hl(qk_enc_gemm_args a) {
     }
 }
 
+// split-K reduce of one row (block per row, N <= 1024) that then LayerNorms
+// the finished row into ln_out, with enc_layernorm's element-to-thread map and
+// reduction order (so the result equals a separate LayerNorm pass)
+__global__ __launch_bounds__(256) void enc_gemm_reduce_ln(qk_enc_gemm_args a) {
+    __shared__ float red[4];
+    const int m = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long MN = (long)a.M * a.N;
+    float v[4];
+    float s = 0.0f;
+    float x[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {      // every slice of the row's 4 columns in one batch of loads
+        const int n = min(threadIdx.x + 256 * j, a.N - 1);
+        x[j] = sum_splits<8>(a.ws + (long)m * a.N + n, a.split, MN);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = threadIdx.x + 256 * j;
+        v[j] = 0.0f;
+        if (n < a.N) {
+            float *y = a.C + (long)m * a.ldc + n;
+            enc_epilogue(a, m, n, x[j], y);
+            v[j] = *y;
+            s += v[j];
+        }
+    }
+    s = wave_sum(s);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)a.N;
+    __syncthreads();
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = threadIdx.x + 256 * j;
+        if (n < a.N) {
+            const float d = v[j] - mean;
+            q = fmaf(d, d, q);
+        }
+    }
+    q = wave_sum(q);
+    if (lane == 0) red[wave] = q;
+    __syncthreads();
+    const float var = (red[0] + red[1] + red[2] + red[3]) / (float)a.N;
+    const float inv_std = 1.0f / sqrtf(var + a.ln_eps);
+    float *o = a.ln_out + (long)m * a.N;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = threadIdx.x + 256 * j;
+        if (n < a.N) o[n] = (v[j] - mean) * inv_std * a.ln_w[n] + a.ln_b[n];
+    }
+}
+
 extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
     if (!a || (a->A16 && a->B16)) return QWEN_HIP_EINVAL;
     const bool hl = a->A16 || a->B16;
@@ -334,6 +387,7 @@ extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
         (a->lda & 3) || (a->ldb & 3) || a->lda < a->K || a->ldb < a->K || a->ldc < a->N || (a->pe && a->pe_rows <= 0))
         return QWEN_HIP_EINVAL;
     if (hl && ((a->K % EH_K) || (a->A16 ? (a->lda & 7) || !a->B : (a->ldb & 7) || !a->A))) return QWEN_HIP_EINVAL;
+    if (a->ln_out && (!a->ln_w || !a->ln_b)) return QWEN_HIP_EINVAL;
     const int kstep = hl ? EH_K : EG_K;
     qk_enc_gemm_args g = *a;
     const long tiles = (long)((a->N + EG_T - 1) / EG_T) * ((a->M + EG_T - 1) / EG_T);
@@ -360,12 +414,22 @@ extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
     } else {
         enc_gemm<<<grid, 256, 0, s>>>(g);
     }
+    const bool ln = a->ln_out != nullptr;
+    if (g.split > 1 && g.split <= 8 && ln && a->N <= 1024 && a->ldc == a->N) {
+        enc_gemm_reduce_ln<<<a->M, 256, 0, s>>>(g);
+        return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+    }
     if (g.split > 1) {
         long blocks = ((long)a->M * a->N + 255) / 256;
         if (blocks > 4096) blocks = 4096;
         enc_gemm_reduce<<<(int)blocks, 256, 0, s>>>(g);
     }
-    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+    if (hipGetLastError() != hipSuccess) return QWEN_HIP_EDEVICE;
+    if (ln) {
+        if (a->ldc != a->N) return QWEN_HIP_EINVAL;
+        return qk_enc_layernorm_launch(a->C, a->ln_w, a->ln_b, a->ln_out, a->M, a->N, a->ln_eps, s);
+    }
+    return 0;
 }
 
 // conv3 output [480][chunks][16][w] -> rows [token][480*16], token = chunk*w + t for

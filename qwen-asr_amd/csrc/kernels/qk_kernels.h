@@ -263,6 +263,12 @@ typedef struct {
      * MFMAs per product, ~2^-17 relative per product); K and the bf16
      * operand's leading dimension must be multiples of 32 and 8. */
     const uint16_t *A16, *B16;
+    /* optional LayerNorm of the finished rows of C into ln_out (weights ln_w,
+     * ln_b, eps ln_eps): done in the split-K reduce when there is one (N <=
+     * 1024), else by a LayerNorm pass after the product */
+    const float *ln_w, *ln_b;
+    float *ln_out;
+    float ln_eps;
 } qk_enc_gemm_args;
 #define QK_ENC_GEMM_WS_ELEMS (2048L * 64 * 64)  /* split * M * N <= (1024 + tiles) * 4096 for every split the launcher picks */
 int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s);
