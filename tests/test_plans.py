@@ -1,0 +1,54 @@
+"""Launch planners of the prefill kernels (host code, no GPU needed):
+qk_gemm_plan_for (row tile, split-K slices of the projection GEMMs) and
+qk_attn_prefill_plan (key chunk per block of the prefill attention).  Their
+invariants are what the kernels rely on: slices cover K exactly once in whole
+64-deep k tiles, at most 16 of them (the partial-sum consumers' bound); key
+chunks are whole 32-key tiles, cover the longest query tile, and no block
+walks more than max(256, a sixth of it) keys."""
+import ctypes as C
+
+import pytest
+
+
+class GemmPlan(C.Structure):
+    _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int)]
+
+
+SHAPES = [(M, N, K) for M in (1, 17, 31, 32, 33, 64, 65, 401, 512, 513, 1515, 8191)
+          for N in (1024, 2048, 4096, 6144, 12288) for K in (1024, 2048, 3072, 6144)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_plan_invariants(qa, M, N, K):
+    p = GemmPlan()
+    qa.lib().qk_gemm_plan_for(M, N, K, C.byref(p))
+    assert p.bm == (32 if M <= 32 else 64 if M <= 512 else 128)
+    assert p.kc > 0 and p.kc % 64 == 0
+    assert 1 <= p.nsplit <= 16
+    assert p.kc * p.nsplit >= K and p.kc * (p.nsplit - 1) < K       # every slice non-empty, K covered once
+    tiles = -(-M // p.bm) * -(-N // 128)
+    if tiles >= 256:
+        assert p.nsplit == 1                                           # the grid alone fills the chip
+
+
+def kmax_of(seq_q, seq_k, q_offset):
+    nq = -(-seq_q // 64)
+    return max(min(seq_k, q_offset + min(seq_q, (t + 1) * 64)) for t in range(nq))
+
+
+@pytest.mark.parametrize("seq_q,seq_k,q_offset", [(1, 1, 0), (31, 1000, 969), (64, 64, 0), (401, 401, 0),
+                                                  (1515, 1515, 0), (6400, 6400, 0), (8191, 8191, 0),
+                                                  (26, 1024, 998), (100, 5000, 4900), (2048, 4096, 2048)])
+def test_attention_plan_invariants(qa, seq_q, seq_k, q_offset):
+    lib = qa.lib()
+    lib.qk_attn_prefill_plan.restype = C.c_size_t
+    lib.qk_attn_prefill_plan.argtypes = [C.c_int] * 5 + [C.POINTER(C.c_int)] * 2
+    chunk, nsplit = C.c_int(), C.c_int()
+    part = lib.qk_attn_prefill_plan(seq_q, seq_k, q_offset, 16, 8, C.byref(chunk), C.byref(nsplit))
+    kmax = kmax_of(seq_q, seq_k, q_offset)
+    assert chunk.value > 0 and chunk.value % 32 == 0
+    assert nsplit.value >= 1 and chunk.value * nsplit.value >= kmax and chunk.value * (nsplit.value - 1) < kmax
+    cap = max(256, -(-(-(-kmax // 6)) // 32) * 32)
+    assert chunk.value <= max(cap, -(-kmax // 32) * 32)
+    # partial buffer: (o[128], m, l) per split, query and head, only when split
+    assert part == (nsplit.value * seq_q * 16 * 130 if nsplit.value > 1 else 0)
