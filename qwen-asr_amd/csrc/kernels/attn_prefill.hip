@@ -145,8 +145,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, kq = lane >> 4;
     const int nq = (a.seq_q + PF_Q - 1) / PF_Q;
-    const int t = nq - 1 - (int)blockIdx.x;              // longest query tiles first
-    const int g = blockIdx.y, split = blockIdx.z;
+    // blocks go out in x order: query tiles longest first, all kv heads of a
+    // tile next to each other, so the causal triangle's long tiles start first
+    const int t = nq - 1 - (int)blockIdx.x / a.kv_heads;
+    const int g = (int)blockIdx.x % a.kv_heads, split = blockIdx.z;
     const int q0 = t * PF_Q;
     const int qn = min(PF_Q, a.seq_q - q0);
     const int kend_tile = min(a.seq_k, a.q_offset + q0 + qn);
@@ -367,6 +369,9 @@ extern "C" size_t qk_attn_prefill_plan(int seq_q, int seq_k, int q_offset, int h
     long cap = ((kmax + 5) / 6 + PF_KT - 1) / PF_KT * PF_KT;
     if (cap < 256) cap = 256;
     if (c > cap) c = cap;
+    // with two (query tile, kv head) blocks per CU or more, the longest-first
+    // order alone balances the CUs: no split, so no partials and no merge pass
+    if ((long)nq * kv_heads >= 2L * 256) c = (kmax + PF_KT - 1) / PF_KT * PF_KT;
     if (c > kmax) c = (kmax + PF_KT - 1) / PF_KT * PF_KT;
     *chunk = (int)c;
     *nsplit = (int)((kmax + c - 1) / c);
@@ -382,7 +387,7 @@ extern "C" int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s) {
     // every key the last query tile sees must fall in some split
     const int kmax = a->seq_k < a->q_offset + a->seq_q ? a->seq_k : a->q_offset + a->seq_q;
     if ((long)a->chunk * a->nsplit < kmax) return QWEN_HIP_EINVAL;
-    attn_prefill<<<dim3(nq, a->kv_heads, a->nsplit), 256, 0, s>>>(*a);
+    attn_prefill<<<dim3(nq * a->kv_heads, 1, a->nsplit), 256, 0, s>>>(*a);
     if (a->nsplit > 1)
         attn_prefill_merge<<<(unsigned)(((long)a->seq_q * a->heads + 3) / 4), 256, 0, s>>>(*a);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;

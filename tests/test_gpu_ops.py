@@ -137,17 +137,23 @@ def test_causal_attention(P, qa, gpu, sq, sk, q_off):
     np.testing.assert_allclose(host(dout), exp, atol=3e-5, rtol=1e-4)
 
 
-def test_causal_attention_long_walk(P, qa, gpu):
-    """6400 query rows: the launch plan caps a block's walk at a sixth of the
-    longest query tile, so blocks walk up to ~1100 keys (the path the 8k-row
-    prefill takes) and the merge combines up to six splits.  Checked against a
+@pytest.mark.parametrize("sq", [3000, 6400])
+def test_causal_attention_long_walk(P, qa, gpu, sq):
+    """Long prefills.  3000 query rows (47 query tiles x 8 kv heads, fewer than
+    two blocks per CU): the plan caps a block's walk at a sixth of the longest
+    query tile, so blocks walk 512 keys and the merge combines six splits.
+    6400 rows (800 blocks): no split, the last query tiles walk all 6400 keys
+    in one block (the path the 8k-row prefill takes).  Checked against a
     float64 causal softmax attention computed with torch on the same device
     (the CPU oracle is too slow at this size)."""
-    sq = sk = 6400
+    sk = sq
     nh, nkv, hd = 16, 8, 128
     chunk, nsplit = C.c_int(), C.c_int()
     qa.lib().qk_attn_prefill_plan(sq, sk, 0, nh, nkv, C.byref(chunk), C.byref(nsplit))
-    assert chunk.value >= 1000 and 2 <= nsplit.value <= 8, (chunk.value, nsplit.value)
+    if sq == 3000:
+        assert chunk.value == 512 and nsplit.value == 6, (chunk.value, nsplit.value)
+    else:
+        assert chunk.value == sq and nsplit.value == 1, (chunk.value, nsplit.value)
     g = gpu.Generator(device="cuda").manual_seed(11)
     Q = gpu.randn((sq, nh * hd), generator=g, device="cuda", dtype=gpu.float32)
     K = gpu.randn((sk, nkv * hd), generator=g, device="cuda", dtype=gpu.float32)
