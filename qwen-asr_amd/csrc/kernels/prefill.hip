@@ -273,6 +273,132 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
     }
 }
 
+// ---------------------------------------------------------------------------
+// Large-M GEMM (same product and epilogues as gemm_hilo): block tile BM x 256
+// with 8 waves, each 64 x (256 / WGN) (BM 128: 2 x 4 waves of 64 x 64; BM 256:
+// 4 x 2 waves of 64 x 128).  K is walked 32 at a time through a ring of NST
+// LDS stages filled by direct global -> LDS loads (global_load_lds, 16 bytes
+// per lane), so no registers stage the operands and NST - 1 k tiles stay in
+// flight behind the MFMAs; one barrier per k tile.  A stage holds A_hi
+// [BM][32], A_lo [BM][32] and W [256][32] in bf16, rows of 64 bytes; a load
+// instruction fills 1 KB (16 rows) with lane l at byte 16 l, i.e. row l / 4,
+// 16-byte slot l % 4.  Slot p of row r holds k chunk p ^ ((r / 4) % 4): the
+// 16 rows x 16 bytes a fragment read touches then fall in 16 different
+// 16-byte bank groups.
+// ---------------------------------------------------------------------------
+#define QK_GBK 32
+
+template <int EPI, int BM>
+__global__ __launch_bounds__(512, 1) void gemm_hilo_wide(const uint16_t *__restrict__ ahi,
+                                                         const uint16_t *__restrict__ alo,
+                                                         const uint16_t *__restrict__ W, int M, int N, int K, int kc,
+                                                         float *y, uint16_t *ohi, uint16_t *olo) {
+    constexpr int BN = 256, WGM = BM / 64, WGN = 8 / WGM, TM = 4, TN = BN / WGN / 16;
+    constexpr int NST = BM == 128 ? 4 : 3;                 // stages: 4 x 32 KB or 3 x 48 KB
+    constexpr int AB = BM * 64, STAGE = 2 * AB + BN * 64;  // bytes: one A half, one stage
+    constexpr int AI = BM / 128;                           // 1 KB load instructions per wave: A half, W
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[NST][STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb = blockIdx.z * kc, ke = min(K, kb + kc);
+    const int nk = (ke - kb) / QK_GBK;
+
+    // this lane's load slot: row rr of a 16-row group, k chunk cl (swizzled)
+    const int rr = lane >> 2, cl = (lane & 3) ^ ((rr >> 2) & 3);
+    const size_t ra0 = (size_t)min(m0 + 16 * (AI * wave) + rr, M - 1) * K + kb + 8 * cl;
+    const size_t ra1 = (size_t)min(m0 + 16 * (AI * wave + 1) + rr, M - 1) * K + kb + 8 * cl;   // AI == 2 only
+    const uint16_t *pw = W + (size_t)(n0 + 32 * wave + rr) * K + kb + 8 * cl;
+    auto issue = [&](int kt) {
+        unsigned char *st = lds[kt % NST];
+        const int ko = kt * QK_GBK;
+        // (written out per row group: the builtin on an array element, or in a
+        // loop, made hipcc drop the kernel's host launch stub)
+        __builtin_amdgcn_global_load_lds(ahi + ra0 + ko, st + 1024 * (AI * wave), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(alo + ra0 + ko, st + AB + 1024 * (AI * wave), 16, 0, 0);
+        if constexpr (AI == 2) {
+            __builtin_amdgcn_global_load_lds(ahi + ra1 + ko, st + 1024 * (AI * wave + 1), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(alo + ra1 + ko, st + AB + 1024 * (AI * wave + 1), 16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds(pw + ko, st + 2 * AB + 2048 * wave, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(pw + (size_t)16 * K + ko, st + 2 * AB + 2048 * wave + 1024, 16, 0, 0);
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    // fragment reads: row (lane & 15) of a 16-row tile, k chunk lane >> 4
+    const int fr = lane & 15;
+    const int fo = fr * 64 + 16 * ((lane >> 4) ^ ((fr >> 2) & 3));
+    for (int t = 0; t < NST - 1 && t < nk; t++) issue(t);
+    for (int kt = 0; kt < nk; kt++) {
+        // this wave's loads of tile kt have landed once at most the later
+        // tiles' loads (2 AI + 2 per tile) are outstanding
+        const int later = min(nk - 1 - kt, NST - 2);
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * (2 * AI + 2)));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * AI + 2));
+        else __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();   // every wave's share of tile kt is in LDS; tile kt-1's stage is free
+        if (kt + NST - 1 < nk) issue(kt + NST - 1);
+        const unsigned char *st = lds[kt % NST];
+        bf16x8 bfr[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            bfr[j] = *reinterpret_cast<const bf16x8 *>(st + 2 * AB + (wn * TN * 16 + j * 16) * 64 + fo);
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int ro = (wm * 64 + i * 16) * 64 + fo;
+            const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(st + ro);
+            const bf16x8 al = *reinterpret_cast<const bf16x8 *>(st + AB + ro);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bfr[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bfr[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    float *yz = y + (EPI == QK_GEMM_STORE ? (size_t)blockIdx.z * M * N : 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * TN * 16 + j * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                const float v = acc[i][j][r];
+                if (EPI == QK_GEMM_SWIGLU) {
+                    const float u = __shfl_xor(v, 1, QK_WAVE);   // column n+1 lives in lane l^1
+                    if ((lane & 1) == 0 && m < M) {
+                        const size_t o = (size_t)m * (N / 2) + (n >> 1);
+                        split2(swiglu1(v, u), ohi[o], olo[o]);
+                    }
+                } else if (m < M) {
+                    if (EPI == QK_GEMM_STORE) yz[(size_t)m * N + n] = v;
+                    else y[(size_t)m * N + n] += v;
+                }
+            }
+        }
+    }
+}
+
+template <int BM>
+static void gemm_wide_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int N, int K,
+                               const qk_gemm_plan *p, int epi, float *y, uint16_t *oh, uint16_t *ol, hipStream_t s) {
+    const dim3 grid(N / 256, (M + BM - 1) / BM, p->nsplit);
+    if (epi == QK_GEMM_STORE)
+        gemm_hilo_wide<QK_GEMM_STORE, BM><<<grid, 512, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+    else if (epi == QK_GEMM_ADD)
+        gemm_hilo_wide<QK_GEMM_ADD, BM><<<grid, 512, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+    else
+        gemm_hilo_wide<QK_GEMM_SWIGLU, BM><<<grid, 512, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+}
+
 template <int WGM, int WGN, int TM, int TN>
 static void gemm_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int N, int K,
                           const qk_gemm_plan *p, int epi, float *y, uint16_t *oh, uint16_t *ol, hipStream_t s) {
@@ -286,6 +412,20 @@ static void gemm_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint
 }
 
 extern "C" void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p) {
+    // 256 x 256 or 128 x 256 tiles (one block per CU) where they alone fill
+    // every CU and the last round of blocks is not mostly empty (>= 85 % of
+    // the rounds' slots used); the larger tile first
+    for (int bm = 256; bm >= 128; bm -= 128) {
+        const long wide = (long)((M + bm - 1) / bm) * (N / 256);
+        const long slots = (wide + QK_GEMM_TARGET - 1) / QK_GEMM_TARGET * QK_GEMM_TARGET;
+        if (M <= 512 || N % 256 || K % QK_GBK || wide < QK_GEMM_TARGET || wide * 100 < slots * 85) continue;
+        p->bm = bm;
+        p->bn = 256;
+        p->nsplit = 1;
+        p->kc = (K + QK_BK - 1) / QK_BK * QK_BK;
+        return;
+    }
+    p->bn = QK_GEMM_BN;
     p->bm = M <= 32 ? 32 : M <= 512 ? 64 : 128;
     const long tiles = (long)((M + p->bm - 1) / p->bm) * ((N + QK_GEMM_BN - 1) / QK_GEMM_BN);
     const int kt = (K + QK_BK - 1) / QK_BK;
@@ -306,6 +446,13 @@ extern "C" int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const 
         return QWEN_HIP_EINVAL;
     if (p->nsplit > 1 && epi != QK_GEMM_STORE) return QWEN_HIP_EINVAL;
     if (epi == QK_GEMM_SWIGLU ? (!out_hi || !out_lo || (N & 1)) : !y) return QWEN_HIP_EINVAL;
+    if (p->bn == 256) {
+        if ((p->bm != 128 && p->bm != 256) || N % 256 || K % QK_GBK || p->kc % QK_GBK) return QWEN_HIP_EINVAL;
+        if (p->bm == 128) gemm_wide_dispatch<128>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);
+        else gemm_wide_dispatch<256>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);
+        return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+    }
+    if (p->bn != QK_GEMM_BN) return QWEN_HIP_EINVAL;
     if (p->bm == 32) gemm_dispatch<1, 4, 2, 2>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);
     else if (p->bm == 64) gemm_dispatch<2, 2, 2, 4>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);
     else if (p->bm == 128) gemm_dispatch<2, 2, 4, 4>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);

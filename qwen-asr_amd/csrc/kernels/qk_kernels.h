@@ -220,13 +220,13 @@ int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride,
                             float eps, uint16_t *hi, uint16_t *lo, hipStream_t s);
 
 enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2 };
-/* Tiling of one M x N x K product: block rows bm (32 / 64 / 128, columns
- * QK_GEMM_BN), and nsplit slices of kc (a multiple of 64) along K so a launch
- * has about QK_GEMM_TARGET blocks. */
+/* Tiling of one M x N x K product: block rows bm x columns bn (32 / 64 / 128
+ * x QK_GEMM_BN, or 128 x 256 for large M), and nsplit slices of kc (a
+ * multiple of 64) along K so a launch has about QK_GEMM_TARGET blocks. */
 #define QK_GEMM_BN 128
 #define QK_GEMM_TARGET 256
 #define QK_GEMM_MAX_SPLIT 16
-typedef struct { int bm, nsplit, kc; } qk_gemm_plan;
+typedef struct { int bm, nsplit, kc, bn; } qk_gemm_plan;
 void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p);
 /* Y[M][N] (=, +=) (A_hi + A_lo)[M][K] . W[N][K]^T on bf16 MFMA with fp32
  * accumulation; SWIGLU writes silu(Y[:,2j]) * Y[:,2j+1] as a bf16 hi/lo

@@ -65,6 +65,62 @@ def test_gemm_hilo(P, qa, gpu, M, N, K):
     assert np.all(np.abs(y - yo) <= bound), float(np.max(np.abs(y - yo) / bound))
 
 
+class GemmPlan(C.Structure):
+    _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int)]
+
+
+# the three epilogues of the prefill GEMM on every tile shape it plans:
+# 256 x 256 and 128 x 256 (direct-to-LDS rings; M not a multiple of the tile,
+# k walks shorter than the ring), 64 x 128 and split 128 x 128 (STORE into
+# partials, summed by the reduce pass with the epilogue)
+@pytest.mark.parametrize("M,N,K,bm,bn", [(1000, 16384, 64, 256, 256), (4000, 4096, 96, 256, 256),
+                                         (4000, 2048, 96, 128, 256), (2000, 4096, 32, 128, 256),
+                                         (401, 6144, 1024, 64, 128), (1515, 1024, 512, 128, 128)])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_epilogues(P, qa, gpu, M, N, K, bm, bn, epi):
+    lib = qa.lib()
+    p = GemmPlan()
+    lib.qk_gemm_plan_for(M, N, K, C.byref(p))
+    assert (p.bm, p.bn) == (bm, bn), (p.bm, p.bn, p.nsplit)
+    W = P.synth_bf16(N * K, 2, 9400 + N).reshape(N, K)
+    x = P.synth_f32(M * K, 2, 9500 + M).reshape(M, K)
+    hi = P.f32_to_bf16(x)
+    lo = P.f32_to_bf16(x - P.bf16_to_f32(hi))
+    prod = (P.bf16_to_f32(hi).astype(np.float64) + P.bf16_to_f32(lo)) @ P.bf16_to_f32(W).astype(np.float64).T
+    absum = np.abs(x).astype(np.float64) @ np.abs(P.bf16_to_f32(W)).astype(np.float64).T
+    bound = 4 * K * 2.0 ** -24 * absum + 1e-12
+    y0 = P.synth_f32(M * N, 2, 9600 + M).reshape(M, N)
+    dh, dl, dW = dev(gpu, hi.view(np.int16)), dev(gpu, lo.view(np.int16)), dev(gpu, W.view(np.int16))
+    lib.qk_gemm_launch.argtypes = [C.c_void_p] * 3 + [C.c_int] * 3 + [C.c_void_p, C.c_int] + [C.c_void_p] * 4
+    lib.qk_gemm_reduce_launch.argtypes = [C.c_void_p] + [C.c_int] * 4 + [C.c_void_p] * 4
+    split = p.nsplit > 1
+    dy = dev(gpu, y0) if epi == 1 else gpu.zeros((M, N), dtype=gpu.float32, device="cuda")
+    oh = gpu.zeros((M, N // 2), dtype=gpu.int16, device="cuda")
+    ol = gpu.zeros((M, N // 2), dtype=gpu.int16, device="cuda")
+    outs = (None, ptr(oh), ptr(ol)) if epi == 2 else (ptr(dy), None, None)
+    if split:
+        part = gpu.empty((p.nsplit, M, N), dtype=gpu.float32, device="cuda")
+        qa.check(lib.qk_gemm_launch(ptr(dh), ptr(dl), ptr(dW), M, N, K, C.byref(p), 0, ptr(part), None, None,
+                                    None), "gemm")
+        qa.check(lib.qk_gemm_reduce_launch(ptr(part), p.nsplit, M, N, epi, *outs, None), "reduce")
+    else:
+        qa.check(lib.qk_gemm_launch(ptr(dh), ptr(dl), ptr(dW), M, N, K, C.byref(p), epi, *outs, None), "gemm")
+    gpu.cuda.synchronize()
+    if epi == 2:
+        g, u = prod[:, 0::2], prod[:, 1::2]
+        exp = g / (1.0 + np.exp(-g)) * u
+        got = P.bf16_to_f32(host(oh).view(np.uint16)).astype(np.float64) + P.bf16_to_f32(host(ol).view(np.uint16))
+        # product errors through silu(g) u (|d/dg| <= 1.1 |u|, |silu(g)| <= |g| + 0.3), plus
+        # the hi + lo carry of the result (~2^-17 relative)
+        tol = 1e-5 * np.abs(exp) + 1.2 * (np.abs(u) * bound[:, 0::2] + (np.abs(g) + 0.3) * bound[:, 1::2]) + 1e-9
+        assert np.all(np.abs(got - exp) <= tol), float(np.max(np.abs(got - exp) / tol))
+    else:
+        exp = prod + (y0 if epi == 1 else 0.0)
+        got = host(dy).astype(np.float64)
+        tol = bound + (2.0 ** -23 * np.abs(exp) if epi == 1 else 0.0)
+        assert np.all(np.abs(got - exp) <= tol), float(np.max(np.abs(got - exp) / tol))
+
+
 def test_elementwise_ops(P, qa, gpu):
     lib, orc = qa.lib(), P.orc_lib()
     r = np.random.default_rng(0)

@@ -1,5 +1,5 @@
 """Launch planners of the prefill kernels (host code, no GPU needed):
-qk_gemm_plan_for (row tile, split-K slices of the projection GEMMs) and
+qk_gemm_plan_for (tile shape, split-K slices of the projection GEMMs) and
 qk_attn_prefill_plan (key chunk per block of the prefill attention).  Their
 invariants are what the kernels rely on: slices cover K exactly once in whole
 64-deep k tiles, at most 16 of them (the partial-sum consumers' bound); key
@@ -12,7 +12,7 @@ import pytest
 
 
 class GemmPlan(C.Structure):
-    _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int)]
+    _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int)]
 
 
 SHAPES = [(M, N, K) for M in (1, 17, 31, 32, 33, 64, 65, 401, 512, 513, 1515, 8191)
@@ -23,11 +23,19 @@ SHAPES = [(M, N, K) for M in (1, 17, 31, 32, 33, 64, 65, 401, 512, 513, 1515, 81
 def test_gemm_plan_invariants(qa, M, N, K):
     p = GemmPlan()
     qa.lib().qk_gemm_plan_for(M, N, K, C.byref(p))
-    assert p.bm == (32 if M <= 32 else 64 if M <= 512 else 128)
+    def fills(bm):   # bm x 256 tiles alone fill the CUs, last round >= 85 % used
+        wt = -(-M // bm) * (N // 256)
+        return M > 512 and N % 256 == 0 and K % 32 == 0 and wt >= 256 and wt * 100 >= -(-wt // 256) * 256 * 85
+    if fills(256):                                                     # wide tiles, never split
+        assert (p.bm, p.bn, p.nsplit) == (256, 256, 1)
+    elif fills(128):
+        assert (p.bm, p.bn, p.nsplit) == (128, 256, 1)
+    else:
+        assert p.bn == 128 and p.bm == (32 if M <= 32 else 64 if M <= 512 else 128)
     assert p.kc > 0 and p.kc % 64 == 0
     assert 1 <= p.nsplit <= 16
     assert p.kc * p.nsplit >= K and p.kc * (p.nsplit - 1) < K       # every slice non-empty, K covered once
-    tiles = -(-M // p.bm) * -(-N // 128)
+    tiles = -(-M // p.bm) * -(-N // p.bn)
     if tiles >= 256:
         assert p.nsplit == 1                                           # the grid alone fills the chip
 
