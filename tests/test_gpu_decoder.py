@@ -118,6 +118,46 @@ def test_tiny_against_oracle_free_run(P, qa, tiny):
             break
 
 
+def test_long_prefill_wide_kernels(P, qa, gpu):
+    """A 4095-row prefill on the 0.6B layer shape (two layers, 4096-token
+    vocabulary): the plans pick the 256 x 256 QKV and 128 x 256 gate|up GEMMs
+    (direct-to-LDS rings, STORE into the RoPE/append consumer and the SwiGLU
+    epilogue) and unsplit causal attention (64 query tiles x 8 kv heads), so
+    the decoder's long-prefill path runs end to end; the next token's logits
+    and final hidden state are checked against the CPU oracle."""
+    import ctypes as C
+
+    class GemmPlan(C.Structure):
+        _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int)]
+
+    lib = qa.lib()
+    S = 4095
+    for (n, k), want in (((4096, 1024), (256, 256)), ((6144, 1024), (128, 256))):
+        p = GemmPlan()
+        lib.qk_gemm_plan_for(S, n, k, C.byref(p))
+        assert (p.bm, p.bn, p.nsplit) == want + (1,), (n, p.bm, p.bn, p.nsplit)
+    chunk, nsplit = C.c_int(), C.c_int()
+    lib.qk_attn_prefill_plan(S, S, 0, 16, 8, C.byref(chunk), C.byref(nsplit))
+    assert nsplit.value == 1
+    m = P.SynthModel(P.Config(1024, 2, 16, 8, 128, 3072, 4096), seed=3, norm_std=0.1)
+    rows, _ = P.prompt_rows(m, S - 5, 6, seed=3)
+    o = P.Oracle(m, threads=16)
+    o.prefill(rows[:-1])
+    to, lo, ho = o.forward(rows[-1], True, True)
+    d = make_decoder(qa, P, m, kv_capacity=S + 64)
+    d.set_keep_logits(True)
+    d.prefill(rows[:-1])
+    td = d.forward(rows[-1])
+    lg, hid = d.read_logits(), d.read_hidden()
+    print(f"4095-row prefill: max |dlogit| {np.abs(lg - lo).max():.2e}, max |dhidden| {np.abs(hid - ho).max():.2e}")
+    assert close(lg, lo)
+    np.testing.assert_allclose(hid, ho, atol=1e-3, rtol=1e-3)
+    if td != to:
+        s = np.sort(lo)
+        assert s[-1] - s[-2] < TIE
+    d.close()
+
+
 def test_tiny_long_context_crosses_step_variants(P, qa, tiny):
     """Decode attention switches from <= 8 splits merged in the O-projection
     (<= 2048 keys) to up to 32 splits + a merge kernel: logits on both sides
