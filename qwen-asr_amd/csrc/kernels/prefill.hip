@@ -342,7 +342,10 @@ __global__ __launch_bounds__(512, 1) void gemm_hilo_wide(const uint16_t *__restr
         if (later >= 2) __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * (2 * AI + 2)));
         else if (later == 1) __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * AI + 2));
         else __builtin_amdgcn_s_waitcnt(0x0f70);
-        __syncthreads();   // every wave's share of tile kt is in LDS; tile kt-1's stage is free
+        // every wave's share of tile kt is in LDS; tile kt-1's stage is free.  A
+        // plain s_barrier: __syncthreads() would also wait for this wave's later
+        // tiles still in flight (vmcnt(0)) and drain the ring every k tile
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (kt + NST - 1 < nk) issue(kt + NST - 1);
         const unsigned char *st = lds[kt % NST];
         bf16x8 bfr[TN];
