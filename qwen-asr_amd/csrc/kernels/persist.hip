@@ -628,8 +628,10 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
 // overlaps the hand-overs.  DEEP (0.6B) keeps two stages in flight:
 //   end of D(l-1): K/V(l)     end of A: gate|up(l)
 //   end of O: down(l), Q(l+1) end of F: O(l+1)
-// the 1.7B slabs are 4x larger, so it issues each one stage ahead:
-//   end of D(l-1): K/V(l), O(l)   end of O: gate|up(l)   end of F: down(l), Q(l+1)
+// the 1.7B slabs are 4x larger, so it issues each one stage ahead, between
+// the two barriers that open the stage before the one that uses it (its
+// stream then overlaps the sync wave's wait there, not the compute waves'):
+//   Q(l): K/V(l), O(l)   F(l): gate|up(l), used right after   D(l): down(l), Q(l+1)
 // ---------------------------------------------------------------------------
 template <int H, int I, int NCW>
 __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, PxKvLds<NCW> &kvb, int wave,
@@ -697,8 +699,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
     {
         const PxSplit sp(a.pos0, r);
         wq.load(Wq(0), H, wave, lane);
-        if (!DEEP) wo.load(Wo(0), PX_QD, wave, lane);
-        px_kv_dma<AB>(kvb[wave], Kc(0), Vc(0), gl, sp.s0 + gid, NG, sp.cend, sp.active);
+        if (DEEP) px_kv_dma<AB>(kvb[wave], Kc(0), Vc(0), gl, sp.s0 + gid, NG, sp.cend, sp.active);
     }
 
     for (int s = 0; s < a.n_steps; s++) {
@@ -717,6 +718,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
 
             // ---- Q: the group's Q|K|V rows (qwen_linear_nobias_bf16_qkv, qwen_asr_kernels.c:434-460) ----
             px_sync();
+            if (!DEEP) {   // streams while the sync wave waits for the residual
+                wo.load(Wo(l), PX_QD, wave, lane);
+                px_kv_dma<AB>(kvb[wave], Kc(l), Vc(l), gl, sp.s0 + gid, NG, sp.cend, sp.active);
+            }
             px_sync();
             if (S.abort_) return;
             {
@@ -923,11 +928,11 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     for (int i = 0; i < SO / 2 / NCW; i++) px_put_global(dst + SlabO::row(wave, i, lane), y[i], T + 2u);
                 }
             }
-            if (!DEEP) wf.load(Wf(l), H, wave, lane);
             mark(7);
 
             // ---- F: gate|up rows of the group + SwiGLU (qwen_asr_decoder.c:463-466) ----
             px_sync();
+            if (!DEEP) wf.load(Wf(l), H, wave, lane);
             px_sync();
             if (S.abort_) return;
             if (DEEP) wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
@@ -942,13 +947,13 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                         px_put_local(dst + SlabF::row(wave, i, 0) / 2, swiglu1(y[i], y[i + 1]), T + 4u);
                 }
             }
+
+            // ---- D: this block's rows of W_down over the group's columns (:467-468) ----
+            px_sync();
             if (!DEEP) {
                 wd.load(Wd(l), I, wave, lane);
                 wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
             }
-
-            // ---- D: this block's rows of W_down over the group's columns (:467-468) ----
-            px_sync();
             px_sync();
             if (S.abort_) return;
             {
@@ -964,8 +969,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             {   // the next layer's operands (after the last layer: layer 0 of the next step)
                 const int ln = l + 1 < L ? l + 1 : 0;
                 const PxSplit sn(l + 1 < L ? pos : pos + 1, r);
-                if (!DEEP) wo.load(Wo(ln), PX_QD, wave, lane);
-                px_kv_dma<AB>(kvb[wave], Kc(ln), Vc(ln), gl, sn.s0 + gid, NG, sn.cend, sn.active);
+                if (DEEP) px_kv_dma<AB>(kvb[wave], Kc(ln), Vc(ln), gl, sn.s0 + gid, NG, sn.cend, sn.active);
             }
         }
         // the first LM-head rows, issued before the final hand-over
