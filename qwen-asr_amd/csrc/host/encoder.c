@@ -257,9 +257,24 @@ int qwen_hip_encoder_load_stem(qwen_hip_encoder *e, const qwen_hip_enc_stem_weig
     QK_TRY(up(&e->c1w, c1, ENC_CH * ENC_K1));
     QK_TRY(up(&e->c1b, w->conv1_b, ENC_CH));
     const size_t k2 = (size_t)ENC_CH * ENC_K2, ko = d * ENC_CH * 16;
-    QK_TRY(up_mat(&e->c2w, k2, 0, w->conv2_w, k2, w->conv2_w && bf16_exact(w->conv2_w, k2)));
+    /* conv2 / conv3 [480][480][3][3]: columns reordered tap-major (k = tap *
+     * 480 + ic) to match the channel-last stem activations */
+    if (!w->conv2_w || !w->conv3_w) { qk_set_err("encoder weight pointer is NULL"); return QWEN_HIP_EINVAL; }
+    float *tm = (float *)malloc(k2 * sizeof(float));
+    if (!tm) { qk_set_err("out of host memory"); return QWEN_HIP_ENOMEM; }
+    const float *cw[2] = {w->conv2_w, w->conv3_w};
+    enc_mat *cm[2] = {&e->c2w, &e->c3w};
+    int rc = 0;
+    for (int i = 0; i < 2 && !rc; i++) {
+        for (size_t oc = 0; oc < ENC_CH; oc++)
+            for (size_t ic = 0; ic < ENC_CH; ic++)
+                for (size_t tap = 0; tap < 9; tap++)
+                    tm[oc * ENC_K2 + tap * ENC_CH + ic] = cw[i][oc * ENC_K2 + ic * 9 + tap];
+        rc = up_mat(cm[i], k2, 0, tm, k2, bf16_exact(tm, k2));
+    }
+    free(tm);
+    QK_TRY(rc);
     QK_TRY(up(&e->c2b, w->conv2_b, ENC_CH));
-    QK_TRY(up_mat(&e->c3w, k2, 0, w->conv3_w, k2, w->conv3_w && bf16_exact(w->conv3_w, k2)));
     QK_TRY(up(&e->c3b, w->conv3_b, ENC_CH));
     QK_TRY(up_mat(&e->cow, ko, 0, w->conv_out_w, ko, w->conv_out_w && bf16_exact(w->conv_out_w, ko)));
     QK_TRY(up(&e->lnpw, w->ln_post_w, d));
@@ -397,16 +412,24 @@ static int gemm_add_ln(qwen_hip_encoder *e, const float *A, int lda, const enc_m
     return qk_enc_gemm_launch(&g, e->stream);
 }
 
-/* one stem layer: im2col over every chunk, GEMM with bias + GELU, padding zeroed */
+/* one stem layer, channel-last output [chunk][h_out][w_out][480] = GEMM rows
+ * (position) x columns (output channel), bias + GELU, padding zeroed.  conv1
+ * (mel_frames > 0): im2col of the mel, fp32 product.  conv2 / conv3 (input
+ * channel-last): with bf16 weights the product reads the input as an
+ * implicit im2col, else through a channel-last im2col into e->cols. */
 static int stem_layer(qwen_hip_encoder *e, const float *in, int c_in, int chunks, int h_in, int w_in, int kpad,
                       int mel_frames, const float *w, const uint16_t *w16, const float *b, float *out,
                       int valid_last) {
     const int h_out = conv_out(h_in), w_out = conv_out(w_in);
-    const int N = chunks * h_out * w_out;
-    QK_TRY(qk_enc_im2col_launch(in, e->cols, c_in, chunks, h_in, w_in, h_out, w_out, kpad, mel_frames, e->stream));
-    qk_enc_gemm_args g = {.A = w, .B = e->cols, .C = out, .M = ENC_CH, .N = N, .K = kpad, .lda = kpad,
-                          .ldb = kpad, .ldc = N, .bias_m = b, .gelu = 1, .col_w = w_out, .col_h = h_out,
-                          .col_chunks = chunks, .col_valid = valid_last, .A16 = w16};
+    const int M = chunks * h_out * w_out;
+    const int implicit = mel_frames == 0 && w16;
+    if (!implicit)
+        QK_TRY(qk_enc_im2col_launch(in, e->cols, c_in, chunks, h_in, w_in, h_out, w_out, kpad, mel_frames,
+                                    e->stream));
+    qk_enc_gemm_args g = {.A = implicit ? in : e->cols, .B = w, .C = out, .M = M, .N = ENC_CH, .K = kpad,
+                          .lda = kpad, .ldb = kpad, .ldc = ENC_CH, .bias_n = b, .gelu = 1, .col_w = w_out,
+                          .col_h = h_out, .col_chunks = chunks, .col_valid = valid_last, .pad_rows = 1,
+                          .conv_c = implicit ? c_in : 0, .conv_in_h = h_in, .conv_in_w = w_in, .B16 = w16};
     return qk_enc_gemm_launch(&g, e->stream);
 }
 

@@ -9,12 +9,16 @@
 // and only the summation order differs.
 //
 //   enc_im2col   Conv2D(3x3, stride 2, pad 1) patches of all chunks at once:
-//                row n = (chunk, oh, ow), column k = (ic, ki, kj)
-//                (the reference's im2col, qwen_asr_kernels.c:566-590)
+//                row n = (chunk, oh, ow), column k = (ki, kj, ic) tap-major
+//                (the reference's im2col, qwen_asr_kernels.c:566-590, with
+//                the weight columns reordered to match); the stem
+//                activations are channel-last [chunk][h][w][480], and with
+//                bf16 weights conv2 / conv3 skip this pass: the GEMM reads
+//                the same patches straight from the activations
 //   enc_gemm     C[M][N] = A[M][K] . B[N][K]^T with the encoder epilogues:
 //                bias along M or N, GELU, residual add, positional table add,
-//                zeroing of the padded columns of a partial last chunk
-//   enc_stem_rows conv3 output [480][chunk][16][w] -> token rows [t][480*16]
+//                zeroing of the padded positions of a partial last chunk
+//   enc_stem_rows conv3 output [chunk][16][w][480] -> token rows [t][480*16]
 //                (qwen_asr_encoder.c:281-290)
 //   enc_layernorm  (x - mean) * inv_std * w + b, two-pass mean / variance
 //                (qwen_layer_norm, qwen_asr_kernels.c:640-748)
@@ -38,10 +42,10 @@ __device__ __forceinline__ float enc_gelu(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// im2col of one stem layer over every chunk.  in: [c_in][chunks][h_in][w_in]
-// (conv1: the mel [128][frames], chunk c covering frames [c*cw, c*cw + cw),
-// frames past `frames` read as 0).  cols: [chunks*h_out*w_out][kpad], the
-// columns past c_in*9 zero.
+// im2col of one stem layer over every chunk.  in: conv1 the mel [128][frames]
+// (chunk c covering frames [c*cw, c*cw + cw), frames past `frames` read as
+// 0); conv2 / conv3 channel-last [chunks][h_in][w_in][c_in].  cols:
+// [chunks*h_out*w_out][kpad], the columns past c_in*9 zero.
 // ---------------------------------------------------------------------------
 // conv1 (one input channel, the mel read in place): thread = (row, k), 256 / kpad
 // rows per block, 32-bit index math
@@ -62,32 +66,31 @@ __global__ __launch_bounds__(256) void enc_im2col_mel(const float *mel, float *c
     }
 }
 
-// conv2 / conv3: one block per column row n = (chunk, oh, ow), decoded once;
-// threads along k (consecutive taps of one input row are adjacent in memory),
-// 32-bit index math (k / 9 and k % 9 by a constant)
+// conv2 / conv3 on channel-last input [chunk][h_in][w_in][c_in]: one block
+// per row n = (chunk, oh, ow); k = tap * c_in + ic, so each tap is c_in
+// contiguous floats of one input pixel (float4 copies, both sides coalesced)
 __global__ __launch_bounds__(256) void enc_im2col(const float *in, float *cols, int c_in, int chunks, int rows,
                                                   int h_in, int w_in, int h_out, int w_out, int kpad) {
+    const int q4 = c_in / 4;
     for (int n = blockIdx.x; n < rows; n += gridDim.x) {
         const int ow = n % w_out, t = n / w_out, oh = t % h_out, c = t / h_out;
-        const int ih0 = 2 * oh - 1, iw0 = 2 * ow - 1;
-        const long plane = (long)chunks * h_in * w_in;
-        const float *src = in + (long)c * h_in * w_in;
         float *dst = cols + (long)n * kpad;
-        for (int k = threadIdx.x; k < kpad; k += 256) {
-            float v = 0.0f;
-            if (k < c_in * 9) {
-                const int ic = k / 9, tap = k - 9 * ic;
-                const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
-                if (ih >= 0 && ih < h_in && iw >= 0 && iw < w_in) v = src[ic * plane + ih * w_in + iw];
-            }
-            dst[k] = v;
+        for (int i = threadIdx.x; i < 9 * q4; i += 256) {
+            const int tap = i / q4, q = i - tap * q4;
+            const int ih = 2 * oh - 1 + tap / 3, iw = 2 * ow - 1 + tap % 3;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (ih >= 0 && ih < h_in && iw >= 0 && iw < w_in)
+                v = *reinterpret_cast<const float4 *>(in + (((long)c * h_in + ih) * w_in + iw) * c_in + 4 * q);
+            *reinterpret_cast<float4 *>(dst + tap * c_in + 4 * q) = v;
         }
+        for (int k = 9 * c_in + threadIdx.x; k < kpad; k += 256) dst[k] = 0.0f;
     }
 }
 
 extern "C" int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int chunks, int h_in, int w_in,
                                     int h_out, int w_out, int kpad, int mel_frames, hipStream_t s) {
     if (!in || !cols || c_in <= 0 || chunks <= 0 || kpad < c_in * 9 || (kpad & 15)) return QWEN_HIP_EINVAL;
+    if (mel_frames <= 0 && (c_in & 3)) return QWEN_HIP_EINVAL;
     const long rows = (long)chunks * h_out * w_out;
     if (rows > 0x7fffffffL) return QWEN_HIP_EINVAL;
     if (mel_frames > 0) {
@@ -119,9 +122,11 @@ __device__ __forceinline__ void enc_epilogue(const qk_enc_gemm_args &a, int m, i
     if (a.pe) v += a.pe[(long)(m % a.pe_rows) * a.N + n];
     if (a.gelu) v = enc_gelu(v);
     if (a.col_w > 0) {
-        // stem output column n = (chunk, oh, ow): the last chunk's columns past its
-        // valid width are the zero padding the reference's next convolution sees
-        const int ow = n % a.col_w, c = n / (a.col_w * a.col_h);
+        // stem output position (chunk, oh, ow) (column n, or row m when
+        // pad_rows): the last chunk's positions past its valid width are the
+        // zero padding the reference's next convolution sees
+        const int p = a.pad_rows ? m : n;
+        const int ow = p % a.col_w, c = p / (a.col_w * a.col_h);
         if (c == a.col_chunks - 1 && ow >= a.col_valid) v = 0.0f;
     }
     if (a.add) v += *y;                    // residual (qwen_add_inplace after the projection)
@@ -240,12 +245,39 @@ __global__ __launch_bounds__(256) void enc_gemm_hl(qk_enc_gemm_args a) {
 
     float4 rx[XPT];
     uint4 rw[WPT];
-    auto gload = [&](int k0) {
+    // implicit im2col (A side only): this thread's rows as (input plane base,
+    // top-left input row / column of the 3x3 window); -1 marks rows past M
+    const bool conv = !WA && a.conv_c > 0;
+    int cb[XPT], ci[XPT], cj[XPT];
+    if (conv) {
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
-            const int g = xr0 + xr + 32 * i, gk = k0 + xk;
-            rx[i] = (g < xrn && gk < a.K) ? *reinterpret_cast<const float4 *>(X + (long)g * ldx + gk)
-                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int g = xr0 + xr + 32 * i;
+            const int ow = g % a.col_w, t = g / a.col_w, oh = t % a.col_h, c = t / a.col_h;
+            cb[i] = g < xrn ? c * a.conv_in_h * a.conv_in_w : -1;
+            ci[i] = 2 * oh - 1;
+            cj[i] = 2 * ow - 1;
+        }
+    }
+    auto gload = [&](int k0) {
+        if (conv) {
+            // a 32-wide k tile lies in one tap: channels ic .. ic + 3 of one input pixel
+            const int tap = k0 / a.conv_c, ic = k0 - tap * a.conv_c + xk;
+            const int dy = tap / 3, dx = tap - 3 * dy;
+#pragma unroll
+            for (int i = 0; i < XPT; i++) {
+                const int ih = ci[i] + dy, iw = cj[i] + dx;
+                const bool ok = cb[i] >= 0 && ih >= 0 && ih < a.conv_in_h && iw >= 0 && iw < a.conv_in_w;
+                rx[i] = ok ? *reinterpret_cast<const float4 *>(X + ((long)cb[i] + ih * a.conv_in_w + iw) * a.conv_c + ic)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < XPT; i++) {
+                const int g = xr0 + xr + 32 * i, gk = k0 + xk;
+                rx[i] = (g < xrn && gk < a.K) ? *reinterpret_cast<const float4 *>(X + (long)g * ldx + gk)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
 #pragma unroll
         for (int i = 0; i < WPT; i++) {
@@ -387,6 +419,9 @@ extern "C" int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s) {
         (a->lda & 3) || (a->ldb & 3) || a->lda < a->K || a->ldb < a->K || a->ldc < a->N || (a->pe && a->pe_rows <= 0))
         return QWEN_HIP_EINVAL;
     if (hl && ((a->K % EH_K) || (a->A16 ? (a->lda & 7) || !a->B : (a->ldb & 7) || !a->A))) return QWEN_HIP_EINVAL;
+    if (a->conv_c > 0 && (!a->B16 || a->conv_c % EH_K || a->K != 9 * a->conv_c || a->col_w <= 0 || a->col_h <= 0 ||
+                          a->conv_in_h <= 0 || a->conv_in_w <= 0 || !a->pad_rows))
+        return QWEN_HIP_EINVAL;
     if (a->ln_out && (!a->ln_w || !a->ln_b)) return QWEN_HIP_EINVAL;
     const int kstep = hl ? EH_K : EG_K;
     qk_enc_gemm_args g = *a;
@@ -442,7 +477,7 @@ __global__ __launch_bounds__(256) void enc_stem_rows(const float *c3, float *row
         const int tok = (int)(e / D), col = (int)(e % D);
         const int ch = col / h, f = col % h;
         const int c = tok / w, t = tok % w;
-        rows[e] = c3[(((long)ch * chunks + c) * h + f) * w + t];
+        rows[e] = c3[(((long)c * h + f) * w + t) * ch_n + ch];   // c3 channel-last [chunk][h][w][ch]
     }
 }
 

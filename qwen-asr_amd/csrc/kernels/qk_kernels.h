@@ -241,8 +241,13 @@ int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, fl
 /* ---- audio encoder (fp32 matrix cores) --------------------------------- */
 /* C[M][N] (=, +=) A[M][K] . B[N][K]^T (+ bias_m[m] | bias_n[n]) (+ pe[m % pe_rows][n])
  * (GELU); K and the leading dimensions multiples of 4.  col_w > 0: stem
- * output, column n = (chunk, oh, ow) with col_h x col_w per chunk; the last
- * chunk's columns with ow >= col_valid are written as 0.  ws: optional
+ * output, column n (row m when pad_rows) = (chunk, oh, ow) with col_h x col_w
+ * per chunk; the last chunk's positions with ow >= col_valid are written as
+ * 0.  conv_c > 0 (with B16 only): A is read as the implicit im2col of a 3x3,
+ * stride 2, pad 1 convolution over channel-last activations
+ * [chunk][conv_in_h][conv_in_w][conv_c]: row m = (chunk, oh, ow) of
+ * col_h x col_w per chunk, column k = tap * conv_c + ic, 0 outside the
+ * input; K = 9 conv_c, conv_c a multiple of 32, lda unused.  ws: optional
  * workspace of ws_elems floats; when the tile grid is too small to fill the
  * chip, K is split over up to 8 slices whose raw partials go to ws and are
  * summed in slice order by a second kernel that applies the epilogue
@@ -253,7 +258,8 @@ typedef struct {
     int M, N, K, lda, ldb, ldc;
     const float *bias_m, *bias_n, *pe;
     int pe_rows, gelu, add;
-    int col_w, col_h, col_chunks, col_valid;
+    int col_w, col_h, col_chunks, col_valid, pad_rows;
+    int conv_c, conv_in_h, conv_in_w;
     float *ws;
     long ws_elems;
     int kc, split;
