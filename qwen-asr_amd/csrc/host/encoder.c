@@ -414,7 +414,7 @@ static int gemm_add_ln(qwen_hip_encoder *e, const float *A, int lda, const enc_m
 
 /* one stem layer, channel-last output [chunk][h_out][w_out][480] = GEMM rows
  * (position) x columns (output channel), bias + GELU, padding zeroed.  conv1
- * (mel_frames > 0): im2col of the mel, fp32 product.  conv2 / conv3 (input
+ * (mel_frames > 0): im2col of the mel, then a direct 9-tap pass.  conv2 / conv3 (input
  * channel-last): with bf16 weights the product reads the input as an
  * implicit im2col, else through a channel-last im2col into e->cols. */
 static int stem_layer(qwen_hip_encoder *e, const float *in, int c_in, int chunks, int h_in, int w_in, int kpad,
@@ -426,6 +426,8 @@ static int stem_layer(qwen_hip_encoder *e, const float *in, int c_in, int chunks
     if (!implicit)
         QK_TRY(qk_enc_im2col_launch(in, e->cols, c_in, chunks, h_in, w_in, h_out, w_out, kpad, mel_frames,
                                     e->stream));
+    if (mel_frames > 0)   /* conv1: 9 taps per output, a direct pass */
+        return qk_enc_conv1_launch(e->cols, kpad, w, b, out, M, ENC_CH, h_out, w_out, chunks, valid_last, e->stream);
     qk_enc_gemm_args g = {.A = implicit ? in : e->cols, .B = w, .C = out, .M = M, .N = ENC_CH, .K = kpad,
                           .lda = kpad, .ldb = kpad, .ldc = ENC_CH, .bias_n = b, .gelu = 1, .col_w = w_out,
                           .col_h = h_out, .col_chunks = chunks, .col_valid = valid_last, .pad_rows = 1,

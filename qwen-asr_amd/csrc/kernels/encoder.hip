@@ -481,6 +481,60 @@ __global__ __launch_bounds__(256) void enc_stem_rows(const float *c3, float *row
     }
 }
 
+// conv1 directly from its patches (one input channel, 9 taps in cols[pos][kpad]):
+// out[pos][ch] = GELU(b[ch] + sum_tap cols[pos][tap] w[ch][tap]) for 4
+// channels per thread, float4 stores, so each position's 480 outputs are one
+// contiguous run (the product is 9 multiply-adds per output: the pass is
+// bound by the 4 bytes it writes per output).  Positions (chunk, oh, ow) of
+// the last chunk with ow >= valid are the zero padding the next layer sees.
+__global__ __launch_bounds__(256) void enc_conv1(const float *cols, int kpad, const float *w, const float *b, float *out,
+                                                 int rows, int ch, int h_out, int w_out, int chunks, int valid) {
+    // the grid stride is a multiple of ch / 4, so a thread keeps one channel
+    // quad (its 36 weights and 4 biases in registers) for every position it visits
+    const int q4 = ch / 4;
+    const long i0 = blockIdx.x * 256L + threadIdx.x, stride = (long)gridDim.x * 256;
+    const int c0 = 4 * (int)(i0 % q4);
+    float wr[4][9], br[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        br[j] = b[c0 + j];
+#pragma unroll
+        for (int t = 0; t < 9; t++) wr[j][t] = w[(c0 + j) * kpad + t];
+    }
+    for (long i = i0; i < (long)rows * q4; i += stride) {
+        const int pos = (int)(i / q4);
+        const int ow = pos % w_out, cc = pos / (w_out * h_out);
+        const float *x = cols + (long)pos * kpad;
+        float v[4] = {br[0], br[1], br[2], br[3]};
+#pragma unroll
+        for (int t = 0; t < 9; t++) {
+            const float xt = x[t];
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = fmaf(xt, wr[j][t], v[j]);
+        }
+        const bool pad = cc == chunks - 1 && ow >= valid;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = pad ? 0.0f : enc_gelu(v[j]);
+        *reinterpret_cast<float4 *>(out + (long)pos * ch + c0) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+extern "C" int qk_enc_conv1_launch(const float *cols, int kpad, const float *w, const float *b, float *out, int rows,
+                                   int ch, int h_out, int w_out, int chunks, int valid, hipStream_t s) {
+    if (!cols || !w || !b || !out || rows <= 0 || (ch & 3) || kpad < 9 || h_out <= 0 || w_out <= 0 || chunks <= 0)
+        return QWEN_HIP_EINVAL;
+    // blocks: a multiple of q4 / gcd(q4, 256) so the grid stride is a multiple of q4
+    const int q4 = ch / 4;
+    int g = q4, t = 256;
+    while (t) { const int r = g % t; g = t; t = r; }
+    const long unit = q4 / g;
+    long blocks = ((long)rows * q4 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    blocks = (blocks + unit - 1) / unit * unit;
+    enc_conv1<<<(int)blocks, 256, 0, s>>>(cols, kpad, w, b, out, rows, ch, h_out, w_out, chunks, valid);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+}
+
 extern "C" int qk_enc_stem_rows_launch(const float *c3, float *rows, int chunks, int w, int h, int ch_n, int tokens,
                                        hipStream_t s) {
     if (!c3 || !rows || tokens <= 0 || tokens > chunks * w) return QWEN_HIP_EINVAL;

@@ -280,6 +280,11 @@ typedef struct {
 int qk_enc_gemm_launch(const qk_enc_gemm_args *a, hipStream_t s);
 int qk_enc_im2col_launch(const float *in, float *cols, int c_in, int chunks, int h_in, int w_in, int h_out,
                          int w_out, int kpad, int mel_frames, hipStream_t s);
+/* conv1 from its im2col patches cols[rows][kpad] (taps 0..8) and weights
+ * w[ch][kpad]: channel-last out[rows][ch] with bias, GELU and the last
+ * chunk's padding positions zeroed */
+int qk_enc_conv1_launch(const float *cols, int kpad, const float *w, const float *b, float *out, int rows, int ch,
+                        int h_out, int w_out, int chunks, int valid, hipStream_t s);
 int qk_enc_stem_rows_launch(const float *c3, float *rows, int chunks, int w, int h, int ch_n, int tokens,
                             hipStream_t s);
 int qk_enc_layernorm_launch(const float *x, const float *w, const float *b, float *out, int rows, int D, float eps,
