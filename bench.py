@@ -261,6 +261,24 @@ ENC_FRAMES, ENC_CPU_FRAMES = 3000, 200
 BF16_MFMA_PEAK_TFS = 2500.0        # dense bf16 matrix-core peak (the encoder's GEMMs and attention run there)
 
 
+def prefill_rates(cfg, rows, seconds):
+    """Whole-prefill arithmetic rate from the timed median: the reference's
+    fp32 work (projections 2 * weights-per-layer * layers flop per row, causal
+    attention 4 * hd * heads * layers * sum(pos + 1)) and the bf16 MFMA work
+    the kernels execute for it (two products per projection term: hi and lo
+    activation halves; three per attention term), against the dense bf16
+    peak.  Includes everything in the prefill (norms, RoPE, launches)."""
+    hd, H, I, L = cfg.head_dim, cfg.hidden, cfg.intermediate, cfg.layers
+    per_layer_w = H * (cfg.heads * hd + 2 * cfg.kv_heads * hd) + cfg.heads * hd * H + 3 * H * I
+    proj = 2.0 * per_layer_w * L * rows
+    attn = 4.0 * hd * cfg.heads * L * rows * (rows + 1) / 2
+    mfma = 2.0 * proj + 3.0 * attn
+    return {"rows": rows, "ms": round(seconds * 1e3, 3), "fp32_equiv_tflops": round((proj + attn) / seconds / 1e12, 2),
+            "mfma_tflops": round(mfma / seconds / 1e12, 2),
+            "mfma_frac": round(mfma / seconds / 1e12 / BF16_MFMA_PEAK_TFS, 4),
+            "note": "whole prefill (projections x2 hi/lo and attention x3 bf16 MFMA work) over the median wall time"}
+
+
 def enc_flops(c, frames):
     """Algorithmic flops of one encoder forward (2 per multiply-add): conv
     stem as GEMMs (conv1 K = 9), conv_out, per layer the Q/K/V/O, FFN and
@@ -549,6 +567,7 @@ def main():
                    "prefill_rows": n_rows - 1, "decode_positions": [base, base + K - 1],
                    "engine": {0: "graph", 1: "eager", 2: "persistent"}.get(d.engine(), d.engine())},
         "prefill_tok_s": round((n_rows - 1) / prefill_s, 2),
+        "prefill": prefill_rates(cfg, n_rows - 1, prefill_s),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      **launch_fields(d.engine(), K, step_bytes, gpu_ms)},
