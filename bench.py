@@ -418,8 +418,8 @@ def main():
                          "known-size kernel that calibrates rocprofv3 read/write byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (one decoder context per GPU; "
-              "see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (independent utterances would run "
+              "one decoder context per GPU with no exchange). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
