@@ -78,10 +78,24 @@ def pmc_pass(counter, workload, timeout=150):
            sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--steps", str(PMC_STEPS),
            "--warmup", "2", "--calib-copy-mb", "256", "--workload", workload]
     env = dict(os.environ, TMPDIR="/tmp")
+    errlog = os.path.join(out, "child.err")
     try:
-        subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
-                       timeout=timeout, check=False)
+        with open(errlog, "w") as ef:
+            # own process group, so a time-out ends the profiler and the program under it
+            p = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=ef,
+                                 start_new_session=True)
+            try:
+                rc = p.wait(timeout=timeout)
+            except subprocess.TimeoutExpired:
+                os.killpg(p.pid, 9)
+                p.wait()
+                rc = "timeout"
         files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+        if rc != 0 or not files:
+            tail = open(errlog, errors="replace").read().splitlines()[-6:]
+            log(f"[gpu] rocprofv3 --pmc {counter} pass: exit {rc}, {len(files)} counter files; stderr tail:")
+            for line in tail:
+                log("    " + line)
         if not files:
             return None
         per_dispatch, names, cal = {}, {}, None
@@ -393,7 +407,7 @@ def launch_fields(engine, K, step_bytes, gpu_ms):
     K timed steps in one px_decode dispatch; the graph engine replays one graph
     (per-layer GEMV/attention kernels + LM head argmax) per step."""
     if engine == 2:
-        return {"kernel": f"px_decode (persistent cooperative kernel: {K} greedy decode steps per launch)",
+        return {"kernel": f"px_decode (persistent kernel, one block per CU: {K} greedy decode steps per launch)",
                 "steps_per_launch": K, "bytes_per_launch": round(sum(step_bytes)),
                 "launch_us": round(gpu_ms * 1e3, 3), "step_us": round(gpu_ms * 1e3 / K, 3)}
     return {"kernel": "decode step graph (one token: all layers + LM head argmax)", "steps_per_launch": 1,
@@ -459,6 +473,7 @@ def main():
         d = qa.Decoder(cfg, 0, C5_CAP + 64)
         if args.engine is not None:
             d.set_engine(args.engine)
+        d.set_fallback(False)      # a failed persistent launch fails the run instead of being redone
         d.load_synthetic(0, 0.02, 0.0)
         run_streaming(qa, d, cfg, 2)                      # warm-up
         toks, times = run_streaming(qa, d, cfg, C5_CHUNKS)
@@ -474,12 +489,14 @@ def main():
             "config": {"workload": wl["desc"], "engine": {0: "graph", 1: "eager", 2: "persistent"}.get(d.engine())},
             "chunk_ms": {"mean": round(total / C5_CHUNKS * 1e3, 4), "max": round(max(times) * 1e3, 4)},
             "tokens_head": [int(t) for t in toks[0][:8]]}), flush=True)
+        d.close()
         return
     n_rows = wl["n_audio"] + wl["n_ids"]
     K, W = args.steps or wl.get("steps", 128), args.warmup
     d = qa.Decoder(cfg, 0, n_rows + K + W + 1024)
     if args.engine is not None:
         d.set_engine(args.engine)
+    d.set_fallback(False)          # a failed persistent launch fails the run instead of being redone
     t0 = time.time()
     d.load_synthetic(0, 0.02, 0.0)
     rows, ids, emb = qa.prompt_rows(cfg, wl["n_audio"], wl["n_ids"])
@@ -531,14 +548,7 @@ def main():
 
     traffic = None
     traffic_note = None
-    if d.engine() == 2 and not args.no_traffic:
-        # rocprofv3 --pmc (dispatch counter collection) did not complete on the
-        # cooperative launch of px_decode within 150 s; not run on it again.
-        traffic_note = ("null: rocprofv3 --pmc counter collection does not complete on the cooperative px_decode "
-                        "launch; per-kernel HBM traffic of the same step is measured on the graph engine "
-                        "(bench.py --engine 0)")
-        log("[gpu] traffic passes skipped for the persistent engine (counter collection on a cooperative launch)")
-    elif not args.no_traffic:
+    if not args.no_traffic:
         fr = pmc_pass("FETCH_SIZE", args.workload)
         wr = pmc_pass("WRITE_SIZE", args.workload)
         if fr and wr:
@@ -574,6 +584,7 @@ def main():
         "cpu_baseline": cpu,
         "tokens_head": [int(first)] + [int(t) for t in toks[:7]],
     }
+    d.close()
     print(json.dumps(out), flush=True)
 
 

@@ -154,14 +154,24 @@ int qwen_hip_decoder_read_logits(qwen_hip_decoder *dec, float *out);
 
 /* Decode engine: 0 = one kernel per fused op, replayed from a HIP graph;
  * 1 = the same kernels launched eagerly (no graph); 2 = the whole greedy loop
- * of a forward/generate call in one persistent cooperative kernel (default
+ * of a forward/generate call in one persistent kernel, one block per CU (default
  * where supported: 16 query / 8 kv heads, the 0.6B or 1.7B shape, 256 CUs in
  * 8 XCDs).  set_engine(2) returns QWEN_HIP_EINVAL where it is not supported.
- * If a persistent run fails it reports on stderr, switches the decoder to
- * engine 0 and redoes the steps there.  No reference counterpart: the
- * reference has one CPU path (qwen_asr_kernels.c). */
+ * Every wait inside the persistent kernel is bounded (set_wait_limit, default
+ * 1 s of the device wall clock); a run that times out or finds its grid not
+ * laid out one block per CU raises an error bit, and all its blocks leave.
+ * With fallback on (set_fallback, the default) the decoder then reports on
+ * stderr, counts the event (fallbacks), switches to engine 0 and redoes the
+ * steps there; with fallback off the call returns QWEN_HIP_EDEVICE (forward:
+ * the failure token) and the decoder is left as before the call.  No
+ * reference counterpart: the reference has one CPU path (qwen_asr_kernels.c). */
 int qwen_hip_decoder_set_engine(qwen_hip_decoder *dec, int engine);
 int qwen_hip_decoder_engine(const qwen_hip_decoder *dec);
+int qwen_hip_decoder_set_fallback(qwen_hip_decoder *dec, int on);
+int qwen_hip_decoder_fallbacks(const qwen_hip_decoder *dec);
+/* seconds in [0, 60]; 0 makes every wait that is not satisfied by its first
+ * poll give up (a test of the give-up path) */
+int qwen_hip_decoder_set_wait_limit(qwen_hip_decoder *dec, double seconds);
 
 /* Diagnostics of the persistent engine (no reference counterpart; the
  * reference only times whole phases with gettimeofday, qwen_asr.c:362-366).

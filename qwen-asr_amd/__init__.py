@@ -64,6 +64,9 @@ SIGNATURES = [
     ("qwen_hip_decoder_read_logits", _i, [_vp, _vp]),
     ("qwen_hip_decoder_set_engine", _i, [_vp, _i]),
     ("qwen_hip_decoder_engine", _i, [_vp]),
+    ("qwen_hip_decoder_set_fallback", _i, [_vp, _i]),
+    ("qwen_hip_decoder_fallbacks", _i, [_vp]),
+    ("qwen_hip_decoder_set_wait_limit", _i, [_vp, _d]),
     ("qwen_hip_decoder_set_trace", _i, [_vp, _i]),
     ("qwen_hip_decoder_read_trace", _i, [_vp, _vp, C.c_size_t]),
     ("qwen_hip_decoder_stream", _vp, [_vp]),
@@ -467,6 +470,18 @@ class Decoder:
     def engine(self):
         """Active decode engine: 0 graph, 1 eager, 2 persistent."""
         return lib().qwen_hip_decoder_engine(self.h)
+
+    def set_fallback(self, on):
+        """on: a failed persistent launch is redone by the graph engine (and counted);
+        off: the call fails with QWEN_HIP_EDEVICE."""
+        check(lib().qwen_hip_decoder_set_fallback(self.h, 1 if on else 0), "set_fallback")
+
+    def fallbacks(self):
+        """How many persistent launches failed and were redone by the graph engine."""
+        return check(lib().qwen_hip_decoder_fallbacks(self.h), "fallbacks")
+
+    def set_wait_limit(self, seconds):
+        check(lib().qwen_hip_decoder_set_wait_limit(self.h, float(seconds)), "set_wait_limit")
 
     def set_trace(self, step):
         check(lib().qwen_hip_decoder_set_trace(self.h, int(step)), "set_trace")

@@ -119,6 +119,10 @@ struct qwen_hip_decoder {
     unsigned px_epoch;
     unsigned long long *px_trace;   /* [256][QK_PX_TRACE] when tracing */
     int px_trace_step;              /* < 0: off */
+    unsigned long long px_wait_ticks; /* bound of every in-kernel wait (device wall-clock ticks) */
+    double px_ticks_per_s;
+    int px_fallback;                /* 1: a failed persistent launch is redone by the graph engine */
+    int px_fallbacks;               /* number of such fallbacks */
 };
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -271,6 +275,12 @@ static int px_alloc(qwen_hip_decoder *d) {
     QK_HIP(hipMemset(d->px_ctl, 0, 64 * sizeof(unsigned)));
     d->px_epoch = 1;
     d->px_trace_step = -1;
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->device) != hipSuccess || khz <= 0)
+        khz = 100000;                              /* the MI355X constant-rate clock: 100 MHz */
+    d->px_ticks_per_s = (double)khz * 1e3;
+    d->px_wait_ticks = (unsigned long long)d->px_ticks_per_s;   /* one second */
+    d->px_fallback = 1;
     return 0;
 }
 
@@ -711,7 +721,7 @@ static int log_reserve(qwen_hip_decoder *d, int n) {
     return 0;
 }
 
-/* The persistent engine: n steps from position kv_len in one cooperative
+/* The persistent engine: n steps from position kv_len in one persistent
  * launch; the first input is emb[first_tok] or, for first_tok < 0, the row
  * staged in d->x.  Synchronises and checks the kernel's error bits. */
 static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
@@ -733,6 +743,7 @@ static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
         .layers = c->layers, .vocab = c->vocab, .eps = c->rms_eps, .scale = d->scale,
         .xq = d->xq, .xa = d->xa, .xo = d->xo, .xla = d->xla, .xh = d->xh, .xd = d->xd, .xlb = d->xlb,
         .xc = d->xc, .xv = d->xv, .cnt = d->px_ctl, .err = d->px_ctl + 16, .epoch = d->px_epoch,
+        .wait_ticks = d->px_wait_ticks,
         .pos0 = d->kv_len, .n_steps = n, .first_tok = first_tok, .x_in = d->x, .log = d->d_log,
         .tok_out = d->d_tok, .pos_out = d->d_pos, .hidden_out = d->hidden,
         .logits = d->keep_logits ? d->logits : NULL,
@@ -751,16 +762,26 @@ static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
 
 /* Run n steps from position kv_len; first_tok as for px_run.  Tokens land in
  * d_log[0, n), the last one also in the control block.  Does not advance
- * kv_len.  If the persistent engine fails it is switched off for this decoder
- * and the steps are redone by the graph engine (they rewrite the same K/V
- * positions, so a partial run leaves nothing behind). */
+ * kv_len.  If a persistent launch fails (a wait timed out, the grid was not
+ * laid out one block per CU): with fallback on (the default) the decoder
+ * switches to the graph engine, counts the fallback (qwen_hip_decoder_fallbacks)
+ * and redoes the steps there (they rewrite the same K/V positions, so a
+ * partial run leaves nothing behind); with fallback off the call fails with
+ * QWEN_HIP_EDEVICE and the decoder state is as before the call. */
 static int steps_run(qwen_hip_decoder *d, int first_tok, int n) {
     if (d->engine == ENGINE_PERSIST) {
-        if (px_run(d, first_tok, n) == 0) return 0;
-        fprintf(stderr, "qwen_asr_hip: %s; using the graph engine\n", qwen_hip_last_error());
-        d->px_ok = 0;
-        d->engine = ENGINE_GRAPH;
+        int rc = px_run(d, first_tok, n);
+        if (rc == 0) return 0;
+        char msg[512];
+        snprintf(msg, sizeof msg, "%s", qwen_hip_last_error());
         QK_TRY(set_dev_pos(d));       /* the failed run may have advanced it */
+        if (!d->px_fallback) {
+            qk_set_err("%s", msg);
+            return rc;
+        }
+        fprintf(stderr, "qwen_asr_hip: %s; using the graph engine\n", msg);
+        d->px_fallbacks++;
+        d->engine = ENGINE_GRAPH;
     }
     d->h_int[0] = first_tok;
     d->h_int[2] = 0;
@@ -815,7 +836,8 @@ int qwen_hip_decoder_generate(qwen_hip_decoder *d, int first, int n, int *out, i
     if (n == 0) return 0;
     QK_TRY(forward_prepare(d, n));
     const int start = d->kv_len;
-    QK_TRY(steps_run(d, first, n));
+    int rc = steps_run(d, first, n);   /* keeps its own error message */
+    if (rc) return rc;
     QK_HIP(hipMemcpyAsync(out, d->d_log, (size_t)n * 4, hipMemcpyDeviceToHost, d->stream));
     QK_HIP(hipStreamSynchronize(d->stream));
     int kept = n;
@@ -856,6 +878,21 @@ int qwen_hip_decoder_set_engine(qwen_hip_decoder *d, int engine) {
 }
 
 int qwen_hip_decoder_engine(const qwen_hip_decoder *d) { return d ? d->engine : QWEN_HIP_EINVAL; }
+
+int qwen_hip_decoder_set_fallback(qwen_hip_decoder *d, int on) {
+    if (!d) return QWEN_HIP_EINVAL;
+    d->px_fallback = on != 0;
+    return 0;
+}
+
+int qwen_hip_decoder_fallbacks(const qwen_hip_decoder *d) { return d ? d->px_fallbacks : QWEN_HIP_EINVAL; }
+
+int qwen_hip_decoder_set_wait_limit(qwen_hip_decoder *d, double seconds) {
+    if (!d || !(seconds >= 0.0) || seconds > 60.0) { qk_set_err("set_wait_limit: seconds outside [0, 60]"); return QWEN_HIP_EINVAL; }
+    if (!d->px_ok) { qk_set_err("set_wait_limit: the persistent engine is not available"); return QWEN_HIP_ESTATE; }
+    d->px_wait_ticks = (unsigned long long)(seconds * d->px_ticks_per_s);
+    return 0;
+}
 
 int qwen_hip_decoder_set_trace(qwen_hip_decoder *d, int step) {
     if (!d) return QWEN_HIP_EINVAL;

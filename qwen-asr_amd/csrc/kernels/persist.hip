@@ -36,6 +36,16 @@
 // polls, so outstanding weight prefetches of the compute waves never hold up
 // a poll (loads retire in order per wave).  Both roles walk the same barrier
 // sequence; the block barrier does not wait on global loads.
+//
+// Every wait is bounded in wall-clock time: a poll that has not seen its words
+// after a.wait_ticks ticks of the constant-rate clock (the host passes about
+// one second) raises QK_PX_ERR_TIMEOUT, and every poll also gives up once
+// another block raised an error, so all waves of the grid reach the end of the
+// kernel whatever happens to the others (a block that is never scheduled, a
+// producer that faulted).  The kernel is launched as an ordinary grid of one
+// block per CU (each block's LDS does not leave room for a second one); the
+// launch check-in verifies that every block is resident and that each XCD holds
+// exactly 32 of them before any work starts.
 #include "common.h"
 #include "qk_kernels.h"
 #include "qwen_asr_hip.h"
@@ -44,7 +54,6 @@
 
 typedef unsigned long long u64;
 
-#define PX_SPIN_LIMIT (1u << 22)
 #define PX_QD 2048                 // 16 query heads x 128
 #define PX_KVD 1024                // 8 kv heads x 128
 
@@ -89,10 +98,14 @@ __device__ __forceinline__ float4 px_ldf4(const void *base, unsigned off) {
 __device__ __forceinline__ void px_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Sync wave: wait until the n words at addr(i), i < n, carry `tag`, then
-// dst[i] = value.  PER words per lane in flight per pass.  False on timeout or
-// when another block raised an error.
+// dst[i] = value.  PER words per lane in flight per pass.  False when the wait
+// passed a.wait_ticks (QK_PX_ERR_TIMEOUT raised) or another block raised an
+// error.  The clock is read while the pass's loads are in flight, so the
+// bound costs no extra round trip.
 template <int PER, typename Addr>
-__device__ bool px_poll(Addr addr, int n, unsigned tag, float *dst, unsigned *err, int lane, float *ssq = nullptr) {
+__device__ bool px_poll(const qk_persist_args &a, Addr addr, int n, unsigned tag, float *dst, int lane,
+                        float *ssq = nullptr) {
+    const u64 t0 = wall_clock64();
     for (int base = 0; base < n; base += 64 * PER) {
         for (unsigned spin = 1;; spin++) {
             u64 w[PER];
@@ -101,6 +114,7 @@ __device__ bool px_poll(Addr addr, int n, unsigned tag, float *dst, unsigned *er
                 const int i = base + j * 64 + lane;
                 w[j] = (i < n) ? px_get(addr(i)) : ((u64)tag << 32);
             }
+            const u64 now = wall_clock64();
             bool ok = true;
 #pragma unroll
             for (int j = 0; j < PER; j++) ok = ok && ((unsigned)(w[j] >> 32) == tag);
@@ -116,11 +130,11 @@ __device__ bool px_poll(Addr addr, int n, unsigned tag, float *dst, unsigned *er
                 }
                 break;
             }
-            if (spin >= PX_SPIN_LIMIT) {
-                if (lane == 0) px_raise(err, QK_PX_ERR_TIMEOUT);
+            if (now - t0 > a.wait_ticks) {
+                if (lane == 0) px_raise(a.err, QK_PX_ERR_TIMEOUT);
                 return false;
             }
-            if ((spin & 127u) == 0u && px_aborted(err)) return false;
+            if ((spin & 15u) == 0u && px_aborted(a.err)) return false;
         }
     }
     return true;
@@ -382,7 +396,7 @@ __device__ bool px_x_update(const qk_persist_args &a, PxShared<H, I, NCW> &S, co
     const int r = S.r;
     // this block's slice of the 8 split-K partials
     auto slice = [&](int i) { return yp + (long)(i / SO) * H + SO * r + (i % SO); };
-    if (!px_poll<8 * SO / 64>(slice, 8 * SO, ty, S.ysum, a.err, lane)) return false;
+    if (!px_poll<8 * SO / 64>(a, slice, 8 * SO, ty, S.ysum, lane)) return false;
     if (tr_hop) *tr_hop = wall_clock64();
     if (lane < SO) {
         float o = S.ysum[lane];
@@ -393,7 +407,7 @@ __device__ bool px_x_update(const qk_persist_args &a, PxShared<H, I, NCW> &S, co
     // the XCD's whole new residual
     auto whole = [&](int i) { return xl + i; };
     ssq = 0.0f;
-    return px_poll<(H / 64 < 16 ? H / 64 : 16)>(whole, H, tx, S.xs, a.err, lane, &ssq);
+    return px_poll<(H / 64 < 16 ? H / 64 : 16)>(a, whole, H, tx, S.xs, lane, &ssq);
 }
 
 // xn = rms_norm(xs) * w (qwen_rms_norm, qwen_asr_kernels.c:750-809); w was
@@ -439,7 +453,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
     {
         float *dst = S.cand;   // scratch
         auto addr = [&](int i) { return a.xv + i; };
-        bool ok = px_poll<4>(addr, QK_PX_BLOCKS, a.epoch, dst, a.err, lane);
+        bool ok = px_poll<4>(a, addr, QK_PX_BLOCKS, a.epoch, dst, lane);
         if (ok) {
             bool good = true;
             for (int i = lane; i < QK_PX_BLOCKS; i += 64) good = good && (__float_as_uint(dst[i]) & 1u);
@@ -506,7 +520,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             {
                 const u64 *src = a.xq + (par * WG + g) * 512;
                 auto addr = [&](int i) { return src + i; };
-                ok = px_poll<8>(addr, 512, T, S.qkv, a.err, lane);
+                ok = px_poll<8>(a, addr, 512, T, S.qkv, lane);
             }
             mark(10 * l + 3);
             if (lane == 0) S.abort_ = !ok;
@@ -523,7 +537,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
                 const u64 *src = a.xa + (par * WG + g) * (long)(QK_PX_MAX_SPLIT * QK_PX_PART);
                 auto addr = [&](int i) { return src + i; };
                 // words per lane in flight: the 1.7B kernel has fewer registers per wave
-                ok = px_poll<(NCW == 4 ? 33 : 17)>(addr, sp.nsplit * QK_PX_PART, T + 1u, S.part, a.err, lane);
+                ok = px_poll<(NCW == 4 ? 33 : 17)>(a, addr, sp.nsplit * QK_PX_PART, T + 1u, S.part, lane);
             }
             mark(10 * l + 5);
             if (lane == 0) S.abort_ = !ok;
@@ -552,7 +566,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             {
                 const u64 *src = a.xh + (par * WG + g) * HG;
                 auto addr = [&](int i) { return src + i; };
-                ok = px_poll<(HG + 63) / 64>(addr, HG, T + 4u, S.hs, a.err, lane);
+                ok = px_poll<(HG + 63) / 64>(a, addr, HG, T + 4u, S.hs, lane);
             }
             mark(10 * l + 9);
             if (lane == 0) S.abort_ = !ok;
@@ -587,7 +601,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             px_sync();
             mark(10 * L + 2);
             auto addr = [&](int i) { return a.xc + i; };
-            bool ok = px_poll<8>(addr, 2 * QK_PX_BLOCKS, Tc, S.cand, a.err, lane);
+            bool ok = px_poll<8>(a, addr, 2 * QK_PX_BLOCKS, Tc, S.cand, lane);
             mark(10 * L + 3);
             if (ok) {
                 float bv = -1e30f;
@@ -1071,15 +1085,18 @@ static const void *px_kernel(int hidden, int inter, int *threads) {
     return nullptr;
 }
 
+// The grid is one block per CU and every block must be resident at once: the
+// device must have exactly 256 CUs and a block must fit on a CU, and at most one
+// may (the LDS of a block is more than half a CU's), so the dispatcher spreads
+// the grid one block per CU.
 extern "C" int qk_persist_supported(int hidden, int inter, int heads, int kv_heads, int device) {
     int threads = 0;
     const void *k = px_kernel(hidden, inter, &threads);
     if (!k || heads != 16 || kv_heads != QK_PX_XCD) return 0;
-    int cus = 0, coop = 0, per = 0;
+    int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
-    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess) return 0;
-    if (cus != QK_PX_BLOCKS || !coop) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, threads, 0) != hipSuccess || per < 1) return 0;
+    if (cus != QK_PX_BLOCKS) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, threads, 0) != hipSuccess || per != 1) return 0;
     return 1;
 }
 
@@ -1094,7 +1111,9 @@ extern "C" int qk_persist_launch(const qk_persist_args *a, int hidden, int inter
     if (a->first_tok >= a->vocab || a->pos0 < 0 || a->pos0 + a->n_steps > a->cap) return QWEN_HIP_EINVAL;
     qk_persist_args copy = *a;
     void *args[] = {&copy};
-    if (hipLaunchCooperativeKernel(k, dim3(QK_PX_BLOCKS), dim3(threads), args, 0, s) != hipSuccess)
-        return QWEN_HIP_EDEVICE;
+    // An ordinary launch on the caller's stream: residency of the whole grid is
+    // checked by the kernel's own check-in, under the same bounded wait as
+    // every other hand-over.
+    if (hipLaunchKernel(k, dim3(QK_PX_BLOCKS), dim3(threads), args, 0, s) != hipSuccess) return QWEN_HIP_EDEVICE;
     return 0;
 }

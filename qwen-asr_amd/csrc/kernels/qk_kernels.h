@@ -177,6 +177,7 @@ typedef struct {
     unsigned *cnt;             /* [16] per-XCD tickets, zeroed before every launch */
     unsigned *err;             /* QK_PX_ERR_* bits, zeroed before every launch */
     unsigned epoch;            /* first tag of this launch (>= 1) */
+    unsigned long long wait_ticks; /* bound of every wait, in ticks of the device wall clock */
     /* the steps */
     int pos0, n_steps;
     int first_tok;             /* >= 0: step 0 input is emb[first_tok] */

@@ -1,5 +1,5 @@
 """The persistent decode engine (engine 2: every layer, the LM head and the
-greedy feedback of all steps of one call in a single cooperative kernel)
+greedy feedback of all steps of one call in a single persistent kernel)
 against the graph engine (engine 0) on the reference's shapes.
 
 Both engines compute in fp32 from the same bf16 weights and fp32 K/V cache;
@@ -249,3 +249,44 @@ def test_streaming_rollback_pattern(qa, dec06):
         if a != b:
             s = np.sort(lg[i])
             assert s[-1] - s[-2] < TIE, (i, a, b)
+
+
+def test_wait_bound_gives_up(qa, dec06):
+    """Every wait inside the persistent kernel is bounded in wall-clock time.
+    With a zero limit every wait that its first poll does not satisfy gives
+    up: the launch still ends (every block leaves), and with the fallback off
+    the call fails with QWEN_HIP_EDEVICE and leaves kv_len as it was; with the
+    fallback on the same call is redone by the graph engine, counted, and
+    gives the graph engine's tokens; with the limit restored the persistent
+    engine is usable again and reproduces its own earlier tokens."""
+    d, rows = dec06
+    try:
+        d.set_engine(ENGINE_PERSIST)
+        d.set_kv_len(0)
+        d.prefill(rows[:-1])
+        base = d.kv_len()
+        first = d.forward(rows[-1])
+        ref = list(d.generate(first, 6))
+        n0 = d.fallbacks()
+        d.set_kv_len(base + 1)
+        d.set_fallback(False)
+        d.set_wait_limit(0.0)
+        with pytest.raises(RuntimeError, match="EDEVICE.*timed out"):
+            d.generate(first, 6)
+        assert d.kv_len() == base + 1
+        assert d.engine() == ENGINE_PERSIST and d.fallbacks() == n0
+        d.set_fallback(True)
+        got = list(d.generate(first, 6))
+        assert d.fallbacks() == n0 + 1 and d.engine() == ENGINE_GRAPH
+        assert d.kv_len() == base + 7
+        d.set_kv_len(base + 1)
+        assert list(d.generate(first, 6)) == got, "the fallback's tokens are the graph engine's"
+        d.set_wait_limit(1.0)
+        d.set_engine(ENGINE_PERSIST)
+        d.set_kv_len(base + 1)
+        assert list(d.generate(first, 6)) == ref
+        assert d.fallbacks() == n0 + 1
+    finally:
+        d.set_wait_limit(1.0)
+        d.set_fallback(True)
+        d.set_engine(ENGINE_PERSIST)
