@@ -93,14 +93,21 @@ static float orc_dot_f32(const float *a, const float *b, int n) {
 }
 
 /* qwen_linear_nobias_bf16 / bf16 matvec, rows split over threads
- * (qwen_asr_kernels.c:351-373, :462-472).  y[s][o] = W[o] . x[s]. */
+ * (qwen_asr_kernels.c:351-373, :462-472).  y[s][o] = W[o] . x[s].  Each
+ * (s, o) is one orc_dot_bf16 whatever the tiling, so the result does not
+ * depend on it; input rows are taken 16 at a time so a weight row is read
+ * once per 16 rows (the oracle's long prefills). */
+#define ORC_ROW_TILE 16
 void orc_linear_bf16(float *y, const float *x, const uint16_t *W,
                      int seq, int in_dim, int out_dim) {
-    long total = (long)seq * out_dim;
+    const long tiles = (seq + ORC_ROW_TILE - 1) / ORC_ROW_TILE;
+    const long total = tiles * out_dim;
 #pragma omp parallel for schedule(static)
     for (long t = 0; t < total; t++) {
-        int s = (int)(t / out_dim), o = (int)(t % out_dim);
-        y[(size_t)s * out_dim + o] = orc_dot_bf16(W + (size_t)o * in_dim, x + (size_t)s * in_dim, in_dim);
+        const int o = (int)(t % out_dim), s0 = (int)(t / out_dim) * ORC_ROW_TILE;
+        const int s1 = s0 + ORC_ROW_TILE < seq ? s0 + ORC_ROW_TILE : seq;
+        for (int s = s0; s < s1; s++)
+            y[(size_t)s * out_dim + o] = orc_dot_bf16(W + (size_t)o * in_dim, x + (size_t)s * in_dim, in_dim);
     }
 }
 
