@@ -342,6 +342,56 @@ class RefModel(_Decoder):
 
 
 # ---------------------------------------------------------------------------
+# the reference's callers of the decoder (restated for the tests)
+# ---------------------------------------------------------------------------
+TOKEN_ENDOFTEXT, TOKEN_IM_END = 151643, 151645
+
+
+def greedy_until_eos(dec, token, max_tokens):
+    """The reference's greedy loop after the first token (qwen_asr.c:729-759,
+    and the chunk loop :1802-1814): while fewer than max_tokens tokens were
+    generated, stop at <|endoftext|> / <|im_end|>, otherwise keep the token
+    and forward its embedding.  `dec` (Oracle or RefModel) has just produced
+    `token`.  Returns (kept tokens, the token the last forward produced)."""
+    kept, n = [], 0
+    while n < max_tokens:
+        n += 1
+        if token in (TOKEN_ENDOFTEXT, TOKEN_IM_END):
+            break
+        kept.append(int(token))
+        token, _, _ = dec.forward(dec.embed(token))
+    return kept, token
+
+
+class RefStream:
+    """The decoder half of the reference's streaming transcriber
+    (qwen_asr.c:1748-1829) on a CPU decoder: per chunk, keep the KV of the
+    longest prefix of the prefill rows (all rows but the last) that is
+    bitwise equal to the previous chunk's (memcmp, :1752-1761), prefill the
+    rest (:1764-1770), forward the last row (:1773-1774), then the greedy
+    loop up to max_new tokens (:1802-1814)."""
+
+    def __init__(self, dec):
+        self.dec, self.prev = dec, None
+
+    def chunk(self, rows, max_new):
+        rows = np.ascontiguousarray(rows, np.float32)
+        n = rows.shape[0] - 1
+        reused = 0
+        if self.prev is not None:
+            cmp = min(n, self.prev.shape[0])
+            while reused < cmp and self.prev[reused].tobytes() == rows[reused].tobytes():
+                reused += 1
+        self.dec.set_kv_len(reused)
+        if n > reused:
+            self.dec.prefill(rows[reused:n])
+        token, _, _ = self.dec.forward(rows[n])
+        self.prev = rows[:n].copy()
+        kept, _ = greedy_until_eos(self.dec, token, max_new)
+        return kept, reused
+
+
+# ---------------------------------------------------------------------------
 # workload inputs (BASELINE.json configs)
 # ---------------------------------------------------------------------------
 def prompt_rows(model: SynthModel, n_audio, n_ids, seed=0, audio_chunk=0, token_set=0, embed=None):

@@ -45,6 +45,35 @@ def test_gemv_sweep(P, qa, gpu, rows, cols):
     assert np.all(np.abs(y - yo) <= bound), float(np.max(np.abs(y - yo) / bound))
 
 
+@pytest.mark.parametrize("hidden,qd,kvd", [(1024, 2048, 1024), (2048, 2048, 1024)])
+def test_linear_qkv(P, qa, gpu, hidden, qd, kvd):
+    """qwen_hip_linear_nobias_bf16_qkv (qwen_asr_kernels.h:45-49): the three
+    seq = 1 products of one input row, each against the reference's own
+    qwen_linear_nobias_bf16 (oracle/_ref) and the oracle, at the GEMV rounding
+    bound."""
+    Ws = [P.synth_bf16(n * hidden, 2, 9400 + i).reshape(n, hidden) for i, n in enumerate((qd, kvd, kvd))]
+    x = P.synth_uniform(hidden, 2, 9450 + hidden)
+    dW = [dev(gpu, W.view(np.int16)) for W in Ws]
+    dx = dev(gpu, x)
+    dq = gpu.empty(qd, dtype=gpu.float32, device="cuda")
+    dk = gpu.empty(kvd, dtype=gpu.float32, device="cuda")
+    dv = gpu.empty(kvd, dtype=gpu.float32, device="cuda")
+    qa.check(qa.lib().qwen_hip_linear_nobias_bf16_qkv(ptr(dq), ptr(dk), ptr(dv), ptr(dx), ptr(dW[0]), ptr(dW[1]),
+                                                      ptr(dW[2]), hidden, qd, kvd, None), "qkv")
+    gpu.cuda.synchronize()
+    ref = P.ref_lib() if P.ref_available() else None
+    for W, d in zip(Ws, (dq, dk, dv)):
+        y, n = host(d), W.shape[0]
+        yo = np.empty(n, np.float32)
+        P.orc_lib().orc_linear_bf16(yo, x, W, 1, hidden, n)
+        bound = 8 * hidden * 2.0 ** -24 * (np.abs(P.bf16_to_f32(W)) @ np.abs(x)) + 1e-12
+        assert np.all(np.abs(y - yo) <= bound)
+        if ref is not None:
+            yr = np.empty(n, np.float32)
+            ref.qwen_linear_nobias_bf16(yr, x, np.ascontiguousarray(W), 1, hidden, n)
+            assert np.all(np.abs(y - yr) <= bound)
+
+
 # covers every tiling of qk_gemm_plan_for: 32 / 64 / 128-row blocks, split-K
 # with its reduce pass (and the odd-N case that cannot split), one split
 @pytest.mark.parametrize("M,N,K", [(2, 64, 256), (31, 4096, 1024), (64, 1024, 2048), (401, 6144, 1024),

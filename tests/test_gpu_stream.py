@@ -41,6 +41,17 @@ def test_checkpoint_decoder_equals_load_layer(P, qa, gpu, tmp_path):
         out.append((toks, np.array(lg)))
     assert out[0][0] == out[1][0]
     assert np.array_equal(out[0][1], out[1][1])
+    # and against the CPU oracle on the same weights (teacher-forced with the
+    # checkpoint decoder's tokens): logits within the north-star bar
+    o = P.Oracle(m)
+    o.prefill(rows[:-1])
+    for i, t in enumerate(out[0][0]):
+        _, lo, _ = o.forward(rows[-1] if i == 0 else o.embed(out[0][0][i - 1]), True)
+        assert np.all(np.abs(out[0][1][i] - lo) <= 2e-2 + 1e-2 * np.abs(lo)), i
+        if t != int(np.argmax(lo)):
+            s = np.sort(lo)
+            assert s[-1] - s[-2] < TIE, i
+    o.close()
     a.close()
     b.close()
 

@@ -319,3 +319,60 @@ def test_oracle_prefill_split_and_rollback(P):
     a.set_kv_len(20)
     a.prefill(rows[20:-1])
     np.testing.assert_allclose(a.forward(rows[-1], True)[1], la, atol=1e-6)
+
+
+EOS_CFG = (1024, 2, 16, 8, 128, 3072, 151936)
+
+
+def eos_model(P):
+    """Two layers of the 0.6B shape with the full vocabulary, <|im_end|>'s
+    embedding row scaled by 3: greedy decoding from the seed-3 prompt below
+    emits <|im_end|> as its 5th token (top-2 margins >= 0.1 on the way)."""
+    m = P.SynthModel(P.Config(*EOS_CFG), seed=3)
+    m.emb[P.TOKEN_IM_END] = P.f32_to_bf16(P.bf16_to_f32(m.emb[P.TOKEN_IM_END]) * 3.0)
+    return m
+
+
+def test_greedy_loop_restatement(P):
+    """greedy_until_eos (qwen_asr.c:729-759) on the oracle and on the
+    reference's own decoder (oracle/_ref): the same kept tokens, stop at the
+    first EOS without keeping or forwarding it, the KV holds exactly the
+    forwarded tokens, and a max_tokens cap keeps exactly that many."""
+    need_ref(P)
+    m = eos_model(P)
+    rows, _ = P.prompt_rows(m, 40, 8, seed=3)
+    runs = []
+    for dec in (P.Oracle(m), P.RefModel(m, threads=4)):
+        dec.prefill(rows[:-1])
+        t, _, _ = dec.forward(rows[-1])
+        kept, last = P.greedy_until_eos(dec, t, 30)
+        runs.append((kept, last, dec.kv_len()))
+        assert dec.kv_len() == rows.shape[0] + len(kept)      # last row + every kept token forwarded once
+        dec.set_kv_len(rows.shape[0])
+        capped, _ = P.greedy_until_eos(dec, t, 2)
+        assert capped == kept[:2] and dec.kv_len() == rows.shape[0] + 2
+        dec.close()
+    assert runs[0] == runs[1]
+    assert runs[0][0] == [118997, 144330, 76550, 77354] and runs[0][1] == P.TOKEN_IM_END
+
+
+def test_stream_restatement(P):
+    """RefStream (qwen_asr.c:1748-1829): the reused prefix is the longest run of
+    bitwise-equal leading prefill rows, the KV after a chunk holds its prefill
+    rows + the last row + the kept tokens, and chunks with reuse give the same
+    tokens as the same chunks prefilled from scratch (the oracle's prefill is
+    split-invariant bit for bit)."""
+    m = eos_model(P)
+    head, _ = P.prompt_rows(m, 0, 8, seed=3)
+    audio = [P.synth_f32(12 * 1024, 3, P.synth_audio_id(c)).reshape(12, 1024) for c in range(4)]
+    tail = np.stack([m.embed(t) for t in (151644, 77091, 198)])
+    chunks = [np.concatenate([head] + audio[:c + 1] + [tail]) for c in range(4)]
+    chunks.append(np.concatenate([head] + audio[2:4] + [tail]))       # oldest audio evicted
+    reuse = P.RefStream(P.Oracle(m))
+    for i, rows in enumerate(chunks):
+        kept, reused = reuse.chunk(rows, 6)
+        want = 0 if i == 0 else (8 if i == 4 else 8 + 12 * i)
+        assert reused == want, (i, reused)
+        assert reuse.dec.kv_len() == rows.shape[0] + len(kept)
+        fresh = P.RefStream(P.Oracle(m))
+        assert fresh.chunk(rows, 6) == (kept, 0)
