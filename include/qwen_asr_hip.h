@@ -387,6 +387,20 @@ int qwen_hip_swiglu_multiply(float *out, const float *gate_up, int seq_len,
 int qwen_hip_linear_nobias_bf16(float *y, const float *x, const uint16_t *W_bf16,
                                 int seq_len, int in_dim, int out_dim, hipStream_t s);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same product as qwen_hip_linear_nobias_bf16 with the same
+ * kernels and results, but it never allocates or frees memory and never
+ * synchronises; it only enqueues on s.  Its temporary memory is one fixed
+ * per-GPU device array of qwen_hip_linear_noalloc_max_bytes() bytes (32 MiB),
+ * held from library load to process exit.  A call whose seq > 1 product
+ * needs more (about 4*seq*in bytes, plus split-K partials for small products)
+ * returns QWEN_HIP_EINVAL.  All calls on one GPU share that array: calls
+ * whose kernels overlap in time on one GPU race, so order them (one stream). */
+int qwen_hip_linear_nobias_bf16_noalloc(float *y, const float *x, const uint16_t *W_bf16,
+                                        int seq_len, int in_dim, int out_dim, hipStream_t s);
+size_t qwen_hip_linear_noalloc_max_bytes(void);
+
 /* qwen_linear_nobias_bf16_qkv (qwen_asr_kernels.h:45): the three seq=1 matvecs */
 int qwen_hip_linear_nobias_bf16_qkv(float *q, float *k, float *v, const float *x,
                                     const uint16_t *Wq_bf16, const uint16_t *Wk_bf16,

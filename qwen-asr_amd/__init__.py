@@ -111,6 +111,8 @@ SIGNATURES = [
     ("qwen_hip_swiglu_multiply", _i, [_vp, _vp, _i, _i, _vp]),
     ("qwen_hip_linear_nobias_bf16", _i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     ("qwen_hip_linear_nobias_bf16_qkv", _i, [_vp] * 7 + [_i, _i, _i, _vp]),
+    ("qwen_hip_linear_nobias_bf16_noalloc", _i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    ("qwen_hip_linear_noalloc_max_bytes", C.c_size_t, []),
     ("qwen_hip_causal_attention", _i, [_vp] * 4 + [_i] * 5 + [_f, _i, _vp]),
     ("qwen_hip_argmax_matvec_bf16", _i, [_vp, _vp, _i, _i, _vp]),
     ("qwen_synth_key", _u64, [_u64, _u64]),

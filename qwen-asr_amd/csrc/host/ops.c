@@ -70,6 +70,42 @@ int qwen_hip_swiglu_multiply(float *out, const float *gu, int S, int inter, hipS
     return qk_swiglu_launch(out, gu, S, inter, s);
 }
 
+/* Plan of the seq > 1 product: tiling as qk_gemm_plan_for, except that an odd
+ * output width keeps one split (the split-K reduce works on column pairs). */
+static void linear_plan(int S, int in_dim, int out_dim, qk_gemm_plan *p) {
+    qk_gemm_plan_for(S, out_dim, in_dim, p);
+    if (p->nsplit > 1 && (out_dim & 1)) {
+        p->kc = ((in_dim + 63) / 64) * 64;
+        p->nsplit = 1;
+    }
+}
+
+size_t qk_linear_ws_bytes(int S, int in_dim, int out_dim) {
+    qk_gemm_plan p;
+    linear_plan(S, in_dim, out_dim, &p);
+    const size_t n = (size_t)S * in_dim;
+    const size_t part = p.nsplit > 1 ? (size_t)p.nsplit * S * out_dim : 0;
+    return ((2 * n * sizeof(uint16_t) + 255) & ~(size_t)255) + part * sizeof(float);
+}
+
+int qk_linear_gemm(float *y, const float *x, const uint16_t *W, int S, int in_dim, int out_dim, void *ws,
+                   hipStream_t s) {
+    qk_gemm_plan p;
+    linear_plan(S, in_dim, out_dim, &p);
+    const size_t n = (size_t)S * in_dim;
+    const size_t abytes = (2 * n * sizeof(uint16_t) + 255) & ~(size_t)255;
+    uint16_t *ah = (uint16_t *)ws, *al = ah + n;
+    float *pp = (float *)((char *)ws + abytes);
+    int rc = qk_split_bf16_launch(x, (long)n, ah, al, s);
+    if (!rc && p.nsplit > 1) {
+        rc = qk_gemm_launch(ah, al, W, S, out_dim, in_dim, &p, QK_GEMM_STORE, pp, NULL, NULL, s);
+        if (!rc) rc = qk_gemm_reduce_launch(pp, p.nsplit, S, out_dim, QK_GEMM_STORE, y, NULL, NULL, s);
+    } else if (!rc) {
+        rc = qk_gemm_launch(ah, al, W, S, out_dim, in_dim, &p, QK_GEMM_STORE, y, NULL, NULL, s);
+    }
+    return rc;
+}
+
 int qwen_hip_linear_nobias_bf16(float *y, const float *x, const uint16_t *W, int S, int in_dim, int out_dim,
                                 hipStream_t s) {
     if (!y || !x || !W || S <= 0 || in_dim <= 0 || out_dim <= 0) return QWEN_HIP_EINVAL;
@@ -79,25 +115,8 @@ int qwen_hip_linear_nobias_bf16(float *y, const float *x, const uint16_t *W, int
     }
     pthread_mutex_lock(&g_ws_lock);
     void *ws = NULL;
-    const size_t n = (size_t)S * in_dim;
-    qk_gemm_plan p;
-    qk_gemm_plan_for(S, out_dim, in_dim, &p);
-    if (p.nsplit > 1 && (out_dim & 1)) {              /* the reduce pass works on column pairs */
-        p.kc = ((in_dim + 63) / 64) * 64;
-        p.nsplit = 1;
-    }
-    const size_t part = p.nsplit > 1 ? (size_t)p.nsplit * S * out_dim : 0;
-    const size_t abytes = (2 * n * sizeof(uint16_t) + 255) & ~(size_t)255;
-    int rc = workspace(abytes + part * sizeof(float), &ws);
-    uint16_t *ah = (uint16_t *)ws, *al = ah + n;
-    float *pp = (float *)((char *)ws + abytes);
-    if (!rc) rc = qk_split_bf16_launch(x, (long)n, ah, al, s);
-    if (!rc && p.nsplit > 1) {
-        rc = qk_gemm_launch(ah, al, W, S, out_dim, in_dim, &p, QK_GEMM_STORE, pp, NULL, NULL, s);
-        if (!rc) rc = qk_gemm_reduce_launch(pp, p.nsplit, S, out_dim, QK_GEMM_STORE, y, NULL, NULL, s);
-    } else if (!rc) {
-        rc = qk_gemm_launch(ah, al, W, S, out_dim, in_dim, &p, QK_GEMM_STORE, y, NULL, NULL, s);
-    }
+    int rc = workspace(qk_linear_ws_bytes(S, in_dim, out_dim), &ws);
+    if (!rc) rc = qk_linear_gemm(y, x, W, S, in_dim, out_dim, ws, s);
     if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = QWEN_HIP_EDEVICE;
     pthread_mutex_unlock(&g_ws_lock);
     return rc;

@@ -238,6 +238,13 @@ int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W
 /* Sum nsum partials [nsum][M][N] in order and apply epi (N even). */
 int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, float *y, uint16_t *out_hi,
                           uint16_t *out_lo, hipStream_t s);
+/* y[S][out] = x[S][in] . W[out][in]^T for S > 1 (the op-level linear's
+ * product path, csrc/host/ops.c): split x to bf16 hi/lo, GEMM, split-K reduce,
+ * all launched on s with ws (>= qk_linear_ws_bytes bytes) as the only
+ * temporary memory. */
+size_t qk_linear_ws_bytes(int S, int in_dim, int out_dim);
+int qk_linear_gemm(float *y, const float *x, const uint16_t *W, int S, int in_dim, int out_dim, void *ws,
+                   hipStream_t s);
 
 /* ---- audio encoder (fp32 matrix cores) --------------------------------- */
 /* C[M][N] (=, +=) A[M][K] . B[N][K]^T (+ bias_m[m] | bias_n[n]) (+ pe[m % pe_rows][n])
