@@ -379,9 +379,18 @@ def run_encoder(qa, args, wl):
         "wall_ms_per_step": round(wall / K * 1e3, 4), "cpu_baseline": cpu}), flush=True)
 
 
+CPU_1T_STEPS = 8
+REF_BLAS = ("none: the reference's BLAS build (Makefile:47-48, cblas_sgemm in qwen_asr_kernels.c:181-202) "
+            "needs cblas.h and an OpenBLAS library, which this image does not have; the reference is built "
+            "from its sources without USE_BLAS, so its prefill runs the non-BLAS loop "
+            "(qwen_asr_kernels.c:211-222) and its decode (seq 1, never BLAS) is unaffected")
+
+
 def cpu_baseline(wl, rows, first_token, threads, decode_steps):
     """Reference decoder (oracle/_ref) on this host: prefill of the same rows
-    and `decode_steps` greedy forwards from the same first token."""
+    and `decode_steps` greedy forwards from the same first token on `threads`
+    threads, then CPU_1T_STEPS forwards on one thread from the same position;
+    with the host's CPU model, ISA level and STREAM-style triad bandwidth."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as P
     if not P.ref_available():
@@ -393,10 +402,25 @@ def cpu_baseline(wl, rows, first_token, threads, decode_steps):
     log(f"[cpu] weights generated in {time.time() - t0:.1f}s; prefill {rows.shape[0] - 1} rows on {threads} threads")
     tp = r.time_prefill(rows[:-1])
     tok, _, _ = r.forward(rows[-1])
+    base = r.kv_len()
     toks, td = r.generate(first_token, decode_steps)
-    log(f"[cpu] prefill {tp:.1f}s, {decode_steps} decode steps {td:.2f}s (first token {tok})")
+    r.set_kv_len(base)
+    r.lib.ref_set_threads(1)
+    toks1, td1 = r.generate(first_token, CPU_1T_STEPS)
+    r.lib.ref_set_threads(threads)
+    host = P.host_info()
+    bw = P.stream_gbs(threads)
+    bw1 = P.stream_gbs(1)
+    log(f"[cpu] prefill {tp:.1f}s, {decode_steps} decode steps {td:.2f}s (first token {tok}); 1 thread: "
+        f"{CPU_1T_STEPS} steps {td1:.2f}s; triad {bw:.1f} GB/s ({threads} thr), {bw1:.1f} GB/s (1 thr); {host}")
     return {"value": round(decode_steps / td, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
             "prefill_tok_s": round((rows.shape[0] - 1) / tp, 2),
+            "one_thread": {"value": round(CPU_1T_STEPS / td1, 3), "unit": "tok/s", "cores": 1,
+                           "steps": CPU_1T_STEPS,
+                           "same_tokens": bool(list(toks1[:len(toks)]) == list(toks[:len(toks1)]))},
+            "cpu_model": host["cpu_model"], "logical_cpus": host["logical_cpus"], "isa": host["isa"],
+            "host_triad_gb_s": {str(threads): round(bw, 1), "1": round(bw1, 1)},
+            "blas": REF_BLAS,
             "sample": f"reference decoder (oracle/_ref, no BLAS) on the same weights/rows: prefill "
                       f"{rows.shape[0] - 1} rows, then {decode_steps} greedy decode steps; decode tok/s over those steps",
             "first_token_matches_gpu": bool(tok == first_token)}

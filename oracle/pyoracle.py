@@ -120,8 +120,32 @@ def orc_lib():
         lib.orc_argmax_matvec_bf16.restype = C.c_int
         lib.orc_dot_bf16.argtypes = [_u16p, _f32p, C.c_int]
         lib.orc_dot_bf16.restype = C.c_float
+        lib.orc_stream_triad.argtypes = [C.c_long, C.c_int]
+        lib.orc_stream_triad.restype = C.c_double
         _orc = lib
     return _orc
+
+
+def host_info():
+    """CPU model, logical CPUs and the ISA level the compiled reference runs at."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    isa = "x86-64-v4 (AVX-512F/BW)" if _cpu_has_avx512() else "x86-64-v3 (AVX2+FMA)"
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "isa": isa}
+
+
+def stream_gbs(threads, n=1 << 26, reps=5):
+    """STREAM-style triad bandwidth of this host on `threads` OpenMP threads (GB/s)."""
+    lib = orc_lib()
+    lib.orc_set_threads(threads)
+    return float(lib.orc_stream_triad(n, reps))
 
 
 def _cpu_has_avx512():

@@ -437,3 +437,31 @@ void orc_destroy(void *mp) {
     free(m->kc); free(m->vc); free(m->rcos); free(m->rsin); free(m->hidden_state);
     free(m);
 }
+
+/* Host memory bandwidth for the CPU baseline's roofline (bench.py): a
+ * STREAM-style triad a[i] = b[i] + s*c[i] over three n-float arrays on the
+ * OpenMP threads in use, best of `reps` passes; returns GB/s counting 3 x 4
+ * bytes per element (two reads, one write). Not part of the decoder checks. */
+double orc_stream_triad(long n, int reps) {
+    float *a = (float *)malloc((size_t)n * 4), *b = (float *)malloc((size_t)n * 4), *c = (float *)malloc((size_t)n * 4);
+    if (!a || !b || !c) { free(a); free(b); free(c); return 0.0; }
+#pragma omp parallel for schedule(static)
+    for (long i = 0; i < n; i++) { a[i] = 0.0f; b[i] = 1.0f; c[i] = 2.0f; }
+    double best = 0.0;
+    for (int r = 0; r < reps; r++) {
+#ifdef _OPENMP
+        double t0 = omp_get_wtime();
+#endif
+#pragma omp parallel for schedule(static)
+        for (long i = 0; i < n; i++) a[i] = b[i] + 3.0f * c[i];
+#ifdef _OPENMP
+        double dt = omp_get_wtime() - t0;
+        double gbs = 12.0 * (double)n / dt / 1e9;
+        if (gbs > best) best = gbs;
+#endif
+    }
+    volatile float sink = a[n / 2];
+    (void)sink;
+    free(a); free(b); free(c);
+    return best;
+}
