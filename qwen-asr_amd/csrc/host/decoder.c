@@ -529,7 +529,7 @@ static int prefill_layers(qwen_hip_decoder *d, int S) {
     qk_gemm_plan gq, go, gg, gd;
     qk_gemm_plan_for(S, d->qkv_rows, D, &gq);
     qk_gemm_plan_for(S, D, d->qd, &go);
-    qk_gemm_plan_for(S, 2 * I, D, &gg);
+    qk_gemm_plan_epi(S, 2 * I, D, QK_GEMM_SWIGLU, &gg);
     qk_gemm_plan_for(S, D, I, &gd);
     size_t pg = 0;
     const size_t cand[4] = {gq.nsplit > 1 ? (size_t)gq.nsplit * S * d->qkv_rows : 0,

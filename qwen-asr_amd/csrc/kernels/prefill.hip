@@ -97,9 +97,20 @@ __global__ __launch_bounds__(256) void rmsnorm_split_rows(float *x, const float 
         const float *pr = part + (size_t)row * D + lane;
 #pragma unroll
         for (int j = 0; j < DPL; j++) ps[j] = pr[j * 64];
-        for (int sp = 1; sp < nsum; sp++)
+        for (int sp = 1; sp < nsum; sp += 2) {          // two splits' loads per round trip, summed in order
+            const bool two = sp + 1 < nsum;
+            float a[DPL], b[DPL];
 #pragma unroll
-            for (int j = 0; j < DPL; j++) ps[j] += pr[sp * pstride + j * 64];
+            for (int j = 0; j < DPL; j++) {
+                a[j] = pr[sp * pstride + j * 64];
+                b[j] = two ? pr[(sp + 1) * pstride + j * 64] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < DPL; j++) {
+                ps[j] += a[j];
+                if (two) ps[j] += b[j];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < DPL; j++) {
             v[j] += ps[j];
@@ -123,6 +134,47 @@ __global__ __launch_bounds__(256) void rmsnorm_split_rows(float *x, const float 
     }
 }
 
+// D = EPT * RN_THREADS: the same sums and products as rmsnorm_split, with
+// the row and the weights held in registers (one memory round trip fewer)
+template <int EPT>
+__global__ __launch_bounds__(RN_THREADS) void rmsnorm_split_reg(float *x, const float *part, int nsum, long pstride,
+                                                                const float *w, float eps, uint16_t *hi,
+                                                                uint16_t *lo) {
+    constexpr int D = EPT * RN_THREADS;
+    __shared__ float red[RN_THREADS / 64];
+    float *xr = x + (size_t)blockIdx.x * D;
+    float v[EPT], wv[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        const int i = threadIdx.x + e * RN_THREADS;
+        v[e] = xr[i];
+        wv[e] = w ? w[i] : 1.0f;
+    }
+    if (nsum) {
+#pragma unroll
+        for (int e = 0; e < EPT; e++) {
+            const int i = threadIdx.x + e * RN_THREADS;
+            v[e] += sum_splits<QK_GEMM_MAX_SPLIT>(part + (size_t)blockIdx.x * D + i, nsum, pstride);
+            xr[i] = v[e];
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) ss = fmaf(v[e], v[e], ss);
+    float rinv = 1.0f;
+    if (w) {
+        ss = block_sum<RN_THREADS / 64>(ss, red);
+        rinv = 1.0f / sqrtf(ss / (float)D + eps);
+    }
+    if (!hi) return;
+    uint16_t *h = hi + (size_t)blockIdx.x * D, *l = lo + (size_t)blockIdx.x * D;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        const int i = threadIdx.x + e * RN_THREADS;
+        split2(w ? (v[e] * wv[e]) * rinv : v[e], h[i], l[i]);
+    }
+}
+
 extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride, const float *w, int S,
                                        int D, float eps, uint16_t *hi, uint16_t *lo, hipStream_t s) {
     if (S <= 0 || D <= 0 || !x || nsum < 0 || nsum > QK_GEMM_MAX_SPLIT || (nsum && !part) || (!hi) != (!lo) ||
@@ -133,6 +185,10 @@ extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, lo
         const unsigned blocks = (unsigned)((S + 3) / 4);
         if (D == 1024) rmsnorm_split_rows<16><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
         else rmsnorm_split_rows<32><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
+    } else if (D == RN_THREADS) {
+        rmsnorm_split_reg<1><<<S, RN_THREADS, 0, s>>>(x, part, nsum, pstride, w, eps, hi, lo);
+    } else if (D == 2 * RN_THREADS) {
+        rmsnorm_split_reg<2><<<S, RN_THREADS, 0, s>>>(x, part, nsum, pstride, w, eps, hi, lo);
     } else {
         rmsnorm_split<<<S, RN_THREADS, 0, s>>>(x, part, nsum, pstride, w, D, eps, hi, lo);
     }
@@ -402,6 +458,171 @@ static void gemm_wide_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const
         gemm_hilo_wide<QK_GEMM_SWIGLU, BM><<<grid, 512, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
 }
 
+// ---------------------------------------------------------------------------
+// Mid-M GEMM (a few hundred rows, e.g. a 401-row prefill; same product and
+// epilogues as gemm_hilo): block tile BM x BN with NW waves, each 32 x WTN
+// (2 x WTN / 16 MFMA tiles), K walked 32 at a time through a ring of NST LDS
+// stages filled by direct global -> LDS loads in the stage layout and swizzle
+// of gemm_hilo_wide.  At this size a CU holds one or two tiles and walks
+// their whole k range: the register-staged kernel (one k tile in flight)
+// spends ~1.1 us per 64-deep k tile waiting for loads, ~5x its MFMA time.
+// Here NST - 1 stages are in flight; four stages (64 KB at 64 x 128) let two
+// blocks share a CU, which measured faster than deeper rings with one block
+// per CU.  The 16-row load groups of a stage (A_hi, A_lo, W) are dealt
+// round-robin to the waves: LPW 1 KB load instructions per wave and stage.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int ring_waves(int bm, int bn) { return bm / 32 * (bn / 64) < 4 ? 4 : bm / 32 * (bn / 64); }
+__device__ constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 15) | ((n >> 4) << 14); }
+
+// wait until at most later * LPW of this wave's loads are outstanding
+// (later <= MAXL: the stages issued after the one about to be read)
+template <int LPW, int MAXL>
+__device__ __forceinline__ void ring_wait(int later) {
+    if constexpr (MAXL > 0) {
+        if (later >= MAXL) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(MAXL * LPW));
+            return;
+        }
+        ring_wait<LPW, MAXL - 1>(later);
+    } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+}
+
+// 16 bytes per lane from global memory straight into LDS (lane l at byte 16 l
+// of the 1 KB at l0).  Called through this helper: with the builtin written in
+// the kernel on pointers held in an array, hipcc's host pass drops the
+// kernel's launch stub.
+__device__ __forceinline__ void lds_load16(const uint16_t *g, unsigned char *l0) {
+    __builtin_amdgcn_global_load_lds(g, l0, 16, 0, 0);
+}
+
+template <int EPI, int BM, int BN, int NST>
+__global__ __launch_bounds__(ring_waves(BM, BN) * 64) void gemm_hilo_ring(const uint16_t *__restrict__ ahi,
+                                                                           const uint16_t *__restrict__ alo,
+                                                                           const uint16_t *__restrict__ W, int M,
+                                                                           int N, int K, int kc, float *y,
+                                                                           uint16_t *ohi, uint16_t *olo) {
+    constexpr int NW = ring_waves(BM, BN), WGM = BM / 32, WGN = NW / WGM, WTN = BN / WGN, TM = 2, TN = WTN / 16;
+    constexpr int AB = BM * 64, STAGE = 2 * AB + BN * 64;   // bytes: one A half, one stage
+    constexpr int GROUPS = (2 * BM + BN) / 16, LPW = GROUPS / NW;
+    static_assert(WGM * WGN == NW && WTN % 16 == 0 && GROUPS % NW == 0, "wave grid / load split");
+    static_assert((NST - 2) * LPW <= 63 && NST * STAGE <= 160 * 1024, "vmcnt / LDS range");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[NST][STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb = blockIdx.z * kc, ke = min(K, kb + kc);
+    const int nk = (ke - kb) / QK_GBK;
+
+    // this lane's load slots: row rr of each of the wave's 16-row groups,
+    // k chunk cl (swizzled); rows past M re-read row M - 1 (results dropped)
+    const int rr = lane >> 2, cl = (lane & 3) ^ ((rr >> 2) & 3);
+    const uint16_t *src[LPW];
+    int dst[LPW];
+#pragma unroll
+    for (int j = 0; j < LPW; j++) {
+        const int g = wave + NW * j;
+        if (g < BM / 16) {
+            src[j] = ahi + (size_t)min(m0 + 16 * g + rr, M - 1) * K + kb + 8 * cl;
+            dst[j] = 1024 * g;
+        } else if (g < BM / 8) {
+            src[j] = alo + (size_t)min(m0 + 16 * (g - BM / 16) + rr, M - 1) * K + kb + 8 * cl;
+            dst[j] = AB + 1024 * (g - BM / 16);
+        } else {
+            src[j] = W + (size_t)(n0 + 16 * (g - BM / 8) + rr) * K + kb + 8 * cl;
+            dst[j] = 2 * AB + 1024 * (g - BM / 8);
+        }
+    }
+    auto issue = [&](int kt) {
+        unsigned char *st = lds[kt % NST];
+#pragma unroll
+        for (int j = 0; j < LPW; j++) lds_load16(src[j] + kt * QK_GBK, st + dst[j]);
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    const int fr = lane & 15;
+    const int fo = fr * 64 + 16 * ((lane >> 4) ^ ((fr >> 2) & 3));
+    for (int t = 0; t < NST - 1 && t < nk; t++) issue(t);
+    for (int kt = 0; kt < nk; kt++) {
+        ring_wait<LPW, NST - 2>(min(nk - 1 - kt, NST - 2));
+        // every wave's share of stage kt is in LDS and stage kt - 1 is free (a
+        // plain s_barrier: __syncthreads() would also drain the later stages)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kt + NST - 1 < nk) issue(kt + NST - 1);
+        const unsigned char *st = lds[kt % NST];
+        bf16x8 bfr[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            bfr[j] = *reinterpret_cast<const bf16x8 *>(st + 2 * AB + (wn * WTN + j * 16) * 64 + fo);
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int ro = (wm * 32 + i * 16) * 64 + fo;
+            const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(st + ro);
+            const bf16x8 al = *reinterpret_cast<const bf16x8 *>(st + AB + ro);
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bfr[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bfr[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    float *yz = y + (EPI == QK_GEMM_STORE ? (size_t)blockIdx.z * M * N : 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * WTN + j * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+                const float v = acc[i][j][r];
+                if (EPI == QK_GEMM_SWIGLU) {
+                    const float u = __shfl_xor(v, 1, QK_WAVE);   // column n+1 lives in lane l^1
+                    if ((lane & 1) == 0 && m < M) {
+                        const size_t o = (size_t)m * (N / 2) + (n >> 1);
+                        split2(swiglu1(v, u), ohi[o], olo[o]);
+                    }
+                } else if (m < M) {
+                    if (EPI == QK_GEMM_STORE) yz[(size_t)m * N + n] = v;
+                    else y[(size_t)m * N + n] += v;
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int NST>
+static void gemm_ring_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int N, int K,
+                               const qk_gemm_plan *p, int epi, float *y, uint16_t *oh, uint16_t *ol, hipStream_t s) {
+    const dim3 grid(N / BN, (M + BM - 1) / BM, p->nsplit), block(64 * ring_waves(BM, BN));
+    if (epi == QK_GEMM_STORE)
+        gemm_hilo_ring<QK_GEMM_STORE, BM, BN, NST><<<grid, block, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+    else if (epi == QK_GEMM_ADD)
+        gemm_hilo_ring<QK_GEMM_ADD, BM, BN, NST><<<grid, block, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+    else
+        gemm_hilo_ring<QK_GEMM_SWIGLU, BM, BN, NST><<<grid, block, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
+}
+
+// the ring configurations built: (bm, bn, nst); 0 when the plan names another
+static int gemm_ring_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int N, int K,
+                            const qk_gemm_plan *p, int epi, float *y, uint16_t *oh, uint16_t *ol, hipStream_t s) {
+#define QK_RING(BM_, BN_, NST_)                                                                  \
+    if (p->bm == BM_ && p->bn == BN_ && p->nst == NST_) {                                        \
+        gemm_ring_dispatch<BM_, BN_, NST_>(a_hi, a_lo, W, M, N, K, p, epi, y, oh, ol, s);        \
+        return 1;                                                                                \
+    }
+    QK_RING(64, 128, QK_GEMM_RING_NST) QK_RING(32, 128, QK_GEMM_RING_NST)
+#undef QK_RING
+    return 0;
+}
+
 template <int WGM, int WGN, int TM, int TN>
 static void gemm_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int N, int K,
                           const qk_gemm_plan *p, int epi, float *y, uint16_t *oh, uint16_t *ol, hipStream_t s) {
@@ -414,7 +635,10 @@ static void gemm_dispatch(const uint16_t *a_hi, const uint16_t *a_lo, const uint
         gemm_hilo<WGM, WGN, TM, TN, QK_GEMM_SWIGLU><<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, N, K, p->kc, y, oh, ol);
 }
 
-extern "C" void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p) {
+extern "C" void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p) { qk_gemm_plan_epi(M, N, K, QK_GEMM_STORE, p); }
+
+extern "C" void qk_gemm_plan_epi(int M, int N, int K, int epi, qk_gemm_plan *p) {
+    p->nst = 0;
     // 256 x 256 or 128 x 256 tiles (one block per CU) where they alone fill
     // every CU and the last round of blocks is not mostly empty (>= 85 % of
     // the rounds' slots used); the larger tile first
@@ -428,11 +652,28 @@ extern "C" void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p) {
         p->kc = (K + QK_BK - 1) / QK_BK * QK_BK;
         return;
     }
+    // otherwise 32 x 128 (M <= 32) or 64 x 128 tiles on the LDS ring where the
+    // shape allows it (whole 128-column tiles, K in whole 32-deep steps), else
+    // the register-staged kernel
+    const int ring = N % QK_GEMM_BN == 0 && K % QK_GBK == 0;
     p->bn = QK_GEMM_BN;
-    p->bm = M <= 32 ? 32 : M <= 512 ? 64 : 128;
+    p->bm = M <= 32 ? 32 : (ring || M <= 512) ? 64 : 128;
+    p->nst = ring ? QK_GEMM_RING_NST : 0;
     const long tiles = (long)((M + p->bm - 1) / p->bm) * ((N + QK_GEMM_BN - 1) / QK_GEMM_BN);
     const int kt = (K + QK_BK - 1) / QK_BK;
-    long ns = tiles >= QK_GEMM_TARGET ? 1 : (QK_GEMM_TARGET + tiles - 1) / tiles;
+    long ns;
+    if (ring) {
+        // enough blocks for ~7/8 of the CUs (two ring blocks share a CU, so a
+        // second round is cheap), and k walks of QK_GEMM_RING_KSPLIT or more
+        // in two halves: measured faster even where the tiles alone fill the
+        // chip (more splits cost their consumer more than they save), except
+        // for a SwiGLU product, whose partials (twice the output) need a
+        // reduce pass
+        ns = (QK_GEMM_RING_TARGET + tiles - 1) / tiles;
+        if (ns < 2 && K >= QK_GEMM_RING_KSPLIT && epi != QK_GEMM_SWIGLU) ns = 2;
+    } else {
+        ns = tiles >= QK_GEMM_TARGET ? 1 : (QK_GEMM_TARGET + tiles - 1) / tiles;
+    }
     if (ns > QK_GEMM_MAX_SPLIT) ns = QK_GEMM_MAX_SPLIT;
     if (ns > kt) ns = kt;
     const int per = (int)((kt + ns - 1) / ns);      // k tiles per split
@@ -449,6 +690,11 @@ extern "C" int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const 
         return QWEN_HIP_EINVAL;
     if (p->nsplit > 1 && epi != QK_GEMM_STORE) return QWEN_HIP_EINVAL;
     if (epi == QK_GEMM_SWIGLU ? (!out_hi || !out_lo || (N & 1)) : !y) return QWEN_HIP_EINVAL;
+    if (p->nst) {
+        if (N % p->bn || K % QK_GBK || p->kc % QK_GBK) return QWEN_HIP_EINVAL;
+        if (!gemm_ring_launch(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s)) return QWEN_HIP_EINVAL;
+        return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+    }
     if (p->bn == 256) {
         if ((p->bm != 128 && p->bm != 256) || N % 256 || K % QK_GBK || p->kc % QK_GBK) return QWEN_HIP_EINVAL;
         if (p->bm == 128) gemm_wide_dispatch<128>(a_hi, a_lo, W, M, N, K, p, epi, y, out_hi, out_lo, s);

@@ -221,14 +221,21 @@ int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride,
                             float eps, uint16_t *hi, uint16_t *lo, hipStream_t s);
 
 enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2 };
-/* Tiling of one M x N x K product: block rows bm x columns bn (32 / 64 / 128
- * x QK_GEMM_BN, or 128 x 256 for large M), and nsplit slices of kc (a
- * multiple of 64) along K so a launch has about QK_GEMM_TARGET blocks. */
+/* Tiling of one M x N x K product: block rows bm x columns bn (32 / 64 x
+ * QK_GEMM_BN on the LDS ring of nst stages, 32 / 64 / 128 x QK_GEMM_BN
+ * register-staged (nst 0), or 128 / 256 x 256 for large M), and nsplit slices
+ * of kc (a multiple of 64) along K so a launch has enough blocks. */
 #define QK_GEMM_BN 128
 #define QK_GEMM_TARGET 256
 #define QK_GEMM_MAX_SPLIT 16
-typedef struct { int bm, nsplit, kc, bn; } qk_gemm_plan;
+#define QK_GEMM_RING_NST 4           /* 64 KB of LDS at 64 x 128: two blocks per CU */
+#define QK_GEMM_RING_TARGET 224      /* blocks a ring launch aims for */
+#define QK_GEMM_RING_KSPLIT 2048     /* ring k walks this long or longer: two splits at least */
+typedef struct { int bm, nsplit, kc, bn, nst; } qk_gemm_plan;
 void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p);
+/* the plan for a product with epilogue epi: a SWIGLU product splits K only
+ * to fill the chip (its split partials need a reduce pass) */
+void qk_gemm_plan_epi(int M, int N, int K, int epi, qk_gemm_plan *p);
 /* Y[M][N] (=, +=) (A_hi + A_lo)[M][K] . W[N][K]^T on bf16 MFMA with fp32
  * accumulation; SWIGLU writes silu(Y[:,2j]) * Y[:,2j+1] as a bf16 hi/lo
  * split [M][N/2] into out_hi/out_lo.  With nsplit > 1 only STORE is allowed

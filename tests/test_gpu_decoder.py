@@ -128,7 +128,7 @@ def test_long_prefill_wide_kernels(P, qa, gpu):
     import ctypes as C
 
     class GemmPlan(C.Structure):
-        _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int)]
+        _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int), ("nst", C.c_int)]
 
     lib = qa.lib()
     S = 4095

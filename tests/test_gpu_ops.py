@@ -95,22 +95,26 @@ def test_gemm_hilo(P, qa, gpu, M, N, K):
 
 
 class GemmPlan(C.Structure):
-    _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int)]
+    _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int), ("nst", C.c_int)]
 
 
-# the three epilogues of the prefill GEMM on every tile shape it plans:
-# 256 x 256 and 128 x 256 (direct-to-LDS rings; M not a multiple of the tile,
-# k walks shorter than the ring), 64 x 128 and split 128 x 128 (STORE into
-# partials, summed by the reduce pass with the epilogue)
-@pytest.mark.parametrize("M,N,K,bm,bn", [(1000, 16384, 64, 256, 256), (4000, 4096, 96, 256, 256),
-                                         (4000, 2048, 96, 128, 256), (2000, 4096, 32, 128, 256),
-                                         (401, 6144, 1024, 64, 128), (1515, 1024, 512, 128, 128)])
+# the three epilogues of the prefill GEMM on every tile shape and kernel it
+# plans: 256 x 256 and 128 x 256 (wide direct-to-LDS rings; M not a multiple
+# of the tile, k walks shorter than the ring), 64 x 128 and 32 x 128 on the
+# 4-stage ring (one split, and split with the partials summed by the reduce
+# pass with the epilogue), register-staged 64 x 128 and split 128 x 128 (N
+# not a multiple of 128, K not of 32)
+@pytest.mark.parametrize("M,N,K,bm,bn,nst", [(1000, 16384, 64, 256, 256, 0), (4000, 4096, 96, 256, 256, 0),
+                                             (4000, 2048, 96, 128, 256, 0), (2000, 4096, 32, 128, 256, 0),
+                                             (401, 6144, 1024, 64, 128, 4), (1515, 1024, 512, 64, 128, 4),
+                                             (31, 4096, 1024, 32, 128, 4), (100, 1000, 512, 64, 128, 0),
+                                             (1515, 1000, 520, 128, 128, 0)])
 @pytest.mark.parametrize("epi", [0, 1, 2])
-def test_gemm_epilogues(P, qa, gpu, M, N, K, bm, bn, epi):
+def test_gemm_epilogues(P, qa, gpu, M, N, K, bm, bn, nst, epi):
     lib = qa.lib()
     p = GemmPlan()
     lib.qk_gemm_plan_for(M, N, K, C.byref(p))
-    assert (p.bm, p.bn) == (bm, bn), (p.bm, p.bn, p.nsplit)
+    assert (p.bm, p.bn, p.nst) == (bm, bn, nst), (p.bm, p.bn, p.nst, p.nsplit)
     W = P.synth_bf16(N * K, 2, 9400 + N).reshape(N, K)
     x = P.synth_f32(M * K, 2, 9500 + M).reshape(M, K)
     hi = P.f32_to_bf16(x)

@@ -1,5 +1,5 @@
 """Launch planners of the prefill kernels (host code, no GPU needed):
-qk_gemm_plan_for (tile shape, split-K slices of the projection GEMMs) and
+qk_gemm_plan_for (tile shape, kernel, split-K slices of the projection GEMMs) and
 qk_attn_prefill_plan (key chunk per block of the prefill attention).  Their
 invariants are what the kernels rely on: slices cover K exactly once in whole
 64-deep k tiles, at most 16 of them (the partial-sum consumers' bound); key
@@ -12,11 +12,11 @@ import pytest
 
 
 class GemmPlan(C.Structure):
-    _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int)]
+    _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int), ("nst", C.c_int)]
 
 
 SHAPES = [(M, N, K) for M in (1, 17, 31, 32, 33, 64, 65, 401, 512, 513, 1515, 8191)
-          for N in (1024, 2048, 4096, 6144, 12288) for K in (1024, 2048, 3072, 6144)]
+          for N in (1000, 1024, 2048, 4096, 6144, 12288) for K in (520, 1024, 2048, 3072, 6144)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -26,18 +26,45 @@ def test_gemm_plan_invariants(qa, M, N, K):
     def fills(bm):   # bm x 256 tiles alone fill the CUs, last round >= 85 % used
         wt = -(-M // bm) * (N // 256)
         return M > 512 and N % 256 == 0 and K % 32 == 0 and wt >= 256 and wt * 100 >= -(-wt // 256) * 256 * 85
+    ring = N % 128 == 0 and K % 32 == 0
     if fills(256):                                                     # wide tiles, never split
-        assert (p.bm, p.bn, p.nsplit) == (256, 256, 1)
+        assert (p.bm, p.bn, p.nsplit, p.nst) == (256, 256, 1, 0)
     elif fills(128):
-        assert (p.bm, p.bn, p.nsplit) == (128, 256, 1)
-    else:
-        assert p.bn == 128 and p.bm == (32 if M <= 32 else 64 if M <= 512 else 128)
+        assert (p.bm, p.bn, p.nsplit, p.nst) == (128, 256, 1, 0)
+    elif ring:                                                         # LDS ring, 4 stages
+        assert (p.bn, p.nst) == (128, 4) and p.bm == (32 if M <= 32 else 64)
+    else:                                                              # register-staged
+        assert p.bn == 128 and p.nst == 0 and p.bm == (32 if M <= 32 else 64 if M <= 512 else 128)
     assert p.kc > 0 and p.kc % 64 == 0
     assert 1 <= p.nsplit <= 16
     assert p.kc * p.nsplit >= K and p.kc * (p.nsplit - 1) < K       # every slice non-empty, K covered once
     tiles = -(-M // p.bm) * -(-N // p.bn)
-    if tiles >= 256:
+    if p.nst:
+        # about 224 blocks, and k walks of 2048 or more in two halves at least
+        # (within the 16-split cap and whole 64-deep k tiles)
+        want = min(max(-(-224 // tiles), 2 if K >= 2048 else 1), 16, -(-K // 64))
+        assert p.kc == -(-(-(-K // 64)) // want) * 64                 # whole k tiles, want slices at most
+    elif tiles >= 256:
         assert p.nsplit == 1                                           # the grid alone fills the chip
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_plan_swiglu(qa, M, N, K):
+    """A SwiGLU product (epilogue 2) splits K only to fill the chip: its split
+    partials (twice its output) need a reduce pass; otherwise it is planned
+    like any other product."""
+    lib = qa.lib()
+    p, q = GemmPlan(), GemmPlan()
+    lib.qk_gemm_plan_for(M, N, K, C.byref(p))
+    lib.qk_gemm_plan_epi(M, N, K, 2, C.byref(q))
+    assert (q.bm, q.bn, q.nst) == (p.bm, p.bn, p.nst)
+    assert q.kc * q.nsplit >= K and q.kc * (q.nsplit - 1) < K and q.kc % 64 == 0
+    if p.nst:
+        tiles = -(-M // p.bm) * (N // p.bn)
+        want = min(-(-224 // tiles), 16, -(-K // 64))
+        assert q.kc == -(-(-(-K // 64)) // want) * 64
+    else:
+        assert (q.nsplit, q.kc) == (p.nsplit, p.kc)
 
 
 def kmax_of(seq_q, seq_k, q_offset):
