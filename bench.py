@@ -290,6 +290,11 @@ def prefill_rates(cfg, rows, seconds):
     return {"rows": rows, "ms": round(seconds * 1e3, 3), "fp32_equiv_tflops": round((proj + attn) / seconds / 1e12, 2),
             "mfma_tflops": round(mfma / seconds / 1e12, 2),
             "mfma_frac": round(mfma / seconds / 1e12 / BF16_MFMA_PEAK_TFS, 4),
+            "arithmetic": "projections: each fp32 activation carried as bf16 hi + lo (|x - hi - lo| <= 2^-17 |x|) "
+                          "against the bf16-exact weights, 2 bf16 MFMA products per term, fp32 accumulation; "
+                          "attention: Q, K, V, P split the same way, hi.hi + hi.lo + lo.hi (3 products per term, "
+                          "~2^-16 relative per product); softmax statistics and outputs fp32; the reference runs "
+                          "fp32 SGEMM (2^-24)",
             "note": "whole prefill (projections x2 hi/lo and attention x3 bf16 MFMA work) over the median wall time"}
 
 
