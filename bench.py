@@ -52,6 +52,7 @@ WORKLOADS = {
 }
 C5_CHUNKS, C5_AUDIO, C5_ROLLBACK, C5_STEPS, C5_CAP, C5_HEAD, C5_KEEP = 60, 26, 5, 24, 1024, 9, 3
 HBM_PEAK_GBS = 8000.0
+CPU_MAX_PREFILL, CPU_SAMPLE_ROWS = 1536, 1024   # CPU baseline: longer prefills are sampled
 PREFILL_REPS = 5
 
 
@@ -404,9 +405,15 @@ def cpu_baseline(wl, rows, first_token, threads, decode_steps):
     t0 = time.time()
     m = P.SynthModel(cfg, seed=0)
     r = P.RefModel(m, threads=threads)
-    log(f"[cpu] weights generated in {time.time() - t0:.1f}s; prefill {rows.shape[0] - 1} rows on {threads} threads")
-    tp = r.time_prefill(rows[:-1])
-    tok, _, _ = r.forward(rows[-1])
+    # a long prefill (C4: 8191 rows) would take the reference's non-BLAS loop
+    # many minutes: the sample then prefills the first CPU_SAMPLE_ROWS rows
+    n = rows.shape[0] - 1
+    sampled = n > CPU_MAX_PREFILL
+    pre = rows[:CPU_SAMPLE_ROWS] if sampled else rows[:-1]
+    last = rows[CPU_SAMPLE_ROWS] if sampled else rows[-1]
+    log(f"[cpu] weights generated in {time.time() - t0:.1f}s; prefill {pre.shape[0]} rows on {threads} threads")
+    tp = r.time_prefill(pre)
+    tok, _, _ = r.forward(last)
     base = r.kv_len()
     toks, td = r.generate(first_token, decode_steps)
     r.set_kv_len(base)
@@ -419,16 +426,19 @@ def cpu_baseline(wl, rows, first_token, threads, decode_steps):
     log(f"[cpu] prefill {tp:.1f}s, {decode_steps} decode steps {td:.2f}s (first token {tok}); 1 thread: "
         f"{CPU_1T_STEPS} steps {td1:.2f}s; triad {bw:.1f} GB/s ({threads} thr), {bw1:.1f} GB/s (1 thr); {host}")
     return {"value": round(decode_steps / td, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "prefill_tok_s": round((rows.shape[0] - 1) / tp, 2),
+            "prefill_tok_s": round(pre.shape[0] / tp, 2),
             "one_thread": {"value": round(CPU_1T_STEPS / td1, 3), "unit": "tok/s", "cores": 1,
                            "steps": CPU_1T_STEPS,
                            "same_tokens": bool(list(toks1[:len(toks)]) == list(toks[:len(toks1)]))},
             "cpu_model": host["cpu_model"], "logical_cpus": host["logical_cpus"], "isa": host["isa"],
             "host_triad_gb_s": {str(threads): round(bw, 1), "1": round(bw1, 1)},
             "blas": REF_BLAS,
-            "sample": f"reference decoder (oracle/_ref, no BLAS) on the same weights/rows: prefill "
-                      f"{rows.shape[0] - 1} rows, then {decode_steps} greedy decode steps; decode tok/s over those steps",
-            "first_token_matches_gpu": bool(tok == first_token)}
+            "sample": (f"reference decoder (oracle/_ref, no BLAS) on the same weights/rows: prefill "
+                       f"{pre.shape[0]} rows" + (f" (the first {pre.shape[0]} of the {n}: a bounded sample, so its decode "
+                                                  f"steps run at {pre.shape[0] + 1}+ positions against the GPU's {n + 1}+)"
+                                                  if sampled else "") +
+                       f", then {decode_steps} greedy decode steps; decode tok/s over those steps"),
+            "first_token_matches_gpu": None if sampled else bool(tok == first_token)}
 
 
 def launch_fields(engine, K, step_bytes, gpu_ms):

@@ -527,7 +527,8 @@ static int prefill_layers(qwen_hip_decoder *d, int S) {
     /* GEMM tilings; with split-K the partials go to pgemm and their consumer
      * (RoPE/append, the next RMSNorm, the SwiGLU reduce) sums them in order */
     qk_gemm_plan gq, go, gg, gd;
-    qk_gemm_plan_for(S, d->qkv_rows, D, &gq);
+    qk_gemm_plan_epi(S, d->qkv_rows, D, QK_GEMM_ROPE, &gq);
+    const int rope_fused = qk_gemm_rope_fusable(&gq);   /* RoPE / append in the Q|K|V epilogue */
     qk_gemm_plan_for(S, D, d->qd, &go);
     qk_gemm_plan_epi(S, 2 * I, D, QK_GEMM_SWIGLU, &gg);
     qk_gemm_plan_for(S, D, I, &gd);
@@ -560,14 +561,18 @@ static int prefill_layers(qwen_hip_decoder *d, int S) {
         /* input RMSNorm (completing the previous layer's residual first) + Q|K|V */
         QK_TRY(qk_rmsnorm_split_launch(d->px, d->pgemm, pending, (long)S * D, d->n_in[l], S, D, c->rms_eps,
                                        d->pxh, d->pxl, s));
-        QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_qkv[l], S, d->qkv_rows, D, &gq, QK_GEMM_STORE, qkv, NULL, NULL,
-                              s));
         qk_rope_append_args ra = {
             .qkv = qkv, .nsum = gq.nsplit, .pstride = (long)S * d->qkv_rows, .q_norm = d->n_q[l],
             .k_norm = d->n_k[l], .eps = c->rms_eps, .rope_cos = d->rope_cos, .rope_sin = d->rope_sin,
             .k_cache = kc_layer(d, l), .v_cache = vc_layer(d, l), .cap = d->kv_cap, .pos_dev = NULL,
             .start = start, .S = S, .heads = c->heads, .kv_heads = c->kv_heads, .q_out = d->pqrot};
-        QK_TRY(qk_rope_append_launch(&ra, s));
+        if (rope_fused) {
+            QK_TRY(qk_gemm_rope_launch(d->pxh, d->pxl, d->w_qkv[l], S, D, &gq, &ra, s));
+        } else {
+            QK_TRY(qk_gemm_launch(d->pxh, d->pxl, d->w_qkv[l], S, d->qkv_rows, D, &gq, QK_GEMM_STORE, qkv, NULL,
+                                  NULL, s));
+            QK_TRY(qk_rope_append_launch(&ra, s));
+        }
         qk_attn_args aa = {
             .q = d->pqrot, .k = kc_layer(d, l), .v = vc_layer(d, l), .pos_stride = hd,
             .head_stride = (long)d->kv_cap * hd, .pos_dev = NULL, .seq_k = start + S, .seq_q = S,

@@ -497,18 +497,27 @@ __device__ __forceinline__ void lds_load16(const uint16_t *g, unsigned char *l0)
     __builtin_amdgcn_global_load_lds(g, l0, 16, 0, 0);
 }
 
-template <int EPI, int BM, int BN, int NST>
-__global__ __launch_bounds__(ring_waves(BM, BN) * 64) void gemm_hilo_ring(const uint16_t *__restrict__ ahi,
-                                                                           const uint16_t *__restrict__ alo,
-                                                                           const uint16_t *__restrict__ W, int M,
-                                                                           int N, int K, int kc, float *y,
-                                                                           uint16_t *ohi, uint16_t *olo) {
-    constexpr int NW = ring_waves(BM, BN), WGM = BM / 32, WGN = NW / WGM, WTN = BN / WGN, TM = 2, TN = WTN / 16;
-    constexpr int AB = BM * 64, STAGE = 2 * AB + BN * 64;   // bytes: one A half, one stage
-    constexpr int GROUPS = (2 * BM + BN) / 16, LPW = GROUPS / NW;
+template <int BM, int BN>
+struct RingShape {
+    static constexpr int NW = ring_waves(BM, BN), WGM = BM / 32, WGN = NW / WGM, WTN = BN / WGN, TM = 2,
+                         TN = WTN / 16;
+    static constexpr int AB = BM * 64, STAGE = 2 * AB + BN * 64;   // bytes: one A half, one stage
+    static constexpr int GROUPS = (2 * BM + BN) / 16, LPW = GROUPS / NW;
     static_assert(WGM * WGN == NW && WTN % 16 == 0 && GROUPS % NW == 0, "wave grid / load split");
+};
+
+// The k walk of block (blockIdx.x, blockIdx.y, blockIdx.z) into acc: wave
+// (wm, wn) = (wave / WGN, wave % WGN) holds rows m0 + 32 wm + 16 i + 4 (l >> 4)
+// + r, columns n0 + WTN wn + 16 j + (l & 15) (lane l, acc[i][j][r]).  lds:
+// NST stages of the kernel's shared memory.
+template <int BM, int BN, int NST>
+__device__ __forceinline__ void ring_tile(const uint16_t *__restrict__ ahi, const uint16_t *__restrict__ alo,
+                                          const uint16_t *__restrict__ W, int M, int K, int kc, unsigned char *lds,
+                                          f32x4 (&acc)[2][RingShape<BM, BN>::TN]) {
+    using RS = RingShape<BM, BN>;
+    constexpr int NW = RS::NW, WGN = RS::WGN, WTN = RS::WTN, TM = RS::TM, TN = RS::TN;
+    constexpr int AB = RS::AB, STAGE = RS::STAGE, LPW = RS::LPW;
     static_assert((NST - 2) * LPW <= 63 && NST * STAGE <= 160 * 1024, "vmcnt / LDS range");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[NST][STAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
@@ -536,12 +545,11 @@ __global__ __launch_bounds__(ring_waves(BM, BN) * 64) void gemm_hilo_ring(const 
         }
     }
     auto issue = [&](int kt) {
-        unsigned char *st = lds[kt % NST];
+        unsigned char *st = lds + (kt % NST) * STAGE;
 #pragma unroll
         for (int j = 0; j < LPW; j++) lds_load16(src[j] + kt * QK_GBK, st + dst[j]);
     };
 
-    f32x4 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -556,7 +564,7 @@ __global__ __launch_bounds__(ring_waves(BM, BN) * 64) void gemm_hilo_ring(const 
         // plain s_barrier: __syncthreads() would also drain the later stages)
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (kt + NST - 1 < nk) issue(kt + NST - 1);
-        const unsigned char *st = lds[kt % NST];
+        const unsigned char *st = lds + (kt % NST) * STAGE;
         bf16x8 bfr[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++)
@@ -572,7 +580,22 @@ __global__ __launch_bounds__(ring_waves(BM, BN) * 64) void gemm_hilo_ring(const 
             for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bfr[j], acc[i][j], 0, 0, 0);
         }
     }
+}
 
+template <int EPI, int BM, int BN, int NST>
+__global__ __launch_bounds__(ring_waves(BM, BN) * 64) void gemm_hilo_ring(const uint16_t *__restrict__ ahi,
+                                                                           const uint16_t *__restrict__ alo,
+                                                                           const uint16_t *__restrict__ W, int M,
+                                                                           int N, int K, int kc, float *y,
+                                                                           uint16_t *ohi, uint16_t *olo) {
+    using RS = RingShape<BM, BN>;
+    constexpr int WGN = RS::WGN, WTN = RS::WTN, TM = RS::TM, TN = RS::TN;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[NST * RS::STAGE];
+    f32x4 acc[TM][TN];
+    ring_tile<BM, BN, NST>(ahi, alo, W, M, K, kc, lds, acc);
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     float *yz = y + (EPI == QK_GEMM_STORE ? (size_t)blockIdx.z * M * N : 0);
 #pragma unroll
     for (int i = 0; i < TM; i++) {
@@ -596,6 +619,101 @@ __global__ __launch_bounds__(ring_waves(BM, BN) * 64) void gemm_hilo_ring(const 
             }
         }
     }
+}
+
+// Q|K|V projection with the RoPE / append epilogue (the work of rope_append
+// on the product, reference qwen_asr_decoder.c:270-300): a 64 x 128 tile is
+// 64 rows of one head (Q heads, then K heads, then V heads along N).  The
+// tile goes to LDS (the ring is free after the k walk), then each wave takes
+// 16 rows and runs rope_append's per-row code on them: per-head RMSNorm and
+// NeoX rotation of dims (d, d + 64) for Q and K (Q to q_out, K to the cache),
+// V copied to the cache.  The sums and products are rope_append's, so the
+// result equals GEMM (STORE, one split) + rope_append bit for bit.
+#define RP_ROW (QWEN_HIP_HEAD_DIM + 4)        // floats per row of the staged tile
+__global__ __launch_bounds__(256) void gemm_hilo_ring_rope(const uint16_t *__restrict__ ahi,
+                                                           const uint16_t *__restrict__ alo,
+                                                           const uint16_t *__restrict__ W, int M, int K,
+                                                           qk_rope_append_args ra) {
+    using RS = RingShape<64, QWEN_HIP_HEAD_DIM>;
+    constexpr int WGN = RS::WGN, WTN = RS::WTN, TM = RS::TM, TN = RS::TN, hd = QWEN_HIP_HEAD_DIM, half = hd / 2;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[QK_GEMM_RING_NST * RS::STAGE];
+    static_assert(64 * RP_ROW * sizeof(float) <= sizeof(lds), "staged tile");
+    f32x4 acc[TM][TN];
+    ring_tile<64, QWEN_HIP_HEAD_DIM, QK_GEMM_RING_NST>(ahi, alo, W, M, K, K, lds, acc);
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int m0 = blockIdx.y * 64, head = blockIdx.x;
+
+    __syncthreads();                                   // every wave is past its last k step
+    float *T = reinterpret_cast<float *>(lds);         // [64][RP_ROW]
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                T[(wm * 32 + i * 16 + 4 * (lane >> 4) + r) * RP_ROW + wn * WTN + j * 16 + (lane & 15)] = acc[i][j][r];
+    __syncthreads();
+
+    const int nqk = ra.heads + ra.kv_heads, qd = ra.heads * hd;
+    const bool is_q = head < ra.heads, is_k = !is_q && head < nqk;
+    const int rl0 = 16 * wave;                        // this wave's 16 rows of the tile
+    if (is_q || is_k) {
+        // the rows' cos / sin and the norm weights are loaded up front, so the
+        // row loop below waits for memory once
+        const float *nw = is_q ? ra.q_norm : ra.k_norm;
+        const float w1 = nw[lane], w2 = nw[lane + half];
+        float cv[16], sv[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const size_t p = (size_t)ra.start + min(m0 + rl0 + k, M - 1);
+            cv[k] = ra.rope_cos[p * hd + lane];
+            sv[k] = ra.rope_sin[p * hd + lane];
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int rl = rl0 + k, srow = m0 + rl;
+            if (srow < M) {                           // wave-uniform
+                float x1 = T[rl * RP_ROW + lane], x2 = T[rl * RP_ROW + lane + half];
+                const float ss = wave_sum(fmaf(x1, x1, x2 * x2));
+                const float rinv = 1.0f / sqrtf(ss / (float)hd + ra.eps);
+                x1 = (x1 * w1) * rinv;
+                x2 = (x2 * w2) * rinv;
+                const float r1 = fmaf(x1, cv[k], -(x2 * sv[k]));
+                const float r2 = fmaf(x2, cv[k], x1 * sv[k]);
+                float *d = is_q ? ra.q_out + (size_t)srow * qd + head * hd
+                                : ra.k_cache + ((size_t)(head - ra.heads) * ra.cap + ra.start + srow) * hd;
+                d[lane] = r1;
+                d[lane + half] = r2;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int rl = rl0 + k, srow = m0 + rl;
+            if (srow < M) {
+                float *d = ra.v_cache + ((size_t)(head - nqk) * ra.cap + ra.start + srow) * hd;
+                d[lane] = T[rl * RP_ROW + lane];
+                d[lane + half] = T[rl * RP_ROW + lane + half];
+            }
+        }
+    }
+}
+
+extern "C" int qk_gemm_rope_fusable(const qk_gemm_plan *p) {
+    return p && p->nst == QK_GEMM_RING_NST && p->bm == 64 && p->bn == QK_GEMM_BN && p->nsplit == 1;
+}
+
+extern "C" int qk_gemm_rope_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int K,
+                                   const qk_gemm_plan *p, const qk_rope_append_args *ra, hipStream_t s) {
+    if (M <= 0 || K <= 0 || K % QK_GBK || !a_hi || !a_lo || !W || !ra || !qk_gemm_rope_fusable(p) ||
+        p->kc < K || ra->S != M || ra->pos_dev || ra->nsum > 1 || ra->heads <= 0 || ra->kv_heads <= 0 ||
+        ra->heads % ra->kv_heads || !ra->q_norm || !ra->k_norm || !ra->rope_cos || !ra->rope_sin ||
+        !ra->k_cache || !ra->v_cache || !ra->q_out || ra->start < 0 || ra->start + M > ra->cap)
+        return QWEN_HIP_EINVAL;
+    const dim3 grid(ra->heads + 2 * ra->kv_heads, (M + 63) / 64);
+    gemm_hilo_ring_rope<<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, K, *ra);
+    return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 
 template <int BM, int BN, int NST>
@@ -668,9 +786,9 @@ extern "C" void qk_gemm_plan_epi(int M, int N, int K, int epi, qk_gemm_plan *p) 
         // in two halves: measured faster even where the tiles alone fill the
         // chip (more splits cost their consumer more than they save), except
         // for a SwiGLU product, whose partials (twice the output) need a
-        // reduce pass
+        // reduce pass, and a Q|K|V product whose RoPE epilogue needs one split
         ns = (QK_GEMM_RING_TARGET + tiles - 1) / tiles;
-        if (ns < 2 && K >= QK_GEMM_RING_KSPLIT && epi != QK_GEMM_SWIGLU) ns = 2;
+        if (ns < 2 && K >= QK_GEMM_RING_KSPLIT && epi != QK_GEMM_SWIGLU && epi != QK_GEMM_ROPE) ns = 2;
     } else {
         ns = tiles >= QK_GEMM_TARGET ? 1 : (QK_GEMM_TARGET + tiles - 1) / tiles;
     }

@@ -220,7 +220,7 @@ int qk_persist_launch(const qk_persist_args *a, int hidden, int inter, hipStream
 int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride, const float *w, int S, int D,
                             float eps, uint16_t *hi, uint16_t *lo, hipStream_t s);
 
-enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2 };
+enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2, QK_GEMM_ROPE = 3 /* plans only */ };
 /* Tiling of one M x N x K product: block rows bm x columns bn (32 / 64 x
  * QK_GEMM_BN on the LDS ring of nst stages, 32 / 64 / 128 x QK_GEMM_BN
  * register-staged (nst 0), or 128 / 256 x 256 for large M), and nsplit slices
@@ -234,7 +234,8 @@ enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2 };
 typedef struct { int bm, nsplit, kc, bn, nst; } qk_gemm_plan;
 void qk_gemm_plan_for(int M, int N, int K, qk_gemm_plan *p);
 /* the plan for a product with epilogue epi: a SWIGLU product splits K only
- * to fill the chip (its split partials need a reduce pass) */
+ * to fill the chip (its split partials need a reduce pass), and so does a
+ * ROPE one (the Q|K|V product of qk_gemm_rope_launch) */
 void qk_gemm_plan_epi(int M, int N, int K, int epi, qk_gemm_plan *p);
 /* Y[M][N] (=, +=) (A_hi + A_lo)[M][K] . W[N][K]^T on bf16 MFMA with fp32
  * accumulation; SWIGLU writes silu(Y[:,2j]) * Y[:,2j+1] as a bf16 hi/lo
@@ -245,6 +246,13 @@ int qk_gemm_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W
 /* Sum nsum partials [nsum][M][N] in order and apply epi (N even). */
 int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, float *y, uint16_t *out_hi,
                           uint16_t *out_lo, hipStream_t s);
+/* Q|K|V product (A hi/lo [M][K] . W[(heads + 2 kv_heads) 128][K]^T) with
+ * rope_append's work as its epilogue (qkv / nsum unused, pos_dev NULL, S ==
+ * M): bit for bit qk_gemm_launch(STORE) + qk_rope_append_launch.  Only for
+ * plans with qk_gemm_rope_fusable (64 x 128 ring tiles, one split). */
+int qk_gemm_rope_fusable(const qk_gemm_plan *p);
+int qk_gemm_rope_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int K,
+                        const qk_gemm_plan *p, const qk_rope_append_args *ra, hipStream_t s);
 /* y[S][out] = x[S][in] . W[out][in]^T for S > 1 (the op-level linear's
  * product path, csrc/host/ops.c): split x to bf16 hi/lo, GEMM, split-K reduce,
  * all launched on s with ws (>= qk_linear_ws_bytes bytes) as the only

@@ -154,6 +154,64 @@ def test_gemm_epilogues(P, qa, gpu, M, N, K, bm, bn, nst, epi):
         assert np.all(np.abs(got - exp) <= tol), float(np.max(np.abs(got - exp) / tol))
 
 
+class RopeArgs(C.Structure):
+    _fields_ = [("qkv", C.c_void_p), ("nsum", C.c_int), ("pstride", C.c_long), ("q_norm", C.c_void_p),
+                ("k_norm", C.c_void_p), ("eps", C.c_float), ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+                ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("cap", C.c_int), ("pos_dev", C.c_void_p),
+                ("start", C.c_int), ("S", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int), ("q_out", C.c_void_p)]
+
+
+# the Q|K|V GEMM with rope_append's work as its epilogue: bit for bit the
+# GEMM (STORE) followed by rope_append, on a full and a partial last row tile,
+# at a nonzero start position, for the 0.6B and 1.7B widths
+@pytest.mark.parametrize("M,K,start", [(401, 1024, 37), (130, 2048, 0), (64, 1024, 900)])
+def test_gemm_rope_epilogue(P, qa, gpu, M, K, start):
+    lib = qa.lib()
+    H, KVH, hd, cap = 16, 8, 128, 1024
+    N = (H + 2 * KVH) * hd
+    p = GemmPlan()
+    lib.qk_gemm_plan_epi(M, N, K, 3, C.byref(p))
+    # the plan fuses where the tiles fill the chip without a split (C1's 401
+    # rows, 7 x 32 tiles); the kernel takes any M with one split
+    assert lib.qk_gemm_rope_fusable(C.byref(p)) == (1 if M >= 385 else 0), (p.bm, p.bn, p.nst, p.nsplit)
+    p = GemmPlan(64, 1, K, 128, 4)
+    r = np.random.default_rng(M + K)
+    W = P.synth_bf16(N * K, 3, 9700 + K).reshape(N, K)
+    x = P.synth_f32(M * K, 3, 9800 + M).reshape(M, K)
+    hi = P.f32_to_bf16(x)
+    lo = P.f32_to_bf16(x - P.bf16_to_f32(hi))
+    qn = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+    cs = np.empty((cap, hd), np.float32)
+    sn = np.empty((cap, hd), np.float32)
+    P.orc_lib().orc_rope_table(cs, sn, cap, hd, 1e6)
+    dh, dl, dW = dev(gpu, hi.view(np.int16)), dev(gpu, lo.view(np.int16)), dev(gpu, W.view(np.int16))
+    dqn, dkn, dcs, dsn = dev(gpu, qn), dev(gpu, kn), dev(gpu, cs), dev(gpu, sn)
+    outs = []
+    for fused in (False, True):
+        kc = gpu.full((KVH, cap, hd), 7.0, dtype=gpu.float32, device="cuda")
+        vc = gpu.full((KVH, cap, hd), 7.0, dtype=gpu.float32, device="cuda")
+        qo = gpu.full((M, H * hd), 7.0, dtype=gpu.float32, device="cuda")
+        qkv = gpu.empty((M, N), dtype=gpu.float32, device="cuda")
+        ra = RopeArgs(ptr(qkv), 1, M * N, ptr(dqn), ptr(dkn), 1e-6, ptr(dcs), ptr(dsn), ptr(kc), ptr(vc), cap, None,
+                      start, M, H, KVH, ptr(qo))
+        if fused:
+            lib.qk_gemm_rope_launch.argtypes = [C.c_void_p] * 3 + [C.c_int] * 2 + [C.c_void_p] * 3
+            qa.check(lib.qk_gemm_rope_launch(ptr(dh), ptr(dl), ptr(dW), M, K, C.byref(p), C.byref(ra), None), "fused")
+        else:
+            lib.qk_gemm_launch.argtypes = [C.c_void_p] * 3 + [C.c_int] * 3 + [C.c_void_p, C.c_int] + [C.c_void_p] * 4
+            lib.qk_rope_append_launch.argtypes = [C.c_void_p, C.c_void_p]
+            qa.check(lib.qk_gemm_launch(ptr(dh), ptr(dl), ptr(dW), M, N, K, C.byref(p), 0, ptr(qkv), None, None,
+                                        None), "gemm")
+            qa.check(lib.qk_rope_append_launch(C.byref(ra), None), "rope_append")
+        gpu.cuda.synchronize()
+        outs.append((host(kc), host(vc), host(qo)))
+    for a, b, what in zip(outs[0], outs[1], ("k cache", "v cache", "q")):
+        assert np.array_equal(a, b), what
+    # the rows outside [start, start + M) are untouched
+    assert np.all(outs[1][0][:, :start] == 7.0) and np.all(outs[1][0][:, start + M:] == 7.0)
+
+
 def test_elementwise_ops(P, qa, gpu):
     lib, orc = qa.lib(), P.orc_lib()
     r = np.random.default_rng(0)

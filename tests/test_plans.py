@@ -48,15 +48,17 @@ def test_gemm_plan_invariants(qa, M, N, K):
         assert p.nsplit == 1                                           # the grid alone fills the chip
 
 
+@pytest.mark.parametrize("epi", [2, 3])
 @pytest.mark.parametrize("M,N,K", SHAPES)
-def test_gemm_plan_swiglu(qa, M, N, K):
-    """A SwiGLU product (epilogue 2) splits K only to fill the chip: its split
-    partials (twice its output) need a reduce pass; otherwise it is planned
-    like any other product."""
+def test_gemm_plan_swiglu_rope(qa, M, N, K, epi):
+    """A SwiGLU product (epilogue 2) and the Q|K|V product with the RoPE
+    epilogue (3) split K only to fill the chip: SwiGLU's split partials (twice
+    its output) need a reduce pass, and the RoPE epilogue runs on one split;
+    otherwise they are planned like any other product."""
     lib = qa.lib()
     p, q = GemmPlan(), GemmPlan()
     lib.qk_gemm_plan_for(M, N, K, C.byref(p))
-    lib.qk_gemm_plan_epi(M, N, K, 2, C.byref(q))
+    lib.qk_gemm_plan_epi(M, N, K, epi, C.byref(q))
     assert (q.bm, q.bn, q.nst) == (p.bm, p.bn, p.nst)
     assert q.kc * q.nsplit >= K and q.kc * (q.nsplit - 1) < K and q.kc % 64 == 0
     if p.nst:
@@ -65,6 +67,8 @@ def test_gemm_plan_swiglu(qa, M, N, K):
         assert q.kc == -(-(-(-K // 64)) // want) * 64
     else:
         assert (q.nsplit, q.kc) == (p.nsplit, p.kc)
+    # the fused Q|K|V + RoPE kernel takes exactly the one-split 64 x 128 ring plans
+    assert lib.qk_gemm_rope_fusable(C.byref(q)) == int((q.nst, q.bm, q.bn, q.nsplit) == (4, 64, 128, 1))
 
 
 def kmax_of(seq_q, seq_k, q_offset):
