@@ -369,6 +369,15 @@ extern "C" size_t qk_attn_prefill_plan(int seq_q, int seq_k, int q_offset, int h
     long cap = ((kmax + 5) / 6 + PF_KT - 1) / PF_KT * PF_KT;
     if (cap < 256) cap = 256;
     if (c > cap) c = cap;
+    // with several query tiles and up to 2048 keys, splits of a quarter of the
+    // longest key range (nearest 32) at least: every split adds partials and a
+    // merge pass (7 us at 401 rows), and the tiles themselves already spread
+    // the work (C1 401 rows: 96-key splits 26.1 us against 32-key 28.3; C3
+    // 1515 rows: 384-key 78.5 us against 224-key ~87, attention + merge)
+    if (nq >= 4 && kmax <= 2048) {
+        long q4 = (kmax / 4 + PF_KT / 2) / PF_KT * PF_KT;
+        if (c < q4) c = q4;
+    }
     // with two (query tile, kv head) blocks per CU or more, the longest-first
     // order alone balances the CUs: no split, so no partials and no merge pass
     if ((long)nq * kv_heads >= 2L * 256) c = (kmax + PF_KT - 1) / PF_KT * PF_KT;

@@ -4,8 +4,10 @@ qk_attn_prefill_plan (key chunk per block of the prefill attention).  Their
 invariants are what the kernels rely on: slices cover K exactly once in whole
 64-deep k tiles, at most 16 of them (the partial-sum consumers' bound); key
 chunks are whole 32-key tiles, cover the longest query tile, and no block
-walks more than max(256, a sixth of it) keys, except that a prefill with at
-least two (64-query tile, kv head) blocks per CU is not split at all."""
+walks more than max(256, a sixth of it) keys, except that with four or more
+query tiles and up to 2048 keys a split covers a quarter of the longest range
+at least, and a prefill with at least two (64-query tile, kv head) blocks per
+CU is not split at all."""
 import ctypes as C
 
 import pytest
@@ -89,8 +91,12 @@ def test_attention_plan_invariants(qa, seq_q, seq_k, q_offset):
     assert chunk.value > 0 and chunk.value % 32 == 0
     assert nsplit.value >= 1 and chunk.value * nsplit.value >= kmax and chunk.value * (nsplit.value - 1) < kmax
     cap = max(256, -(-(-(-kmax // 6)) // 32) * 32)
-    assert chunk.value <= max(cap, -(-kmax // 32) * 32)
-    if -(-seq_q // 64) * 8 >= 512:
+    q4 = (kmax // 4 + 16) // 32 * 32                 # a quarter of the range, nearest 32
+    nq = -(-seq_q // 64)
+    assert chunk.value <= max(cap, q4, -(-kmax // 32) * 32)
+    if nq >= 4 and kmax <= 2048:                      # several query tiles: quarter-range splits at least
+        assert chunk.value >= min(q4, -(-kmax // 32) * 32)
+    if nq * 8 >= 512:
         assert nsplit.value == 1
     # partial buffer: (o[128], m, l) per split, query and head, only when split
     assert part == (nsplit.value * seq_q * 16 * 130 if nsplit.value > 1 else 0)
