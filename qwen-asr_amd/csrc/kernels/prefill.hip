@@ -338,9 +338,11 @@ __global__ __launch_bounds__(256) void gemm_hilo(const uint16_t *__restrict__ ah
 // flight behind the MFMAs; one barrier per k tile.  A stage holds A_hi
 // [BM][32], A_lo [BM][32] and W [256][32] in bf16, rows of 64 bytes; a load
 // instruction fills 1 KB (16 rows) with lane l at byte 16 l, i.e. row l / 4,
-// 16-byte slot l % 4.  Slot p of row r holds k chunk p ^ ((r / 4) % 4): the
-// 16 rows x 16 bytes a fragment read touches then fall in 16 different
-// 16-byte bank groups.
+// 16-byte slot l % 4.  Slot p of row r holds k chunk p ^ ((r / 2) % 4): the
+// 16 rows x 16 bytes a fragment read touches fall in 16 different 16-byte bank
+// groups, and SQ_LDS_BANK_CONFLICT reads 0 for the fragment reads (with
+// p ^ ((r / 4) % 4), also 16 distinct groups, it read 0.12 conflict cycles
+// per active LDS cycle).
 // ---------------------------------------------------------------------------
 #define QK_GBK 32
 
@@ -362,7 +364,7 @@ __global__ __launch_bounds__(512, 1) void gemm_hilo_wide(const uint16_t *__restr
     const int nk = (ke - kb) / QK_GBK;
 
     // this lane's load slot: row rr of a 16-row group, k chunk cl (swizzled)
-    const int rr = lane >> 2, cl = (lane & 3) ^ ((rr >> 2) & 3);
+    const int rr = lane >> 2, cl = (lane & 3) ^ ((rr >> 1) & 3);
     const size_t ra0 = (size_t)min(m0 + 16 * (AI * wave) + rr, M - 1) * K + kb + 8 * cl;
     const size_t ra1 = (size_t)min(m0 + 16 * (AI * wave + 1) + rr, M - 1) * K + kb + 8 * cl;   // AI == 2 only
     const uint16_t *pw = W + (size_t)(n0 + 32 * wave + rr) * K + kb + 8 * cl;
@@ -389,7 +391,7 @@ __global__ __launch_bounds__(512, 1) void gemm_hilo_wide(const uint16_t *__restr
 
     // fragment reads: row (lane & 15) of a 16-row tile, k chunk lane >> 4
     const int fr = lane & 15;
-    const int fo = fr * 64 + 16 * ((lane >> 4) ^ ((fr >> 2) & 3));
+    const int fo = fr * 64 + 16 * ((lane >> 4) ^ ((fr >> 1) & 3));
     for (int t = 0; t < NST - 1 && t < nk; t++) issue(t);
     for (int kt = 0; kt < nk; kt++) {
         // this wave's loads of tile kt have landed once at most the later
@@ -527,7 +529,7 @@ __device__ __forceinline__ void ring_tile(const uint16_t *__restrict__ ahi, cons
 
     // this lane's load slots: row rr of each of the wave's 16-row groups,
     // k chunk cl (swizzled); rows past M re-read row M - 1 (results dropped)
-    const int rr = lane >> 2, cl = (lane & 3) ^ ((rr >> 2) & 3);
+    const int rr = lane >> 2, cl = (lane & 3) ^ ((rr >> 1) & 3);
     const uint16_t *src[LPW];
     int dst[LPW];
 #pragma unroll
@@ -556,7 +558,7 @@ __device__ __forceinline__ void ring_tile(const uint16_t *__restrict__ ahi, cons
         for (int j = 0; j < TN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     const int fr = lane & 15;
-    const int fo = fr * 64 + 16 * ((lane >> 4) ^ ((fr >> 2) & 3));
+    const int fo = fr * 64 + 16 * ((lane >> 4) ^ ((fr >> 1) & 3));
     for (int t = 0; t < NST - 1 && t < nk; t++) issue(t);
     for (int kt = 0; kt < nk; kt++) {
         ring_wait<LPW, NST - 2>(min(nk - 1 - kt, NST - 2));
