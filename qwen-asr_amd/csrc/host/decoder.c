@@ -114,7 +114,7 @@ struct qwen_hip_decoder {
     int px_ok;
     unsigned long long *px_buf;
     size_t px_words;
-    unsigned long long *xq, *xa, *xo, *xla, *xh, *xd, *xlb, *xc, *xv;
+    unsigned long long *xq, *xa, *xm, *xo, *xla, *xh, *xd, *xlb, *xc, *xv;
     unsigned *px_ctl;         /* [0, 16) per-XCD tickets, [16] error bits */
     unsigned px_epoch;
     unsigned long long *px_trace;   /* [256][QK_PX_TRACE] when tracing */
@@ -257,13 +257,14 @@ static int check_cfg(const qwen_hip_config *c) {
 static int px_alloc(qwen_hip_decoder *d) {
     const size_t H = d->cfg.hidden, I = d->cfg.intermediate, P = 2 * QK_PX_XCD;
     const size_t n_q = P * 512, n_a = P * QK_PX_MAX_SPLIT * QK_PX_PART, n_h = P * H, n_i = P * (I / QK_PX_XCD);
-    const size_t n_c = 2 * QK_PX_BLOCKS, n_v = QK_PX_BLOCKS;
-    d->px_words = n_q + n_a + 4 * n_h + n_i + n_c + n_v;
+    const size_t n_c = 2 * QK_PX_BLOCKS, n_v = QK_PX_BLOCKS, n_m = P * 256;
+    d->px_words = n_q + n_a + n_m + 4 * n_h + n_i + n_c + n_v;
     QK_TRY(dev_alloc((void **)&d->px_buf, d->px_words * 8));
     QK_TRY(dev_alloc((void **)&d->px_ctl, 64 * sizeof(unsigned)));
     unsigned long long *p = d->px_buf;
     d->xq = p;  p += n_q;
     d->xa = p;  p += n_a;
+    d->xm = p;  p += n_m;
     d->xo = p;  p += n_h;
     d->xla = p; p += n_h;
     d->xd = p;  p += n_h;
@@ -746,7 +747,7 @@ static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
         .off_nk = (const char *)d->n_k[0] - l0, .emb = d->emb, .fnorm = d->fnorm, .k_cache = d->kc,
         .v_cache = d->vc, .cap = d->kv_cap, .rope_cos = d->rope_cos, .rope_sin = d->rope_sin,
         .layers = c->layers, .vocab = c->vocab, .eps = c->rms_eps, .scale = d->scale,
-        .xq = d->xq, .xa = d->xa, .xo = d->xo, .xla = d->xla, .xh = d->xh, .xd = d->xd, .xlb = d->xlb,
+        .xq = d->xq, .xa = d->xa, .xm = d->xm, .xo = d->xo, .xla = d->xla, .xh = d->xh, .xd = d->xd, .xlb = d->xlb,
         .xc = d->xc, .xv = d->xv, .cnt = d->px_ctl, .err = d->px_ctl + 16, .epoch = d->px_epoch,
         .wait_ticks = d->px_wait_ticks,
         .pos0 = d->kv_len, .n_steps = n, .first_tok = first_tok, .x_in = d->x, .log = d->d_log,

@@ -13,11 +13,12 @@
 // g with its query heads 2g, 2g+1, 1/8 of the MLP intermediate rows, and the
 // matching split-K column slices of the O and down projections.  Per layer
 // only the two split-K partial sums (8 x hidden floats) cross XCDs; the other
-// five hand-overs stay inside one XCD and go through its L2.
+// six hand-overs stay inside one XCD and go through its L2.
 //
 //   Q  rms_norm(x) . Wqkv rows of the group (16 rows per block)      -> local
 //   A  q/k norm + RoPE + K/V append + attention over a position split -> local
-//   O  merge splits, W_o[:, group cols] (H/32 rows per block)         -> cross
+//   M  block r merges 8 of the group's 256 attention dims over splits -> local
+//   O  W_o[:, group cols] over the merged output (H/32 rows per block) -> cross
 //   F  x += sum of O partials; rms_norm; gate|up rows + SwiGLU         -> local
 //   D  W_down[:, group cols] (H/32 rows per block)                    -> cross
 //   (next layer's Q adds the down partials to x), LM head + argmax    -> cross
@@ -144,9 +145,11 @@ __device__ bool px_poll(const qk_persist_args &a, Addr addr, int n, unsigned tag
 // A slab of bf16 weight rows held in registers by the compute waves.  Lanes
 // form groups of LW; a group covers 8*LW consecutive columns per 16-byte load
 // (SEGS loads per row), a wave covers 64/LW rows per batch and BPW batches.
-// Rows [0, R) of the slab start at W with row stride ld (elements).
+// Rows [0, R) of the slab start at W with row stride ld (elements).  Wave w
+// owns batches [w*WB, w*WB + BPW) of the row range (WB > BPW: the slab is
+// the first BPW batches of each wave's share, the rest held by another slab).
 // ---------------------------------------------------------------------------
-template <int LW, int SEGS, int BPW>
+template <int LW, int SEGS, int BPW, int WB = BPW>
 struct PxSlab {
     static constexpr int RPI = 64 / LW;
     uint4 w[BPW][SEGS];
@@ -157,14 +160,14 @@ struct PxSlab {
         const unsigned lo = (unsigned)((lane / LW) * ld + (lane % LW) * 8) * 2u;
 #pragma unroll
         for (int b = 0; b < BPW; b++) {
-            const uint16_t *wb = W + (long)((wave * BPW + b) * RPI) * ld;
+            const uint16_t *wb = W + (long)((wave * WB + b) * RPI) * ld;
 #pragma unroll
             for (int s = 0; s < SEGS; s++) w[b][s] = px_ld16(wb + s * 8 * LW, lo);
         }
     }
 
     // slab row of batch b for this lane
-    __device__ __forceinline__ static int row(int wave, int b, int lane) { return (wave * BPW + b) * RPI + lane / LW; }
+    __device__ __forceinline__ static int row(int wave, int b, int lane) { return (wave * WB + b) * RPI + lane / LW; }
 
     // y[b] = W[row] . x for the row of batch b, in every lane of the LW group
     __device__ __forceinline__ void dot(const float *x, float (&y)[BPW], int lane) const {
@@ -356,14 +359,15 @@ struct PxShared {
     float qr[2][128], kr[128], vr[128];         // normed + rotated q, k; v
 
     // attention scratch: the 16-lane groups' (max, sum, output) while the split
-    // is folded (stage A), then the group's split partials polled for the merge
-    // (stage O); the stages are barrier-separated, so they share storage
+    // is folded (stage A), then the (m, l, 8 o words) of every split polled by
+    // the sync wave for its share of the merge (stage O); the stages are
+    // barrier-separated, so they share storage
     union {
         struct {
             float sm_m[NG][2], sm_l[NG][2];
             float sm_o[NG][2][128];
         };
-        float part[QK_PX_MAX_SPLIT * QK_PX_PART];
+        float part[QK_PX_MAX_SPLIT * 10];
     };
     float att[256];                             // merged attention output of the group
     float hs[HG];                               // SwiGLU outputs of the group
@@ -431,6 +435,59 @@ __device__ void px_rmsnorm(const qk_persist_args &a, PxShared<H, I, NCW> &S, con
     const float rinv = 1.0f / sqrtf(ss / (float)H + a.eps);
 #pragma unroll
     for (int j = 0; j < H / 64; j++) S.xn[j * 64 + lane] = (S.xs[j * 64 + lane] * w[j * 64 + lane]) * rinv;
+}
+
+// Stage O's input, in two hand-overs: block r of the group merges 8 of the
+// group's 256 attention output dims (head r / 16, dims 8 (r % 16) ..) over
+// every split (m, l and its 8 o words per split) and publishes them; then the
+// block reads all 256 merged dims into S.att.  The merge is the online merge
+// of qwen_causal_attention_heads' running max and sum (qwen_asr_kernels.c:
+// 1073-1094), taken over chunks of 8 splits.
+template <int H, int I, int NCW>
+__device__ bool px_merge_splits(const qk_persist_args &a, PxShared<H, I, NCW> &S, int pos, int g, int r, int par,
+                                unsigned T, int lane) {
+    const long WG = (long)QK_PX_XCD;
+    const PxSplit sp(pos, 0);
+    const int h = r >> 4, d0 = 8 * (r & 15);
+    const u64 *src = a.xa + (par * WG + g) * (long)(QK_PX_MAX_SPLIT * QK_PX_PART) + h * 130;
+    // word 10 i + k: split i's m (k 0), l (k 1), o[d0 + k - 2] (k 2..9)
+    auto part = [&](int i) {
+        const int sidx = i / 10, k = i - 10 * sidx;
+        return src + (long)sidx * QK_PX_PART + (k < 2 ? k : d0 + k);
+    };
+    if (!px_poll<QK_PX_MAX_SPLIT * 10 / 64>(a, part, 10 * sp.nsplit, T + 1u, S.part, lane)) return false;
+    u64 *xm = a.xm + (par * WG + g) * 256;
+    if (lane < 8) {
+        float M = -INFINITY, Lh = 0.0f, acc = 0.0f;
+        for (int c0 = 0; c0 < sp.nsplit; c0 += 8) {
+            float mv[8], lv[8], ov[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const bool in = c0 + j < sp.nsplit;
+                const float *pp = S.part + (in ? c0 + j : 0) * 10;
+                mv[j] = in ? pp[0] : -INFINITY;
+                lv[j] = in ? pp[1] : 0.0f;
+                ov[j] = in ? pp[2 + lane] : 0.0f;
+            }
+            float Mc = M;
+#pragma unroll
+            for (int j = 0; j < 8; j++) Mc = fmaxf(Mc, mv[j]);
+            const float sc = (M == -INFINITY) ? 0.0f : __expf(M - Mc);
+            Lh *= sc;
+            acc *= sc;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float e = (mv[j] == -INFINITY) ? 0.0f : __expf(mv[j] - Mc);
+                Lh = fmaf(lv[j], e, Lh);
+                acc = fmaf(ov[j], e, acc);
+            }
+            M = Mc;
+        }
+        // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
+        px_put_local(xm + h * 128 + d0 + lane, acc * (1.0f / Lh), T + 7u);
+    }
+    auto whole = [&](int i) { return xm + i; };
+    return px_poll<4>(a, whole, 256, T + 7u, S.att, lane);
 }
 
 // Start the DMA of a norm weight vector [H] into LDS (no registers held while
@@ -529,21 +586,14 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             px_sync();   // after q/k norm + RoPE
             px_sync();   // after the position fold
 
-            // ---- O: the group's split partials ----
+            // ---- O: merge the group's split partials, then read the merged output ----
             px_sync();
             mark(10 * l + 4);
-            {
-                const PxSplit sp(pos, 0);
-                const u64 *src = a.xa + (par * WG + g) * (long)(QK_PX_MAX_SPLIT * QK_PX_PART);
-                auto addr = [&](int i) { return src + i; };
-                // words per lane in flight: the 1.7B kernel has fewer registers per wave
-                ok = px_poll<(NCW == 4 ? 33 : 17)>(a, addr, sp.nsplit * QK_PX_PART, T + 1u, S.part, lane);
-            }
+            ok = px_merge_splits<H, I, NCW>(a, S, pos, g, r, par, T, lane);
             mark(10 * l + 5);
             if (lane == 0) S.abort_ = !ok;
             px_sync();
             if (S.abort_) return;
-            px_sync();   // after the merge
 
             // ---- F: x += O partials; post-attention norm ----
             px_load_norm<H>((const float *)(lb + a.off_npost), S.nw, lane);
@@ -645,7 +695,8 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
 // the 1.7B slabs are 4x larger, so it issues each one stage ahead, between
 // the two barriers that open the stage before the one that uses it (its
 // stream then overlaps the sync wave's wait there, not the compute waves'):
-//   Q(l): K/V(l), O(l)   F(l): gate|up(l), used right after   D(l): down(l), Q(l+1)
+//   Q(l): K/V(l), O(l)   end of A: first half of gate|up(l)
+//   F(l): second half of gate|up(l), used right after   D(l): down(l), Q(l+1)
 // ---------------------------------------------------------------------------
 template <int H, int I, int NCW>
 __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, PxKvLds<NCW> &kvb, int wave,
@@ -660,7 +711,11 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
     constexpr bool DEEP = NCW == 4;
     using SlabQ = PxSlab<64, SEGH, 16 / NCW>;
     using SlabO = PxSlab<32, 1, SO / 2 / NCW>;
-    using SlabF = PxSlab<64, SEGH, RF / NCW>;
+    // gate|up: DEEP holds the block's rows in one slab; 1.7B in two halves, the
+    // first issued after attention, the second when stage F opens
+    constexpr int FB = RF / NCW, FB1 = DEEP ? FB : FB / 2, FB2 = FB - FB1;
+    using SlabF = PxSlab<64, SEGH, FB1, FB>;
+    using SlabF2 = PxSlab<64, SEGH, (FB2 > 0 ? FB2 : 1), FB>;
     using SlabD = PxSlab<16, HG / 128, SO / 4 / NCW>;
     static_assert(16 % NCW == 0 && (SO / 2) % NCW == 0 && RF % NCW == 0 && (SO / 4) % NCW == 0, "slab split");
     // the slabs tile their row ranges exactly (no bounds checks in PxSlab::load)
@@ -707,6 +762,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
     SlabQ wq;
     SlabO wo;
     SlabF wf;
+    SlabF2 wf2;
     SlabD wd;
 
     // first step's layer-0 operands
@@ -892,46 +948,14 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             // those blocks can depend on.
             if (sp.last && (wave == 2 || wave == 3)) px_wait_loads();
             mark(4);
-            if (DEEP) wf.load(Wf(l), H, wave, lane);
+            wf.load(Wf(l), H, wave, lane);
 
-            // ---- O: merge the splits, then this block's rows of W_o over the group's columns ----
+            // ---- O: this block's rows of W_o over the group's columns (merged attention output in S.att) ----
             px_sync();
             px_sync();
             if (S.abort_) return;
             if (DEEP) wd.load(Wd(l), I, wave, lane);
-            if (tid < 256) {
-                // online merge over chunks of 8 splits; a chunk's LDS reads are
-                // issued together (one latency per chunk, not per split)
-                const int h = tid >> 7, d = tid & 127;
-                float M = -INFINITY, Lh = 0.0f, acc = 0.0f;
-                for (int c0 = 0; c0 < sp.nsplit; c0 += 8) {
-                    float mv[8], lv[8], ov[8];
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const bool in = c0 + j < sp.nsplit;
-                        const float *pp = S.part + (in ? c0 + j : 0) * QK_PX_PART + h * 130;
-                        mv[j] = in ? pp[0] : -INFINITY;
-                        lv[j] = in ? pp[1] : 0.0f;
-                        ov[j] = in ? pp[2 + d] : 0.0f;
-                    }
-                    float Mc = M;
-#pragma unroll
-                    for (int j = 0; j < 8; j++) Mc = fmaxf(Mc, mv[j]);
-                    const float sc = (M == -INFINITY) ? 0.0f : __expf(M - Mc);
-                    Lh *= sc;
-                    acc *= sc;
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const float e = (mv[j] == -INFINITY) ? 0.0f : __expf(mv[j] - Mc);
-                        Lh = fmaf(lv[j], e, Lh);
-                        acc = fmaf(ov[j], e, acc);
-                    }
-                    M = Mc;
-                }
-                S.att[h * 128 + d] = acc * (1.0f / Lh);   // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
-            }
             mark(5);
-            px_sync();
             {
                 float y[SO / 2 / NCW];
                 wo.dot(S.att, y, lane);
@@ -946,13 +970,21 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
 
             // ---- F: gate|up rows of the group + SwiGLU (qwen_asr_decoder.c:463-466) ----
             px_sync();
-            if (!DEEP) wf.load(Wf(l), H, wave, lane);
+            if (!DEEP) wf2.load(Wf(l) + (long)FB1 * H, H, wave, lane);
             px_sync();
             if (S.abort_) return;
             if (DEEP) wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
             {
-                float y[RF / NCW];
-                wf.dot(S.xn, y, lane);
+                float y[FB];
+                if constexpr (DEEP) {
+                    wf.dot(S.xn, y, lane);
+                } else {
+                    float y1[FB1], y2[FB2];
+                    wf.dot(S.xn, y1, lane);
+                    wf2.dot(S.xn, y2, lane);
+#pragma unroll
+                    for (int i = 0; i < FB; i++) y[i] = i < FB1 ? y1[i] : y2[i - FB1];
+                }
                 mark(8);
                 if (lane == 0) {
                     u64 *dst = a.xh + (par * WG + g) * HG + (RF / 2) * r;

@@ -149,7 +149,7 @@ int qk_attn_merge_launch(const qk_attn_fused_args *a, hipStream_t s);
 #define QK_PX_MAX_SPLIT 32                 /* attention splits per kv head (one per CU) */
 #define QK_PX_PART 260                     /* words per split: 2 heads x (m, l, o[128]) */
 #define QK_PX_MIN_CHUNK 64                 /* positions per split, at least */
-#define QK_PX_TPL 7                        /* exchange tags per layer */
+#define QK_PX_TPL 8                        /* exchange tags per layer */
 enum { QK_PX_ERR_LAYOUT = 1, QK_PX_ERR_TIMEOUT = 2 };
 
 typedef struct {
@@ -167,6 +167,7 @@ typedef struct {
     /* exchange buffers (zero-initialised; each [2 parities][8 XCDs][...]) */
     unsigned long long *xq;    /* [2][8][512]  q|q|k|v of the group */
     unsigned long long *xa;    /* [2][8][32][QK_PX_PART] attention split partials */
+    unsigned long long *xm;    /* [2][8][256] merged attention output of the group (2 heads x 128) */
     unsigned long long *xo;    /* [2][8][hidden] O-projection split-K partials (cross-XCD) */
     unsigned long long *xla;   /* [2][8][hidden] residual after attention (XCD-local copy) */
     unsigned long long *xh;    /* [2][8][inter/8] SwiGLU outputs of the group */
