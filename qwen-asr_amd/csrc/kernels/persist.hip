@@ -157,7 +157,10 @@ struct PxSlab {
     // wave must be wave-uniform (an SGPR): every per-batch offset then folds
     // into the scalar base and a lane needs one 32-bit offset for all loads.
     __device__ __forceinline__ void load(const uint16_t *W, int ld, int wave, int lane) {
-        const unsigned lo = (unsigned)((lane / LW) * ld + (lane % LW) * 8) * 2u;
+        unsigned lo = (unsigned)((lane / LW) * ld + (lane % LW) * 8) * 2u;
+        // recomputed at every call: otherwise the compiler keeps 64-bit
+        // per-lane slab addresses live across the layer loop and spills them
+        asm volatile("" : "+v"(lo));
 #pragma unroll
         for (int b = 0; b < BPW; b++) {
             const uint16_t *wb = W + (long)((wave * WB + b) * RPI) * ld;
@@ -963,7 +966,11 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 if ((lane & 31) == 0) {
                     u64 *dst = a.xo + (par * WG + g) * H + SO * r;
 #pragma unroll
-                    for (int i = 0; i < SO / 2 / NCW; i++) px_put_global(dst + SlabO::row(wave, i, lane), y[i], T + 2u);
+                    for (int i = 0; i < SO / 2 / NCW; i++) {
+                        unsigned ro = (unsigned)SlabO::row(wave, i, lane);
+                        asm volatile("" : "+v"(ro));   // no per-lane address kept across the loop
+                        px_put_global(dst + ro, y[i], T + 2u);
+                    }
                 }
             }
             mark(7);
@@ -1009,7 +1016,11 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 if ((lane & 15) == 0) {
                     u64 *dst = a.xd + (par * WG + g) * H + SO * r;
 #pragma unroll
-                    for (int i = 0; i < SO / 4 / NCW; i++) px_put_global(dst + SlabD::row(wave, i, lane), y[i], T + 5u);
+                    for (int i = 0; i < SO / 4 / NCW; i++) {
+                        unsigned ro = (unsigned)SlabD::row(wave, i, lane);
+                        asm volatile("" : "+v"(ro));   // no per-lane address kept across the loop
+                        px_put_global(dst + ro, y[i], T + 5u);
+                    }
                 }
             }
             {   // the next layer's operands (after the last layer: layer 0 of the next step)
