@@ -298,13 +298,37 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(qk_attn_args a) {
     const int qi = (int)(u / a.heads), h = (int)(u % a.heads), lane = threadIdx.x & 63;
     const int t = qi / PF_Q;
     const int kend_tile = min(a.seq_k, a.q_offset + min(a.seq_q, (t + 1) * PF_Q));
-    const int n = (kend_tile + a.chunk - 1) / a.chunk;
+    int n = (kend_tile + a.chunk - 1) / a.chunk;
     const size_t stride = (size_t)a.seq_q * a.heads * QK_PF_PART;
     const float *p0 = a.part + ((size_t)qi * a.heads + h) * QK_PF_PART;
     // batches of 8 splits: the loads of a batch are issued together, the sums
     // still run in split order
     constexpr int MB = 8;
     float M = PF_MINIT;
+    float L = 0.0f, ox = 0.0f, oy = 0.0f;
+    if (n >= 1 && n <= MB) {
+        // one batch: every load in one round trip, then the same max and sums
+        float mv[MB], lv[MB];
+        float2 v[MB];
+#pragma unroll
+        for (int j = 0; j < MB; j++) {
+            const bool in = j < n;
+            const float *p = p0 + (in ? j : 0) * stride;
+            mv[j] = in ? p[hd] : PF_MINIT;
+            lv[j] = p[hd + 1];
+            v[j] = *reinterpret_cast<const float2 *>(p + 2 * lane);
+        }
+#pragma unroll
+        for (int j = 0; j < MB; j++) M = fmaxf(M, mv[j]);
+#pragma unroll
+        for (int j = 0; j < MB; j++) {
+            const float w = j < n ? __expf(mv[j] - M) : 0.0f;
+            L = fmaf(lv[j], w, L);
+            ox = fmaf(v[j].x, w, ox);
+            oy = fmaf(v[j].y, w, oy);
+        }
+        n = 0;                                        // the loops below do nothing
+    }
     for (int s0 = 0; s0 < n; s0 += MB) {
         float mv[MB];
 #pragma unroll
@@ -312,7 +336,6 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(qk_attn_args a) {
 #pragma unroll
         for (int j = 0; j < MB; j++) M = fmaxf(M, mv[j]);
     }
-    float L = 0.0f, ox = 0.0f, oy = 0.0f;
     for (int s0 = 0; s0 < n; s0 += MB) {
         float mv[MB], lv[MB];
         float2 v[MB];
