@@ -698,8 +698,9 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
 // the 1.7B slabs are 4x larger, so it issues each one stage ahead, between
 // the two barriers that open the stage before the one that uses it (its
 // stream then overlaps the sync wave's wait there, not the compute waves'):
-//   Q(l): K/V(l), O(l)   end of A: first half of gate|up(l)
-//   F(l): second half of gate|up(l), used right after   D(l): down(l), Q(l+1)
+//   Q(l): K/V(l), O(l)   end of A: gate|up(l) but FR rows per wave (half in
+//   registers, FL rows by LDS DMA into the wave's K/V buffer)
+//   F(l): the FR rows, used right after   D(l): down(l), Q(l+1)
 // ---------------------------------------------------------------------------
 template <int H, int I, int NCW>
 __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, PxKvLds<NCW> &kvb, int wave,
@@ -714,11 +715,18 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
     constexpr bool DEEP = NCW == 4;
     using SlabQ = PxSlab<64, SEGH, 16 / NCW>;
     using SlabO = PxSlab<32, 1, SO / 2 / NCW>;
-    // gate|up: DEEP holds the block's rows in one slab; 1.7B in two halves, the
-    // first issued after attention, the second when stage F opens
+    // gate|up: DEEP holds the block's rows in one slab.  1.7B: the first half
+    // of each wave's rows in registers and FL rows in the wave's share of the
+    // K/V LDS buffer (free between the fold and the next layer's K/V DMA),
+    // both issued after attention; the FR rows left go to registers when
+    // stage F opens
     constexpr int FB = RF / NCW, FB1 = DEEP ? FB : FB / 2, FB2 = FB - FB1;
+    constexpr int KVW = (int)sizeof(PxKvLds<NCW>) / NCW;                     // LDS bytes per wave
+    constexpr int FL = DEEP ? 0 : (FB2 < KVW / (2 * H) ? FB2 : KVW / (2 * H));
+    constexpr int FR = FB2 - FL;
     using SlabF = PxSlab<64, SEGH, FB1, FB>;
-    using SlabF2 = PxSlab<64, SEGH, (FB2 > 0 ? FB2 : 1), FB>;
+    using SlabF2 = PxSlab<64, SEGH, (FR > 0 ? FR : 1), FB>;
+    static_assert(DEEP || (FR >= 1 && FL >= 1), "1.7B gate|up split");
     using SlabD = PxSlab<16, HG / 128, SO / 4 / NCW>;
     static_assert(16 % NCW == 0 && (SO / 2) % NCW == 0 && RF % NCW == 0 && (SO / 4) % NCW == 0, "slab split");
     // the slabs tile their row ranges exactly (no bounds checks in PxSlab::load)
@@ -951,6 +959,19 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             // those blocks can depend on.
             if (sp.last && (wave == 2 || wave == 3)) px_wait_loads();
             mark(4);
+            if constexpr (!DEEP) {
+                // the fold's reads of this wave's K/V buffer are complete and its
+                // K/V DMA has landed (an inactive block never waited for it)
+                px_wait_loads();
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                uint4(*fl)[64] = reinterpret_cast<uint4(*)[64]>(&kvb[wave][0][0][0]);
+                const uint16_t *wl = Wf(l) + (long)(wave * FB + FB1 + FR) * H + lane * 8;
+#pragma unroll
+                for (int b = 0; b < FL; b++)
+#pragma unroll
+                    for (int c = 0; c < SEGH; c++)
+                        __builtin_amdgcn_global_load_lds(wl + (long)b * H + c * 512, &fl[b * SEGH + c][0], 16, 0, 0);
+            }
             wf.load(Wf(l), H, wave, lane);
 
             // ---- O: this block's rows of W_o over the group's columns (merged attention output in S.att) ----
@@ -977,7 +998,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
 
             // ---- F: gate|up rows of the group + SwiGLU (qwen_asr_decoder.c:463-466) ----
             px_sync();
-            if (!DEEP) wf2.load(Wf(l) + (long)FB1 * H, H, wave, lane);
+            if (!DEEP) wf2.load(Wf(l) + (long)FB1 * H, H, wave, lane);   // FR rows
             px_sync();
             if (S.abort_) return;
             if (DEEP) wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
@@ -986,11 +1007,29 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 if constexpr (DEEP) {
                     wf.dot(S.xn, y, lane);
                 } else {
-                    float y1[FB1], y2[FB2];
+                    float y1[FB1], y2[FR], y3[FL];
                     wf.dot(S.xn, y1, lane);
                     wf2.dot(S.xn, y2, lane);
+                    // the FL rows in LDS: PxSlab::dot's sums in the same order
+                    px_wait_loads();
+                    const uint4(*fl)[64] = reinterpret_cast<const uint4(*)[64]>(&kvb[wave][0][0][0]);
+                    const int cl = lane * 8;
 #pragma unroll
-                    for (int i = 0; i < FB; i++) y[i] = i < FB1 ? y1[i] : y2[i - FB1];
+                    for (int b = 0; b < FL; b++) y3[b] = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < SEGH; c++) {
+                        float xv[8];
+                        const float4 p0 = *reinterpret_cast<const float4 *>(S.xn + c * 512 + cl);
+                        const float4 p1 = *reinterpret_cast<const float4 *>(S.xn + c * 512 + cl + 4);
+                        xv[0] = p0.x; xv[1] = p0.y; xv[2] = p0.z; xv[3] = p0.w;
+                        xv[4] = p1.x; xv[5] = p1.y; xv[6] = p1.z; xv[7] = p1.w;
+#pragma unroll
+                        for (int b = 0; b < FL; b++) y3[b] = dot8_bf16(fl[b * SEGH + c][lane], xv, y3[b]);
+                    }
+#pragma unroll
+                    for (int b = 0; b < FL; b++) y3[b] = group_sum<64>(y3[b]);
+#pragma unroll
+                    for (int i = 0; i < FB; i++) y[i] = i < FB1 ? y1[i] : (i < FB1 + FR ? y2[i - FB1] : y3[i - FB1 - FR]);
                 }
                 mark(8);
                 if (lane == 0) {
