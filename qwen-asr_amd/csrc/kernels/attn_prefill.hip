@@ -27,7 +27,11 @@
 //   O^T += V^T P^T  B = the probabilities exactly where S^T left them: k-slot
 //                 8 (l >> 4) + i of the MFMA is key 4 (l >> 4) + i (i < 4) and
 //                 16 + 4 (l >> 4) + i - 4 (i >= 4), and A = V^T reads the same
-//                 keys, so no value crosses lanes.
+//                 keys, so no value crosses lanes.  A V^T row (one dim, 64
+//                 bytes) stores the 32 keys in that order, so a lane's 8 keys
+//                 are one 16-byte chunk: chunk c of row d sits in slot
+//                 c ^ ((d / 2) % 4), and a fragment is one 16-byte read free of
+//                 bank conflicts (the swizzle of the ring GEMM's tiles).
 // O^T lands as lane l: dims 16 dt + 4 (l >> 4) + r of query l & 15, written
 // back as float4 per dt.
 //
@@ -44,7 +48,7 @@
 #define PF_Q 64                   // queries per block (per query head)
 #define PF_KT 32                  // keys per LDS tile
 #define PF_KLDB (QWEN_HIP_HEAD_DIM + 8)  // bf16 row stride of the K tiles: 272 B, fragment reads conflict free
-#define PF_VLDB (PF_KT + 4)               // bf16 row stride of the V^T tiles: 72 B
+#define PF_VLDB PF_KT                     // bf16 row stride of the V^T tiles: 64 B, swizzled chunks
 #define PF_MINIT (-1.0e30f)       // running-max start, as the reference's -1e30 (:1069)
 
 typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
@@ -71,10 +75,17 @@ __device__ __forceinline__ f32x4 pf_mfma3(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x
 }
 
 // The next K/V tile, held in registers while the current one is consumed.
+// V: lane l of wave w holds dim pf_vdim(w, l, j) of keys 4 pf_vgrp(l) + e: per
+// store instruction a wave covers 8 dims x 8 key groups, which the swizzled
+// V^T rows take without bank conflicts (the 32 lanes of a half wave land in
+// 32 distinct bank pairs).
 struct PfStage {
     float4 k[4];     // K rows: float4 (tid + 256 i): key (.. >> 5), dims 4 (.. & 31)
-    float v[16];     // V: dim (tid & 127), keys 4 ((tid >> 7) + 2 j) + e
+    float v[16];     // V: dim pf_vdim(wave, lane, j), keys 4 pf_vgrp(lane) + e
 };
+
+__device__ __forceinline__ int pf_vgrp(int lane) { return (lane >> 2) & 7; }
+__device__ __forceinline__ int pf_vdim(int wave, int lane, int j) { return 8 * (wave + 4 * j) + (lane & 3) + 4 * (lane >> 5); }
 
 __device__ __forceinline__ void pf_load(PfStage &st, const float *kb, const float *vb, long ps, int k0, int kend,
                                         int tid) {
@@ -84,12 +95,13 @@ __device__ __forceinline__ void pf_load(PfStage &st, const float *kb, const floa
         st.k[i] = key < kend ? *reinterpret_cast<const float4 *>(kb + (size_t)key * ps + (idx & 31) * 4)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const int d = tid & 127;
+    const int wave = tid >> 6, lane = tid & 63, g = pf_vgrp(lane);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
+        const int d = pf_vdim(wave, lane, j);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int key = k0 + 4 * ((tid >> 7) + 2 * j) + e;
+            const int key = k0 + 4 * g + e;
             st.v[4 * j + e] = key < kend ? vb[(size_t)key * ps + d] : 0.0f;
         }
     }
@@ -105,21 +117,24 @@ __device__ __forceinline__ void pf_store(const PfStage &st, __bf16 (*sKh)[PF_KLD
         *reinterpret_cast<pf_bf16x4 *>(&sKh[idx >> 5][(idx & 31) * 4]) = h;
         *reinterpret_cast<pf_bf16x4 *>(&sKl[idx >> 5][(idx & 31) * 4]) = l;
     }
-    const int d = tid & 127;
+    // keys 4 g .. 4 g + 3 go to chunk g % 4, half g / 4 of the row (key order
+    // of the MFMA's k slots, see the header)
+    const int wave = tid >> 6, lane = tid & 63, g = pf_vgrp(lane);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
+        const int d = pf_vdim(wave, lane, j);
+        const int o = 8 * ((g & 3) ^ ((d >> 1) & 3)) + 4 * (g >> 2);
         pf_bf16x4 h, l;
         pf_split4(make_float4(st.v[4 * j], st.v[4 * j + 1], st.v[4 * j + 2], st.v[4 * j + 3]), h, l);
-        *reinterpret_cast<pf_bf16x4 *>(&sVh[d][4 * ((tid >> 7) + 2 * j)]) = h;
-        *reinterpret_cast<pf_bf16x4 *>(&sVl[d][4 * ((tid >> 7) + 2 * j)]) = l;
+        *reinterpret_cast<pf_bf16x4 *>(&sVh[d][o]) = h;
+        *reinterpret_cast<pf_bf16x4 *>(&sVl[d][o]) = l;
     }
 }
 
-// 8 bf16 of a V^T row: keys 4 kq .. + 3 and 16 + 4 kq .. + 3 (the keys of this lane's scores)
-__device__ __forceinline__ bf16x8 pf_vrow(const __bf16 *row, int kq) {
-    const pf_bf16x4 a = *reinterpret_cast<const pf_bf16x4 *>(row + 4 * kq);
-    const pf_bf16x4 b = *reinterpret_cast<const pf_bf16x4 *>(row + 16 + 4 * kq);
-    return (bf16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+// 8 bf16 of V^T row d: keys 4 kq .. + 3 and 16 + 4 kq .. + 3 (the keys of this
+// lane's scores), chunk kq of the row
+__device__ __forceinline__ bf16x8 pf_vrow(const __bf16 *row, int d, int kq) {
+    return *reinterpret_cast<const bf16x8 *>(row + 8 * (kq ^ ((d >> 1) & 3)));
 }
 
 __device__ __forceinline__ void pf_write_out(const qk_attn_args &a, size_t base, float4 v) {
@@ -254,8 +269,8 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
                       ph[qt], po[qt]);
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
-            const bf16x8 vh = pf_vrow(&sVh[16 * dt + ql][0], kq);
-            const bf16x8 vl = pf_vrow(&sVl[16 * dt + ql][0], kq);
+            const bf16x8 vh = pf_vrow(&sVh[16 * dt + ql][0], 16 * dt + ql, kq);
+            const bf16x8 vl = pf_vrow(&sVl[16 * dt + ql][0], 16 * dt + ql, kq);
 #pragma unroll
             for (int qt = 0; qt < 2; qt++) o[qt][dt] = pf_mfma3(vh, vl, ph[qt], po[qt], o[qt][dt]);
         }
