@@ -47,7 +47,11 @@
 
 #define PF_Q 64                   // queries per block (per query head)
 #define PF_KT 32                  // keys per LDS tile
-#define PF_KLDB (QWEN_HIP_HEAD_DIM + 8)  // bf16 row stride of the K tiles: 272 B, fragment reads conflict free
+// K tile: four 32-dim slices of 32 keys x 64-byte rows (chunk c of key row r
+// in slot c ^ ((r / 2) % 4): the fragment reads are the ring GEMM's pattern,
+// free of bank conflicts), slices 64 bytes apart beyond their 2 KB so the
+// four slices a store instruction touches fall in different banks
+#define PF_KSL (PF_KT * 32 + 32)         // bf16 per K slice
 #define PF_VLDB PF_KT                     // bf16 row stride of the V^T tiles: 64 B, swizzled chunks
 #define PF_MINIT (-1.0e30f)       // running-max start, as the reference's -1e30 (:1069)
 
@@ -107,15 +111,19 @@ __device__ __forceinline__ void pf_load(PfStage &st, const float *kb, const floa
     }
 }
 
-__device__ __forceinline__ void pf_store(const PfStage &st, __bf16 (*sKh)[PF_KLDB], __bf16 (*sKl)[PF_KLDB],
+__device__ __forceinline__ int pf_kslot(int key, int c) { return key * 32 + 8 * (c ^ ((key >> 1) & 3)); }
+
+__device__ __forceinline__ void pf_store(const PfStage &st, __bf16 (*sKh)[PF_KSL], __bf16 (*sKl)[PF_KSL],
                                          __bf16 (*sVh)[PF_VLDB], __bf16 (*sVl)[PF_VLDB], int tid) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int idx = tid + 256 * i;
         pf_bf16x4 h, l;
         pf_split4(st.k[i], h, l);
-        *reinterpret_cast<pf_bf16x4 *>(&sKh[idx >> 5][(idx & 31) * 4]) = h;
-        *reinterpret_cast<pf_bf16x4 *>(&sKl[idx >> 5][(idx & 31) * 4]) = l;
+        // dims 4 (idx & 31) .. + 3 of key idx >> 5: slice (idx & 31) / 8, chunk (idx & 7) / 2, half idx & 1
+        const int o = pf_kslot(idx >> 5, (idx & 7) >> 1) + 4 * (idx & 1);
+        *reinterpret_cast<pf_bf16x4 *>(&sKh[(idx & 31) >> 3][o]) = h;
+        *reinterpret_cast<pf_bf16x4 *>(&sKl[(idx & 31) >> 3][o]) = l;
     }
     // keys 4 g .. 4 g + 3 go to chunk g % 4, half g / 4 of the row (key order
     // of the MFMA's k slots, see the header)
@@ -153,8 +161,8 @@ __device__ __forceinline__ void pf_write_out(const qk_attn_args &a, size_t base,
 
 __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
     constexpr int hd = QWEN_HIP_HEAD_DIM;
-    __shared__ __attribute__((aligned(16))) __bf16 sKh[PF_KT][PF_KLDB];
-    __shared__ __attribute__((aligned(16))) __bf16 sKl[PF_KT][PF_KLDB];
+    __shared__ __attribute__((aligned(16))) __bf16 sKh[4][PF_KSL];
+    __shared__ __attribute__((aligned(16))) __bf16 sKl[4][PF_KSL];
     __shared__ __attribute__((aligned(16))) __bf16 sVh[hd][PF_VLDB];
     __shared__ __attribute__((aligned(16))) __bf16 sVl[hd][PF_VLDB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -219,8 +227,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
         for (int s4 = 0; s4 < 4; s4++) {
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
-                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&sKh[16 * kt + ql][32 * s4 + 8 * kq]);
-                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&sKl[16 * kt + ql][32 * s4 + 8 * kq]);
+                const int o = pf_kslot(16 * kt + ql, kq);
+                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&sKh[s4][o]);
+                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&sKl[s4][o]);
 #pragma unroll
                 for (int qt = 0; qt < 2; qt++) s[qt][kt] = pf_mfma3(kh, kl, qh[qt][s4], qo[qt][s4], s[qt][kt]);
             }
