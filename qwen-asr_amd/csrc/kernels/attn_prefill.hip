@@ -235,20 +235,33 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
             }
         }
 
-        // online softmax (causal mask: key <= q_offset + query; keys past ks1 belong elsewhere)
+        // online softmax (causal mask: key <= q_offset + query; keys past ks1 belong elsewhere).
+        // A tile wholly below the wave's diagonal and inside the split needs no
+        // mask (wave-uniform test; the unmasked scores are the same values).
+        const bool open = k0 + PF_KT - 1 <= a.q_offset + qs && k0 + PF_KT <= ks1;
         float p[2][2][4];
 #pragma unroll
         for (int qt = 0; qt < 2; qt++) {
             const int qpos = a.q_offset + qs + 16 * qt + ql;
             float sc[2][4], mx = -INFINITY;
+            if (open) {
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++)
+                for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int key = k0 + 16 * kt + 4 * kq + r;
-                    sc[kt][r] = (key <= qpos && key < ks1) ? s[qt][kt][r] * a.scale : -INFINITY;
-                    mx = fmaxf(mx, sc[kt][r]);
-                }
+                    for (int r = 0; r < 4; r++) {
+                        sc[kt][r] = s[qt][kt][r] * a.scale;
+                        mx = fmaxf(mx, sc[kt][r]);
+                    }
+            } else {
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int key = k0 + 16 * kt + 4 * kq + r;
+                        sc[kt][r] = (key <= qpos && key < ks1) ? s[qt][kt][r] * a.scale : -INFINITY;
+                        mx = fmaxf(mx, sc[kt][r]);
+                    }
+            }
             mx = xor_max16_32(mx);
             const float mn = fmaxf(m[qt], mx);
             const float corr = __expf(m[qt] - mn);
