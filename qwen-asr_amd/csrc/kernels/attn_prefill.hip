@@ -93,6 +93,22 @@ __device__ __forceinline__ int pf_vdim(int wave, int lane, int j) { return 8 * (
 
 __device__ __forceinline__ void pf_load(PfStage &st, const float *kb, const float *vb, long ps, int k0, int kend,
                                         int tid) {
+    if (k0 + PF_KT <= kend) {                       // a whole tile (block-uniform): no bounds tests
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = tid + 256 * i;
+            st.k[i] = *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + (idx >> 5)) * ps + (idx & 31) * 4);
+        }
+        const int wave = tid >> 6, lane = tid & 63;
+        const float *vr = vb + (size_t)(k0 + 4 * pf_vgrp(lane)) * ps;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int d = pf_vdim(wave, lane, j);
+#pragma unroll
+            for (int e = 0; e < 4; e++) st.v[4 * j + e] = vr[(size_t)e * ps + d];
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int idx = tid + 256 * i, key = k0 + (idx >> 5);
