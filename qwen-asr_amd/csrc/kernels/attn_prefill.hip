@@ -254,7 +254,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
         // online softmax (causal mask: key <= q_offset + query; keys past ks1 belong elsewhere).
         // A tile wholly below the wave's diagonal and inside the split needs no
         // mask (wave-uniform test; the unmasked scores are the same values).
+        // The statistics run in base 2: m holds max(score) * scale * log2(e) and
+        // p = 2^(score * scale * log2(e) - m) = e^(score * scale - max), the
+        // scale and the subtraction in one fma (the merge takes 2^(m_i - M)).
         const bool open = k0 + PF_KT - 1 <= a.q_offset + qs && k0 + PF_KT <= ks1;
+        const float scale2 = a.scale * 1.44269504088896341f;
         float p[2][2][4];
 #pragma unroll
         for (int qt = 0; qt < 2; qt++) {
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
                 for (int kt = 0; kt < 2; kt++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        sc[kt][r] = s[qt][kt][r] * a.scale;
+                        sc[kt][r] = s[qt][kt][r];
                         mx = fmaxf(mx, sc[kt][r]);
                     }
             } else {
@@ -274,19 +278,20 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const int key = k0 + 16 * kt + 4 * kq + r;
-                        sc[kt][r] = (key <= qpos && key < ks1) ? s[qt][kt][r] * a.scale : -INFINITY;
+                        sc[kt][r] = (key <= qpos && key < ks1) ? s[qt][kt][r] : -INFINITY;
                         mx = fmaxf(mx, sc[kt][r]);
                     }
             }
-            mx = xor_max16_32(mx);
+            // scaling by a positive factor keeps the maximum where it is
+            mx = xor_max16_32(mx) * scale2;
             const float mn = fmaxf(m[qt], mx);
-            const float corr = __expf(m[qt] - mn);
+            const float corr = __builtin_amdgcn_exp2f(m[qt] - mn);
             float sum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    p[qt][kt][r] = __expf(sc[kt][r] - mn);
+                    p[qt][kt][r] = __builtin_amdgcn_exp2f(fmaf(sc[kt][r], scale2, -mn));
                     sum += p[qt][kt][r];
                 }
             sum = xor_sum16_32(sum);
@@ -375,7 +380,7 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(qk_attn_args a) {
         for (int j = 0; j < MB; j++) M = fmaxf(M, mv[j]);
 #pragma unroll
         for (int j = 0; j < MB; j++) {
-            const float w = j < n ? __expf(mv[j] - M) : 0.0f;
+            const float w = j < n ? __builtin_amdgcn_exp2f(mv[j] - M) : 0.0f;
             L = fmaf(lv[j], w, L);
             ox = fmaf(v[j].x, w, ox);
             oy = fmaf(v[j].y, w, oy);
@@ -403,7 +408,7 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(qk_attn_args a) {
 #pragma unroll
         for (int j = 0; j < MB; j++) {
             // a split past n adds lv * 0 and v * 0 (finite values of split 0): no change
-            const float w = s0 + j < n ? __expf(mv[j] - M) : 0.0f;
+            const float w = s0 + j < n ? __builtin_amdgcn_exp2f(mv[j] - M) : 0.0f;
             L = fmaf(lv[j], w, L);
             ox = fmaf(v[j].x, w, ox);
             oy = fmaf(v[j].y, w, oy);
