@@ -738,7 +738,7 @@ static int gemm_ring_launch(const uint16_t *a_hi, const uint16_t *a_lo, const ui
         gemm_ring_dispatch<BM_, BN_, NST_>(a_hi, a_lo, W, M, N, K, p, epi, y, oh, ol, s);        \
         return 1;                                                                                \
     }
-    QK_RING(64, 128, QK_GEMM_RING_NST) QK_RING(32, 128, QK_GEMM_RING_NST)
+    QK_RING(64, 128, QK_GEMM_RING_NST) QK_RING(32, 128, QK_GEMM_RING_NST) QK_RING(128, 128, 3)
 #undef QK_RING
     return 0;
 }
@@ -779,6 +779,14 @@ extern "C" void qk_gemm_plan_epi(int M, int N, int K, int epi, qk_gemm_plan *p) 
     p->bn = QK_GEMM_BN;
     p->bm = M <= 32 ? 32 : (ring || M <= 512) ? 64 : 128;
     p->nst = ring ? QK_GEMM_RING_NST : 0;
+    if (ring && epi == QK_GEMM_SWIGLU && M > 512) {
+        // a SwiGLU product of more than 512 rows: 128 x 128 tiles (8 waves of
+        // 32 x 64, 3 stages = 72 KB, two blocks per CU) move a quarter fewer
+        // bytes per MFMA (C3's gate|up: 184 -> 156 us); the STORE products
+        // gain only through more splits, whose partials cost the consumer
+        p->bm = 128;
+        p->nst = 3;
+    }
     const long tiles = (long)((M + p->bm - 1) / p->bm) * ((N + QK_GEMM_BN - 1) / QK_GEMM_BN);
     const int kt = (K + QK_BK - 1) / QK_BK;
     long ns;

@@ -223,7 +223,8 @@ int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride,
 
 enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2, QK_GEMM_ROPE = 3 /* plans only */ };
 /* Tiling of one M x N x K product: block rows bm x columns bn (32 / 64 x
- * QK_GEMM_BN on the LDS ring of nst stages, 32 / 64 / 128 x QK_GEMM_BN
+ * QK_GEMM_BN on the LDS ring of nst stages, 128 x QK_GEMM_BN on a 3-stage
+ * ring for SwiGLU products above 512 rows, 32 / 64 / 128 x QK_GEMM_BN
  * register-staged (nst 0), or 128 / 256 x 256 for large M), and nsplit slices
  * of kc (a multiple of 64) along K so a launch has enough blocks. */
 #define QK_GEMM_BN 128

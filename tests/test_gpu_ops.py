@@ -115,6 +115,28 @@ def test_gemm_epilogues(P, qa, gpu, M, N, K, bm, bn, nst, epi):
     p = GemmPlan()
     lib.qk_gemm_plan_for(M, N, K, C.byref(p))
     assert (p.bm, p.bn, p.nst) == (bm, bn, nst), (p.bm, p.bn, p.nst, p.nsplit)
+    check_gemm(P, qa, gpu, M, N, K, p, epi)
+
+
+# the 128 x 128 tiles on the 3-stage ring that a SwiGLU product above 512 rows
+# is planned on, with each epilogue, in one split (N 4096: 384 tiles) and in two
+# (N 2048: 192 tiles; STORE partials, then the reduce pass with the epilogue);
+# a partial last row tile (1515 = 11 x 128 + 107)
+@pytest.mark.parametrize("N,ns", [(4096, 1), (2048, 2)])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_ring128(P, qa, gpu, N, ns, epi):
+    M, K = 1515, 1024
+    p = GemmPlan()
+    qa.lib().qk_gemm_plan_epi(M, N, K, 2, C.byref(p))
+    assert (p.bm, p.bn, p.nst, p.nsplit) == (128, 128, 3, ns)
+    check_gemm(P, qa, gpu, M, N, K, p, epi)
+
+
+def check_gemm(P, qa, gpu, M, N, K, p, epi):
+    """Run qk_gemm_launch with plan p and epilogue epi (split plans: STORE
+    partials, then the reduce pass with the epilogue) against an fp64 product
+    of the same bf16 hi/lo operands, within the fp32 accumulation bound."""
+    lib = qa.lib()
     W = P.synth_bf16(N * K, 2, 9400 + N).reshape(N, K)
     x = P.synth_f32(M * K, 2, 9500 + M).reshape(M, K)
     hi = P.f32_to_bf16(x)
