@@ -80,57 +80,71 @@ __global__ __launch_bounds__(RN_THREADS) void rmsnorm_split(float *x, const floa
 }
 
 // Tall inputs: one wave per row, four rows per block, D / 64 elements per
-// lane; partials are summed in split order and then added, as above.
-template <int DPL>
+// lane in 16-byte pieces (lane l holds elements 256 j + 4 l .. + 3); partials
+// are summed in split order and then added, as above.
+template <int Q>
 __global__ __launch_bounds__(256) void rmsnorm_split_rows(float *x, const float *part, int nsum, long pstride,
                                                           const float *w, int S, float eps, uint16_t *hi,
                                                           uint16_t *lo) {
-    constexpr int D = 64 * DPL;
+    constexpr int D = 256 * Q;
     const int row = 4 * blockIdx.x + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= S) return;                                   // whole wave
-    float *xr = x + (size_t)row * D;
-    float v[DPL];
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * D) + lane;
+    float4 v[Q];
 #pragma unroll
-    for (int j = 0; j < DPL; j++) v[j] = xr[j * 64 + lane];
+    for (int j = 0; j < Q; j++) v[j] = xr[64 * j];
     if (nsum) {
-        float ps[DPL];
-        const float *pr = part + (size_t)row * D + lane;
+        const float4 *pr = reinterpret_cast<const float4 *>(part + (size_t)row * D) + lane;
+        const long ps4 = pstride / 4;
+        float4 ps[Q];
 #pragma unroll
-        for (int j = 0; j < DPL; j++) ps[j] = pr[j * 64];
+        for (int j = 0; j < Q; j++) ps[j] = pr[64 * j];
         for (int sp = 1; sp < nsum; sp += 2) {          // two splits' loads per round trip, summed in order
             const bool two = sp + 1 < nsum;
-            float a[DPL], b[DPL];
+            float4 a[Q], b[Q];
 #pragma unroll
-            for (int j = 0; j < DPL; j++) {
-                a[j] = pr[sp * pstride + j * 64];
-                b[j] = two ? pr[(sp + 1) * pstride + j * 64] : 0.0f;
+            for (int j = 0; j < Q; j++) {
+                a[j] = pr[sp * ps4 + 64 * j];
+                b[j] = two ? pr[(sp + 1) * ps4 + 64 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
-            for (int j = 0; j < DPL; j++) {
-                ps[j] += a[j];
-                if (two) ps[j] += b[j];
+            for (int j = 0; j < Q; j++) {
+                ps[j].x += a[j].x; ps[j].y += a[j].y; ps[j].z += a[j].z; ps[j].w += a[j].w;
+                if (two) { ps[j].x += b[j].x; ps[j].y += b[j].y; ps[j].z += b[j].z; ps[j].w += b[j].w; }
             }
         }
 #pragma unroll
-        for (int j = 0; j < DPL; j++) {
-            v[j] += ps[j];
-            xr[j * 64 + lane] = v[j];
+        for (int j = 0; j < Q; j++) {
+            v[j].x += ps[j].x; v[j].y += ps[j].y; v[j].z += ps[j].z; v[j].w += ps[j].w;
+            xr[64 * j] = v[j];
         }
     }
     float rinv = 1.0f;
     if (w) {
         float ss = 0.0f;
 #pragma unroll
-        for (int j = 0; j < DPL; j++) ss = fmaf(v[j], v[j], ss);
+        for (int j = 0; j < Q; j++) {
+            ss = fmaf(v[j].x, v[j].x, ss);
+            ss = fmaf(v[j].y, v[j].y, ss);
+            ss = fmaf(v[j].z, v[j].z, ss);
+            ss = fmaf(v[j].w, v[j].w, ss);
+        }
         ss = wave_sum(ss);
         rinv = 1.0f / sqrtf(ss / (float)D + eps);
     }
     if (!hi) return;
-    uint16_t *h = hi + (size_t)row * D, *l = lo + (size_t)row * D;
+    uint2 *h = reinterpret_cast<uint2 *>(hi + (size_t)row * D) + lane;
+    uint2 *l = reinterpret_cast<uint2 *>(lo + (size_t)row * D) + lane;
+    const float4 *w4 = w ? reinterpret_cast<const float4 *>(w) + lane : nullptr;
 #pragma unroll
-    for (int j = 0; j < DPL; j++) {
-        const int i = j * 64 + lane;
-        split2(w ? (v[j] * w[i]) * rinv : v[j], h[i], l[i]);
+    for (int j = 0; j < Q; j++) {
+        const float4 ww = w ? w4[64 * j] : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w}, we[4] = {ww.x, ww.y, ww.z, ww.w};
+        uint16_t hh[4], ll[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) split2(w ? (e[k] * we[k]) * rinv : e[k], hh[k], ll[k]);
+        h[64 * j] = make_uint2(hh[0] | ((unsigned)hh[1] << 16), hh[2] | ((unsigned)hh[3] << 16));
+        l[64 * j] = make_uint2(ll[0] | ((unsigned)ll[1] << 16), ll[2] | ((unsigned)ll[3] << 16));
     }
 }
 
@@ -180,11 +194,13 @@ extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, lo
     if (S <= 0 || D <= 0 || !x || nsum < 0 || nsum > QK_GEMM_MAX_SPLIT || (nsum && !part) || (!hi) != (!lo) ||
         (!hi && !nsum))
         return QWEN_HIP_EINVAL;
-    if (S >= 1024 && (D == 1024 || D == 2048)) {
+    const bool a16 = ((uintptr_t)x | (uintptr_t)part | (uintptr_t)w) % 16 == 0 && (uintptr_t)hi % 8 == 0 &&
+                     (uintptr_t)lo % 8 == 0 && (nsum <= 1 || pstride % 4 == 0);
+    if (S >= 1024 && (D == 1024 || D == 2048) && a16) {
         // tall inputs: a wave per row keeps the grid at S / 4 blocks
         const unsigned blocks = (unsigned)((S + 3) / 4);
-        if (D == 1024) rmsnorm_split_rows<16><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
-        else rmsnorm_split_rows<32><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
+        if (D == 1024) rmsnorm_split_rows<4><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
+        else rmsnorm_split_rows<8><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
     } else if (D == RN_THREADS) {
         rmsnorm_split_reg<1><<<S, RN_THREADS, 0, s>>>(x, part, nsum, pstride, w, eps, hi, lo);
     } else if (D == 2 * RN_THREADS) {
