@@ -688,17 +688,26 @@ __global__ __launch_bounds__(256) void gemm_hilo_ring_rope(const uint16_t *__res
             cv[k] = ra.rope_cos[p * hd + lane];
             sv[k] = ra.rope_sin[p * hd + lane];
         }
+        // the 16 rows' sums first (independent reductions, interleaved), then
+        // the per-row norm, rotation and stores; rows past M are computed on
+        // the tile's (finite) contents and not stored
+        float x1[16], x2[16], ss[16];
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const int rl = rl0 + k, srow = m0 + rl;
+            x1[k] = T[(rl0 + k) * RP_ROW + lane];
+            x2[k] = T[(rl0 + k) * RP_ROW + lane + half];
+            ss[k] = fmaf(x1[k], x1[k], x2[k] * x2[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++) ss[k] = wave_sum(ss[k]);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int srow = m0 + rl0 + k;
+            const float rinv = 1.0f / sqrtf(ss[k] / (float)hd + ra.eps);
+            const float y1 = (x1[k] * w1) * rinv, y2 = (x2[k] * w2) * rinv;
+            const float r1 = fmaf(y1, cv[k], -(y2 * sv[k]));
+            const float r2 = fmaf(y2, cv[k], y1 * sv[k]);
             if (srow < M) {                           // wave-uniform
-                float x1 = T[rl * RP_ROW + lane], x2 = T[rl * RP_ROW + lane + half];
-                const float ss = wave_sum(fmaf(x1, x1, x2 * x2));
-                const float rinv = 1.0f / sqrtf(ss / (float)hd + ra.eps);
-                x1 = (x1 * w1) * rinv;
-                x2 = (x2 * w2) * rinv;
-                const float r1 = fmaf(x1, cv[k], -(x2 * sv[k]));
-                const float r2 = fmaf(x2, cv[k], x1 * sv[k]);
                 float *d = is_q ? ra.q_out + (size_t)srow * qd + head * hd
                                 : ra.k_cache + ((size_t)(head - ra.heads) * ra.cap + ra.start + srow) * hd;
                 d[lane] = r1;
