@@ -234,6 +234,40 @@ def test_gemm_rope_epilogue(P, qa, gpu, M, K, start):
     assert np.all(outs[1][0][:, :start] == 7.0) and np.all(outs[1][0][:, start + M:] == 7.0)
 
 
+# the prefill RMSNorm that completes the residual: x += part[0] + ... (split
+# order), then hi/lo of rms_norm(x) * w; a wave per row above 1024 rows
+# (16-byte pieces), a block per row below; every split count the planner uses
+@pytest.mark.parametrize("S", [401, 1025])
+@pytest.mark.parametrize("D", [1024, 2048])
+@pytest.mark.parametrize("nsum", [0, 1, 2, 3])
+def test_rmsnorm_split(P, qa, gpu, S, D, nsum):
+    lib = qa.lib()
+    lib.qk_rmsnorm_split_launch.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_long, C.c_void_p, C.c_int, C.c_int,
+                                            C.c_float, C.c_void_p, C.c_void_p, C.c_void_p]
+    r = np.random.default_rng(S + D + nsum)
+    x = r.standard_normal((S, D)).astype(np.float32)
+    part = r.standard_normal((max(nsum, 1), S, D)).astype(np.float32)
+    w = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    dx, dp, dw = dev(gpu, x), dev(gpu, part), dev(gpu, w)
+    hi = gpu.zeros((S, D), dtype=gpu.int16, device="cuda")
+    lo = gpu.zeros((S, D), dtype=gpu.int16, device="cuda")
+    qa.check(lib.qk_rmsnorm_split_launch(ptr(dx), ptr(dp) if nsum else None, nsum, S * D, ptr(dw), S, D, 1e-6,
+                                         ptr(hi), ptr(lo), None), "rmsnorm_split")
+    gpu.cuda.synchronize()
+    v = x.copy()
+    if nsum:
+        ps = part[0].copy()
+        for k in range(1, nsum):
+            ps += part[k]
+        v += ps
+    assert np.array_equal(host(dx), v)                       # the same fp32 sums in the same order
+    v64 = v.astype(np.float64)
+    exp = v64 * w * (1.0 / np.sqrt((v64 * v64).mean(axis=1, keepdims=True) + 1e-6))
+    got = P.bf16_to_f32(host(hi).view(np.uint16)).astype(np.float64) + P.bf16_to_f32(host(lo).view(np.uint16))
+    # hi + lo carries ~2^-17 relative; rinv's sum is in another order (fp32)
+    assert np.all(np.abs(got - exp) <= 1e-5 * np.abs(exp) + 1e-6), float(np.max(np.abs(got - exp)))
+
+
 def test_elementwise_ops(P, qa, gpu):
     lib, orc = qa.lib(), P.orc_lib()
     r = np.random.default_rng(0)
