@@ -347,85 +347,116 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
     }
 }
 
-// One wave per (query, head), four per block: combine the splits of the
-// query's tile in split order (max, then rescaled sums), normalise, store.
+// The splits of one (query, head) combined in split order (max, then
+// rescaled sums) for the 4 dims of this lane: NB splits' loads in one round
+// trip (splits at or past n read split 0, finite, and weigh 0).
+template <int NB>
+__device__ __forceinline__ void pf_merge_batch(const float *p0, size_t stride, int s0, int n, int sl, float &M, float &L,
+                                               float4 &o, bool first_pass) {
+    float mv[NB], lv[NB];
+    float4 v[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const bool in = s0 + j < n;
+        const float *p = p0 + (in ? s0 + j : 0) * stride;
+        mv[j] = in ? p[QWEN_HIP_HEAD_DIM] : PF_MINIT;
+        lv[j] = p[QWEN_HIP_HEAD_DIM + 1];
+        if (!first_pass) v[j] = *reinterpret_cast<const float4 *>(p + 4 * sl);
+    }
+    if (first_pass) {                                     // the max over this batch only
+#pragma unroll
+        for (int j = 0; j < NB; j++) M = fmaxf(M, mv[j]);
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const float w = s0 + j < n ? __builtin_amdgcn_exp2f(mv[j] - M) : 0.0f;
+        L = fmaf(lv[j], w, L);
+        o.x = fmaf(v[j].x, w, o.x);
+        o.y = fmaf(v[j].y, w, o.y);
+        o.z = fmaf(v[j].z, w, o.z);
+        o.w = fmaf(v[j].w, w, o.w);
+    }
+}
+
+// 32 lanes per (query, head), 4 dims each, eight per block: combine the splits
+// of the query's tile in split order (max, then rescaled sums), normalise,
+// store.  Up to 8 splits take one round trip (the max from the same loads).
 __global__ __launch_bounds__(256) void attn_prefill_merge(qk_attn_args a) {
     constexpr int hd = QWEN_HIP_HEAD_DIM;
-    const long u = 4L * blockIdx.x + (threadIdx.x >> 6);
-    if (u >= (long)a.seq_q * a.heads) return;        // whole wave
-    const int qi = (int)(u / a.heads), h = (int)(u % a.heads), lane = threadIdx.x & 63;
+    const long u = 8L * blockIdx.x + (threadIdx.x >> 5);
+    if (u >= (long)a.seq_q * a.heads) return;        // a whole half wave
+    const int qi = (int)(u / a.heads), h = (int)(u % a.heads), sl = threadIdx.x & 31;
     const int t = qi / PF_Q;
     const int kend_tile = min(a.seq_k, a.q_offset + min(a.seq_q, (t + 1) * PF_Q));
-    int n = (kend_tile + a.chunk - 1) / a.chunk;
+    const int n = (kend_tile + a.chunk - 1) / a.chunk;
     const size_t stride = (size_t)a.seq_q * a.heads * QK_PF_PART;
     const float *p0 = a.part + ((size_t)qi * a.heads + h) * QK_PF_PART;
-    // batches of 8 splits: the loads of a batch are issued together, the sums
-    // still run in split order
-    constexpr int MB = 8;
-    float M = PF_MINIT;
-    float L = 0.0f, ox = 0.0f, oy = 0.0f;
-    if (n >= 1 && n <= MB) {
-        // one batch: every load in one round trip, then the same max and sums
-        float mv[MB], lv[MB];
-        float2 v[MB];
+    float M = PF_MINIT, L = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (n >= 1 && n <= 4) {
+        float mv[4], lv[4];
+        float4 v[4];
 #pragma unroll
-        for (int j = 0; j < MB; j++) {
+        for (int j = 0; j < 4; j++) {
             const bool in = j < n;
             const float *p = p0 + (in ? j : 0) * stride;
             mv[j] = in ? p[hd] : PF_MINIT;
             lv[j] = p[hd + 1];
-            v[j] = *reinterpret_cast<const float2 *>(p + 2 * lane);
+            v[j] = *reinterpret_cast<const float4 *>(p + 4 * sl);
         }
 #pragma unroll
-        for (int j = 0; j < MB; j++) M = fmaxf(M, mv[j]);
+        for (int j = 0; j < 4; j++) M = fmaxf(M, mv[j]);
 #pragma unroll
-        for (int j = 0; j < MB; j++) {
+        for (int j = 0; j < 4; j++) {
             const float w = j < n ? __builtin_amdgcn_exp2f(mv[j] - M) : 0.0f;
             L = fmaf(lv[j], w, L);
-            ox = fmaf(v[j].x, w, ox);
-            oy = fmaf(v[j].y, w, oy);
+            o.x = fmaf(v[j].x, w, o.x);
+            o.y = fmaf(v[j].y, w, o.y);
+            o.z = fmaf(v[j].z, w, o.z);
+            o.w = fmaf(v[j].w, w, o.w);
         }
-        n = 0;                                        // the loops below do nothing
-    }
-    for (int s0 = 0; s0 < n; s0 += MB) {
-        float mv[MB];
+    } else if (n >= 5 && n <= 8) {
+        float mv[8], lv[8];
+        float4 v[8];
 #pragma unroll
-        for (int j = 0; j < MB; j++) mv[j] = s0 + j < n ? p0[(s0 + j) * stride + hd] : PF_MINIT;
-#pragma unroll
-        for (int j = 0; j < MB; j++) M = fmaxf(M, mv[j]);
-    }
-    for (int s0 = 0; s0 < n; s0 += MB) {
-        float mv[MB], lv[MB];
-        float2 v[MB];
-#pragma unroll
-        for (int j = 0; j < MB; j++) {
-            const bool in = s0 + j < n;
-            const float *p = p0 + (in ? s0 + j : 0) * stride;
-            mv[j] = p[hd];
+        for (int j = 0; j < 8; j++) {
+            const bool in = j < n;
+            const float *p = p0 + (in ? j : 0) * stride;
+            mv[j] = in ? p[hd] : PF_MINIT;
             lv[j] = p[hd + 1];
-            v[j] = *reinterpret_cast<const float2 *>(p + 2 * lane);
+            v[j] = *reinterpret_cast<const float4 *>(p + 4 * sl);
         }
 #pragma unroll
-        for (int j = 0; j < MB; j++) {
-            // a split past n adds lv * 0 and v * 0 (finite values of split 0): no change
-            const float w = s0 + j < n ? __builtin_amdgcn_exp2f(mv[j] - M) : 0.0f;
+        for (int j = 0; j < 8; j++) M = fmaxf(M, mv[j]);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float w = j < n ? __builtin_amdgcn_exp2f(mv[j] - M) : 0.0f;
             L = fmaf(lv[j], w, L);
-            ox = fmaf(v[j].x, w, ox);
-            oy = fmaf(v[j].y, w, oy);
+            o.x = fmaf(v[j].x, w, o.x);
+            o.y = fmaf(v[j].y, w, o.y);
+            o.z = fmaf(v[j].z, w, o.z);
+            o.w = fmaf(v[j].w, w, o.w);
         }
+    } else {
+        // batches of 8: the max over all splits first, then the sums
+        for (int s0 = 0; s0 < n; s0 += 8) pf_merge_batch<8>(p0, stride, s0, n, sl, M, L, o, true);
+        for (int s0 = 0; s0 < n; s0 += 8) pf_merge_batch<8>(p0, stride, s0, n, sl, M, L, o, false);
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    const size_t base = (size_t)qi * a.heads * hd + h * hd + 2 * lane;
+    const size_t base = (size_t)qi * a.heads * hd + h * hd + 4 * sl;
+    const float e[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
     if (a.out) {
-        *reinterpret_cast<float2 *>(a.out + base) = make_float2(ox * inv, oy * inv);
+        *reinterpret_cast<float4 *>(a.out + base) = make_float4(e[0], e[1], e[2], e[3]);
     } else {
-        const float e[2] = {ox * inv, oy * inv};
+        uint16_t hh[4], ll[4];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint16_t hi = f32_to_bf16_rne(e[i]);
-            a.out_hi[base + i] = hi;
-            a.out_lo[base + i] = f32_to_bf16_rne(e[i] - bf16_to_f32(hi));
+        for (int i = 0; i < 4; i++) {
+            hh[i] = f32_to_bf16_rne(e[i]);
+            ll[i] = f32_to_bf16_rne(e[i] - bf16_to_f32(hh[i]));
         }
+        *reinterpret_cast<uint2 *>(a.out_hi + base) = make_uint2(hh[0] | ((unsigned)hh[1] << 16), hh[2] | ((unsigned)hh[3] << 16));
+        *reinterpret_cast<uint2 *>(a.out_lo + base) = make_uint2(ll[0] | ((unsigned)ll[1] << 16), ll[2] | ((unsigned)ll[3] << 16));
     }
 }
 
@@ -479,6 +510,6 @@ extern "C" int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s) {
     if ((long)a->chunk * a->nsplit < kmax) return QWEN_HIP_EINVAL;
     attn_prefill<<<dim3(nq * a->kv_heads, 1, a->nsplit), 256, 0, s>>>(*a);
     if (a->nsplit > 1)
-        attn_prefill_merge<<<(unsigned)(((long)a->seq_q * a->heads + 3) / 4), 256, 0, s>>>(*a);
+        attn_prefill_merge<<<(unsigned)(((long)a->seq_q * a->heads + 7) / 8), 256, 0, s>>>(*a);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
