@@ -189,6 +189,65 @@ __global__ __launch_bounds__(RN_THREADS) void rmsnorm_split_reg(float *x, const 
     }
 }
 
+// One 256-thread block per row, 4 consecutive elements per thread and
+// 16-byte piece (D = 1024 V4): the same sums and products as rmsnorm_split
+// (partials in split order, each split's loads issued together), a
+// four-wave reduction of the squares.
+template <int V4>
+__global__ __launch_bounds__(256) void rmsnorm_split_vec(float *x, const float *part, int nsum, long pstride,
+                                                         const float *w, float eps, uint16_t *hi, uint16_t *lo) {
+    constexpr int D = 1024 * V4;
+    __shared__ float red[4];
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)blockIdx.x * D) + threadIdx.x;
+    float4 v[V4];
+#pragma unroll
+    for (int e = 0; e < V4; e++) v[e] = xr[256 * e];
+    if (nsum) {
+        const float4 *pr = reinterpret_cast<const float4 *>(part + (size_t)blockIdx.x * D) + threadIdx.x;
+        const long ps4 = pstride / 4;
+#pragma unroll
+        for (int e = 0; e < V4; e++) {
+            float4 q[QK_GEMM_MAX_SPLIT];
+#pragma unroll
+            for (int sp = 0; sp < QK_GEMM_MAX_SPLIT; sp++)
+                q[sp] = sp < nsum ? pr[sp * ps4 + 256 * e] : make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 acc = q[0];
+#pragma unroll
+            for (int sp = 1; sp < QK_GEMM_MAX_SPLIT; sp++)
+                if (sp < nsum) { acc.x += q[sp].x; acc.y += q[sp].y; acc.z += q[sp].z; acc.w += q[sp].w; }
+            v[e].x += acc.x; v[e].y += acc.y; v[e].z += acc.z; v[e].w += acc.w;
+            xr[256 * e] = v[e];
+        }
+    }
+    float rinv = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < V4; e++) {
+            ss = fmaf(v[e].x, v[e].x, ss);
+            ss = fmaf(v[e].y, v[e].y, ss);
+            ss = fmaf(v[e].z, v[e].z, ss);
+            ss = fmaf(v[e].w, v[e].w, ss);
+        }
+        ss = block_sum<4>(ss, red);
+        rinv = 1.0f / sqrtf(ss / (float)D + eps);
+    }
+    if (!hi) return;
+    uint2 *h = reinterpret_cast<uint2 *>(hi + (size_t)blockIdx.x * D) + threadIdx.x;
+    uint2 *l = reinterpret_cast<uint2 *>(lo + (size_t)blockIdx.x * D) + threadIdx.x;
+    const float4 *w4 = w ? reinterpret_cast<const float4 *>(w) + threadIdx.x : nullptr;
+#pragma unroll
+    for (int e = 0; e < V4; e++) {
+        const float4 ww = w ? w4[256 * e] : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float el[4] = {v[e].x, v[e].y, v[e].z, v[e].w}, we[4] = {ww.x, ww.y, ww.z, ww.w};
+        uint16_t hh[4], ll[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) split2(w ? (el[k] * we[k]) * rinv : el[k], hh[k], ll[k]);
+        h[256 * e] = make_uint2(hh[0] | ((unsigned)hh[1] << 16), hh[2] | ((unsigned)hh[3] << 16));
+        l[256 * e] = make_uint2(ll[0] | ((unsigned)ll[1] << 16), ll[2] | ((unsigned)ll[3] << 16));
+    }
+}
+
 extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride, const float *w, int S,
                                        int D, float eps, uint16_t *hi, uint16_t *lo, hipStream_t s) {
     if (S <= 0 || D <= 0 || !x || nsum < 0 || nsum > QK_GEMM_MAX_SPLIT || (nsum && !part) || (!hi) != (!lo) ||
@@ -201,6 +260,9 @@ extern "C" int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, lo
         const unsigned blocks = (unsigned)((S + 3) / 4);
         if (D == 1024) rmsnorm_split_rows<4><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
         else rmsnorm_split_rows<8><<<blocks, 256, 0, s>>>(x, part, nsum, pstride, w, S, eps, hi, lo);
+    } else if ((D == 1024 || D == 2048) && a16) {
+        if (D == 1024) rmsnorm_split_vec<1><<<S, 256, 0, s>>>(x, part, nsum, pstride, w, eps, hi, lo);
+        else rmsnorm_split_vec<2><<<S, 256, 0, s>>>(x, part, nsum, pstride, w, eps, hi, lo);
     } else if (D == RN_THREADS) {
         rmsnorm_split_reg<1><<<S, RN_THREADS, 0, s>>>(x, part, nsum, pstride, w, eps, hi, lo);
     } else if (D == 2 * RN_THREADS) {
