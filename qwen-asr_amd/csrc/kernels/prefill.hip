@@ -866,11 +866,10 @@ extern "C" void qk_gemm_plan_epi(int M, int N, int K, int epi, qk_gemm_plan *p) 
     p->bn = QK_GEMM_BN;
     p->bm = M <= 32 ? 32 : (ring || M <= 512) ? 64 : 128;
     p->nst = ring ? QK_GEMM_RING_NST : 0;
-    if (ring && epi == QK_GEMM_SWIGLU && M > 512) {
-        // a SwiGLU product of more than 512 rows: 128 x 128 tiles (8 waves of
-        // 32 x 64, 3 stages = 72 KB, two blocks per CU) move a quarter fewer
-        // bytes per MFMA (C3's gate|up: 184 -> 156 us); the STORE products
-        // gain only through more splits, whose partials cost the consumer
+    if (ring && (epi == QK_GEMM_SWIGLU || epi == QK_GEMM_STORE) && M > 512) {
+        // more than 512 rows: 128 x 128 tiles (8 waves of 32 x 64, 3 stages =
+        // 72 KB, two blocks per CU) move a quarter fewer bytes per MFMA (C3's
+        // gate|up: 184 -> 156 us, down 103 -> 79 us, O 34.8 -> 33.8 us)
         p->bm = 128;
         p->nst = 3;
     }
@@ -886,6 +885,11 @@ extern "C" void qk_gemm_plan_epi(int M, int N, int K, int epi, qk_gemm_plan *p) 
         // reduce pass, and a Q|K|V product whose RoPE epilogue needs one split
         ns = (QK_GEMM_RING_TARGET + tiles - 1) / tiles;
         if (ns < 2 && K >= QK_GEMM_RING_KSPLIT && epi != QK_GEMM_SWIGLU && epi != QK_GEMM_ROPE) ns = 2;
+        // 128 x 128 STORE tiles: two splits per 4096 of K.  Odd counts leave a
+        // part-empty last round of blocks (C3's down, K 6144: 3 splits 93 us,
+        // 4 splits 79 us, 2 splits 94 us; 1024-column products: 2 splits 29 us
+        // against 3 splits 37 us)
+        if (p->bm == 128 && epi == QK_GEMM_STORE) ns = 2 * ((K + 4095) / 4096);
     } else {
         ns = tiles >= QK_GEMM_TARGET ? 1 : (QK_GEMM_TARGET + tiles - 1) / tiles;
     }

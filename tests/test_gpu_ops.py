@@ -102,11 +102,13 @@ class GemmPlan(C.Structure):
 # plans: 256 x 256 and 128 x 256 (wide direct-to-LDS rings; M not a multiple
 # of the tile, k walks shorter than the ring), 64 x 128 and 32 x 128 on the
 # 4-stage ring (one split, and split with the partials summed by the reduce
-# pass with the epilogue), register-staged 64 x 128 and split 128 x 128 (N
-# not a multiple of 128, K not of 32)
+# pass with the epilogue), 128 x 128 on the 3-stage ring above 512 rows (four
+# 1536-deep splits of K 6144), register-staged 64 x 128 and split 128 x 128
+# (N not a multiple of 128, K not of 32)
 @pytest.mark.parametrize("M,N,K,bm,bn,nst", [(1000, 16384, 64, 256, 256, 0), (4000, 4096, 96, 256, 256, 0),
                                              (4000, 2048, 96, 128, 256, 0), (2000, 4096, 32, 128, 256, 0),
-                                             (401, 6144, 1024, 64, 128, 4), (1515, 1024, 512, 64, 128, 4),
+                                             (401, 6144, 1024, 64, 128, 4), (401, 1024, 2048, 64, 128, 4),
+                                             (700, 1024, 6144, 128, 128, 3),
                                              (31, 4096, 1024, 32, 128, 4), (100, 1000, 512, 64, 128, 0),
                                              (1515, 1000, 520, 128, 128, 0)])
 @pytest.mark.parametrize("epi", [0, 1, 2])
@@ -118,8 +120,8 @@ def test_gemm_epilogues(P, qa, gpu, M, N, K, bm, bn, nst, epi):
     check_gemm(P, qa, gpu, M, N, K, p, epi)
 
 
-# the 128 x 128 tiles on the 3-stage ring that a SwiGLU product above 512 rows
-# is planned on, with each epilogue, in one split (N 4096: 384 tiles) and in two
+# the 128 x 128 tiles on the 3-stage ring that a SwiGLU or STORE product above
+# 512 rows is planned on, with each epilogue, in one split (N 4096: 384 tiles) and in two
 # (N 2048: 192 tiles; STORE partials, then the reduce pass with the epilogue);
 # a partial last row tile (1515 = 11 x 128 + 107)
 @pytest.mark.parametrize("N,ns", [(4096, 1), (2048, 2)])

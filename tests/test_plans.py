@@ -33,6 +33,8 @@ def test_gemm_plan_invariants(qa, M, N, K):
         assert (p.bm, p.bn, p.nsplit, p.nst) == (256, 256, 1, 0)
     elif fills(128):
         assert (p.bm, p.bn, p.nsplit, p.nst) == (128, 256, 1, 0)
+    elif ring and M > 512:                                             # LDS ring, 128 x 128 on 3 stages
+        assert (p.bm, p.bn, p.nst) == (128, 128, 3)
     elif ring:                                                         # LDS ring, 4 stages
         assert (p.bn, p.nst) == (128, 4) and p.bm == (32 if M <= 32 else 64)
     else:                                                              # register-staged
@@ -41,7 +43,11 @@ def test_gemm_plan_invariants(qa, M, N, K):
     assert 1 <= p.nsplit <= 16
     assert p.kc * p.nsplit >= K and p.kc * (p.nsplit - 1) < K       # every slice non-empty, K covered once
     tiles = -(-M // p.bm) * -(-N // p.bn)
-    if p.nst:
+    if p.nst == 3:
+        # 128 x 128 tiles: two splits per 4096 of K (an even count)
+        want = min(2 * -(-K // 4096), 16, -(-K // 64))
+        assert p.kc == -(-(-(-K // 64)) // want) * 64
+    elif p.nst:
         # about 224 blocks, and k walks of 2048 or more in two halves at least
         # (within the 16-split cap and whole 64-deep k tiles)
         want = min(max(-(-224 // tiles), 2 if K >= 2048 else 1), 16, -(-K // 64))
@@ -56,14 +62,15 @@ def test_gemm_plan_swiglu_rope(qa, M, N, K, epi):
     """A SwiGLU product (epilogue 2) and the Q|K|V product with the RoPE
     epilogue (3) split K only to fill the chip: SwiGLU's split partials (twice
     its output) need a reduce pass, and the RoPE epilogue runs on one split;
-    a SwiGLU product above 512 rows that goes to the LDS ring takes 128 x 128
-    tiles on 3 stages; otherwise they are planned like any other product."""
+    above 512 rows on the LDS ring a SwiGLU product takes the 128 x 128 tiles
+    on 3 stages of the STORE products and the Q|K|V + RoPE product the 64 x
+    128 tiles on 4 stages; otherwise they are planned like any other product."""
     lib = qa.lib()
     p, q = GemmPlan(), GemmPlan()
     lib.qk_gemm_plan_for(M, N, K, C.byref(p))
     lib.qk_gemm_plan_epi(M, N, K, epi, C.byref(q))
-    if epi == 2 and p.nst and M > 512:
-        assert (q.bm, q.bn, q.nst) == (128, 128, 3)
+    if epi == 3 and p.nst and M > 512:
+        assert (q.bm, q.bn, q.nst) == (64, 128, 4)
     else:
         assert (q.bm, q.bn, q.nst) == (p.bm, p.bn, p.nst)
     assert q.kc * q.nsplit >= K and q.kc * (q.nsplit - 1) < K and q.kc % 64 == 0
