@@ -718,11 +718,28 @@ __global__ __launch_bounds__(256) void gemm_hilo_ring_rope(const uint16_t *__res
     constexpr int WGN = RS::WGN, WTN = RS::WTN, TM = RS::TM, TN = RS::TN, hd = QWEN_HIP_HEAD_DIM, half = hd / 2;
     __shared__ __attribute__((aligned(1024))) unsigned char lds[QK_GEMM_RING_NST * RS::STAGE];
     static_assert(64 * RP_ROW * sizeof(float) <= sizeof(lds), "staged tile");
-    f32x4 acc[TM][TN];
-    ring_tile<64, QWEN_HIP_HEAD_DIM, QK_GEMM_RING_NST>(ahi, alo, W, M, K, K, lds, acc);
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     const int m0 = blockIdx.y * 64, head = blockIdx.x;
+    const int nqk = ra.heads + ra.kv_heads, qd = ra.heads * hd;
+    const bool is_q = head < ra.heads, is_k = !is_q && head < nqk;
+    const int rl0 = 16 * wave;                        // this wave's 16 rows of the tile
+    // the epilogue's operands (the rows' cos / sin, the norm weights) are
+    // loaded before the k walk, so their latency passes under it
+    float cv[16], sv[16], w1 = 0.f, w2 = 0.f;
+    if (is_q || is_k) {
+        const float *nw = is_q ? ra.q_norm : ra.k_norm;
+        w1 = nw[lane];
+        w2 = nw[lane + half];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const size_t p = (size_t)ra.start + min(m0 + rl0 + k, M - 1);
+            cv[k] = ra.rope_cos[p * hd + lane];
+            sv[k] = ra.rope_sin[p * hd + lane];
+        }
+    }
+    f32x4 acc[TM][TN];
+    ring_tile<64, QWEN_HIP_HEAD_DIM, QK_GEMM_RING_NST>(ahi, alo, W, M, K, K, lds, acc);
 
     __syncthreads();                                   // every wave is past its last k step
     float *T = reinterpret_cast<float *>(lds);         // [64][RP_ROW]
@@ -735,21 +752,7 @@ __global__ __launch_bounds__(256) void gemm_hilo_ring_rope(const uint16_t *__res
                 T[(wm * 32 + i * 16 + 4 * (lane >> 4) + r) * RP_ROW + wn * WTN + j * 16 + (lane & 15)] = acc[i][j][r];
     __syncthreads();
 
-    const int nqk = ra.heads + ra.kv_heads, qd = ra.heads * hd;
-    const bool is_q = head < ra.heads, is_k = !is_q && head < nqk;
-    const int rl0 = 16 * wave;                        // this wave's 16 rows of the tile
     if (is_q || is_k) {
-        // the rows' cos / sin and the norm weights are loaded up front, so the
-        // row loop below waits for memory once
-        const float *nw = is_q ? ra.q_norm : ra.k_norm;
-        const float w1 = nw[lane], w2 = nw[lane + half];
-        float cv[16], sv[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const size_t p = (size_t)ra.start + min(m0 + rl0 + k, M - 1);
-            cv[k] = ra.rope_cos[p * hd + lane];
-            sv[k] = ra.rope_sin[p * hd + lane];
-        }
         // the 16 rows' sums first (independent reductions, interleaved), then
         // the per-row norm, rotation and stores; rows past M are computed on
         // the tile's (finite) contents and not stored
