@@ -158,6 +158,44 @@ def test_long_prefill_wide_kernels(P, qa, gpu):
     d.close()
 
 
+@pytest.mark.parametrize("S", [512, 513])
+def test_prefill_tile_plan_edge(P, qa, gpu, S):
+    """Prefills on either side of the 512-row switch of the GEMM plans (0.6B
+    layer shape, two layers, 4096-token vocabulary): 512 rows run every
+    projection on 64 x 128 ring tiles; 513 rows run O, gate|up and down on
+    128 x 128 tiles (five row tiles, the last holding one row; O and down in
+    two splits) and Q|K|V + RoPE on 64 x 128.  The next token's logits and
+    final hidden state are checked against the CPU oracle."""
+    import ctypes as C
+
+    class GemmPlan(C.Structure):
+        _fields_ = [("bm", C.c_int), ("nsplit", C.c_int), ("kc", C.c_int), ("bn", C.c_int), ("nst", C.c_int)]
+
+    lib = qa.lib()
+    want_bm = 64 if S <= 512 else 128
+    for n, k, epi in ((1024, 2048, 0), (6144, 1024, 2), (1024, 3072, 0)):
+        p = GemmPlan()
+        lib.qk_gemm_plan_epi(S, n, k, epi, C.byref(p))
+        assert (p.bm, p.bn) == (want_bm, 128), (n, k, p.bm, p.bn, p.nst, p.nsplit)
+    m = P.SynthModel(P.Config(1024, 2, 16, 8, 128, 3072, 4096), seed=4, norm_std=0.1)
+    rows, _ = P.prompt_rows(m, S - 5, 6, seed=4)
+    o = P.Oracle(m, threads=16)
+    o.prefill(rows[:-1])
+    to, lo, ho = o.forward(rows[-1], True, True)
+    d = make_decoder(qa, P, m, kv_capacity=S + 64)
+    d.set_keep_logits(True)
+    d.prefill(rows[:-1])
+    td = d.forward(rows[-1])
+    lg, hid = d.read_logits(), d.read_hidden()
+    print(f"{S}-row prefill: max |dlogit| {np.abs(lg - lo).max():.2e}, max |dhidden| {np.abs(hid - ho).max():.2e}")
+    assert close(lg, lo)
+    np.testing.assert_allclose(hid, ho, atol=1e-3, rtol=1e-3)
+    if td != to:
+        s = np.sort(lo)
+        assert s[-1] - s[-2] < TIE
+    d.close()
+
+
 def test_tiny_long_context_crosses_step_variants(P, qa, tiny):
     """Decode attention switches from <= 8 splits merged in the O-projection
     (<= 2048 keys) to up to 32 splits + a merge kernel: logits on both sides
