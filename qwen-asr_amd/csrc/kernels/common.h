@@ -222,6 +222,52 @@ __device__ __forceinline__ void reduce_rows(float (&v)[ROWS], int lane) {
     for (int i = 0; i < KEEP; i++) v[i] = group_sum<G>(v[i]);
 }
 
+// One 128-wide head row held by a 16-lane group: lane c (= lane % 16) owns
+// dims 4c .. 4c+3 (lo) and 64+4c .. 64+4c+3 (hi), i.e. four NeoX RoPE pairs
+// (d, d + 64).  RMSNorm with weights (wl, wh), then the rotation by (c4, s4)
+// (qwen_asr_kernels.c:811-873, :1182-1247).  The sum of squares is this
+// lane's 8 squares in pair order, then the 16 lanes' sums (xor 1, 2, 4, 8).
+__device__ __forceinline__ void norm_rope_row16(float4 &lo, float4 &hi, float4 wl, float4 wh, float4 c4, float4 s4,
+                                                float eps) {
+    float ss = fmaf(lo.x, lo.x, hi.x * hi.x);
+    ss = fmaf(lo.y, lo.y, ss);
+    ss = fmaf(hi.y, hi.y, ss);
+    ss = fmaf(lo.z, lo.z, ss);
+    ss = fmaf(hi.z, hi.z, ss);
+    ss = fmaf(lo.w, lo.w, ss);
+    ss = fmaf(hi.w, hi.w, ss);
+    ss = group_sum<16>(ss);
+    const float rinv = 1.0f / sqrtf(ss / 128.0f + eps);
+    const float a0 = (lo.x * wl.x) * rinv, a1 = (lo.y * wl.y) * rinv, a2 = (lo.z * wl.z) * rinv,
+                a3 = (lo.w * wl.w) * rinv;
+    const float b0 = (hi.x * wh.x) * rinv, b1 = (hi.y * wh.y) * rinv, b2 = (hi.z * wh.z) * rinv,
+                b3 = (hi.w * wh.w) * rinv;
+    lo = make_float4(fmaf(a0, c4.x, -(b0 * s4.x)), fmaf(a1, c4.y, -(b1 * s4.y)), fmaf(a2, c4.z, -(b2 * s4.z)),
+                     fmaf(a3, c4.w, -(b3 * s4.w)));
+    hi = make_float4(fmaf(b0, c4.x, a0 * s4.x), fmaf(b1, c4.y, a1 * s4.y), fmaf(b2, c4.z, a2 * s4.z),
+                     fmaf(b3, c4.w, a3 * s4.w));
+}
+
+// four consecutive elements summed over n split-K partials (stride floats
+// apart), each element in split order as sum_splits
+template <int N>
+__device__ __forceinline__ float4 sum_splits4(const float *p, int n, long stride) {
+    float4 v[N];
+#pragma unroll
+    for (int s = 0; s < N; s++)
+        v[s] = s < n ? *reinterpret_cast<const float4 *>(p + s * stride) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 acc = v[0];
+#pragma unroll
+    for (int s = 1; s < N; s++)
+        if (s < n) {
+            acc.x += v[s].x;
+            acc.y += v[s].y;
+            acc.z += v[s].z;
+            acc.w += v[s].w;
+        }
+    return acc;
+}
+
 // one lane pair (l, l+64) of a 128-wide head: RMSNorm with weight, then RoPE
 __device__ __forceinline__ void norm_rope_pair(float &x1, float &x2, const float *nw, float eps, float c, float sn,
                                                int lane) {

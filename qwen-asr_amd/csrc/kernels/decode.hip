@@ -352,22 +352,20 @@ extern "C" int qk_argmax_finish_launch(const float *cand_val, const int *cand_id
 }
 
 // ---------------------------------------------------------------------------
-// q/k RMSNorm + NeoX RoPE + K/V append.  One wave per (head, row); lane l
-// owns the RoPE pair (l, l+64) of the 128-wide head.
+// q/k RMSNorm + NeoX RoPE + K/V append.  A 16-lane group per (row, head);
+// lane c owns dims 4c .. 4c+3 and their RoPE partners 64+4c .. 64+4c+3
+// (norm_rope_row16).  Every access is a 16-byte vector.
 // ---------------------------------------------------------------------------
-// Element i of the projection row: the sum of its nsum split-K partials.
-__device__ __forceinline__ float qkv_at(const float *p, int nsum, long pstride) {
-    return sum_splits<QK_GEMM_MAX_SPLIT>(p, nsum, pstride);
-}
-
-// One wave per (row, head) unit, four units per block: unit u = 4 block + wave,
-// head = u % (heads + kv_heads) ([0, heads) q, then k/v), row = u / (heads + kv_heads).
+// Unit u = 16 block + 4 wave + lane / 16: head = u % (heads + kv_heads)
+// ([0, heads) q, then k/v), row = u / (heads + kv_heads).  NS: the most
+// split-K partials summed (1: the product as is).
+template <int NS>
 __global__ __launch_bounds__(256) void rope_append(qk_rope_append_args a) {
     const int hd = QWEN_HIP_HEAD_DIM, half = hd / 2;
-    const int lane = threadIdx.x & 63;
+    const int c = threadIdx.x & 15;
     const int nh = a.heads + a.kv_heads;
-    const long u = 4L * blockIdx.x + (threadIdx.x >> 6);
-    if (u >= (long)nh * a.S) return;            // whole wave
+    const long u = 16L * blockIdx.x + (threadIdx.x >> 4);
+    if (u >= (long)nh * a.S) return;            // the whole 16-lane group
     const int head = (int)(u % nh);
     const int srow = (int)(u / nh);
     const int start = a.pos_dev ? *a.pos_dev : a.start;
@@ -379,27 +377,21 @@ __global__ __launch_bounds__(256) void rope_append(qk_rope_append_args a) {
     const float *src = is_q ? row + head * hd : row + qd + kvh * hd;
     const float *nw = is_q ? a.q_norm : a.k_norm;
     const int ns = a.nsum > 0 ? a.nsum : 1;
-    float x1 = qkv_at(src + lane, ns, a.pstride), x2 = qkv_at(src + lane + half, ns, a.pstride);
-    float ss = fmaf(x1, x1, x2 * x2);
-    ss = wave_sum(ss);
-    const float rinv = 1.0f / sqrtf(ss / (float)hd + a.eps);
-    x1 = (x1 * nw[lane]) * rinv;
-    x2 = (x2 * nw[lane + half]) * rinv;
-    const float c = a.rope_cos[(size_t)p * hd + lane];
-    const float sn = a.rope_sin[(size_t)p * hd + lane];
-    const float r1 = fmaf(x1, c, -(x2 * sn));
-    const float r2 = fmaf(x2, c, x1 * sn);
-    if (is_q) {
-        float *dst = a.q_out + (size_t)srow * qd + head * hd;
-        dst[lane] = r1;
-        dst[lane + half] = r2;
-    } else {
-        const size_t off = ((size_t)kvh * a.cap + p) * hd;
-        a.k_cache[off + lane] = r1;
-        a.k_cache[off + lane + half] = r2;
+    float4 lo = sum_splits4<NS>(src + 4 * c, ns, a.pstride);
+    float4 hi = sum_splits4<NS>(src + half + 4 * c, ns, a.pstride);
+    const float4 wl = *reinterpret_cast<const float4 *>(nw + 4 * c);
+    const float4 wh = *reinterpret_cast<const float4 *>(nw + half + 4 * c);
+    const float4 c4 = *reinterpret_cast<const float4 *>(a.rope_cos + (size_t)p * hd + 4 * c);
+    const float4 s4 = *reinterpret_cast<const float4 *>(a.rope_sin + (size_t)p * hd + 4 * c);
+    norm_rope_row16(lo, hi, wl, wh, c4, s4, a.eps);
+    float *dst = is_q ? a.q_out + (size_t)srow * qd + head * hd : a.k_cache + ((size_t)kvh * a.cap + p) * hd;
+    *reinterpret_cast<float4 *>(dst + 4 * c) = lo;
+    *reinterpret_cast<float4 *>(dst + half + 4 * c) = hi;
+    if (!is_q) {
         const float *vs = row + qd + kvd + kvh * hd;
-        a.v_cache[off + lane] = qkv_at(vs + lane, ns, a.pstride);
-        a.v_cache[off + lane + half] = qkv_at(vs + lane + half, ns, a.pstride);
+        float *vd = a.v_cache + ((size_t)kvh * a.cap + p) * hd;
+        *reinterpret_cast<float4 *>(vd + 4 * c) = sum_splits4<NS>(vs + 4 * c, ns, a.pstride);
+        *reinterpret_cast<float4 *>(vd + half + 4 * c) = sum_splits4<NS>(vs + half + 4 * c, ns, a.pstride);
     }
 }
 
@@ -407,9 +399,14 @@ extern "C" int qk_rope_append_launch(const qk_rope_append_args *a, hipStream_t s
     if (!a || a->S <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads ||
         a->nsum > QK_GEMM_MAX_SPLIT)
         return QWEN_HIP_EINVAL;
+    // 16-byte accesses throughout
+    const uintptr_t al = (uintptr_t)a->qkv | (uintptr_t)a->q_norm | (uintptr_t)a->k_norm | (uintptr_t)a->rope_cos |
+                         (uintptr_t)a->rope_sin | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache | (uintptr_t)a->q_out;
+    if (al % 16 || (a->nsum > 1 && a->pstride % 4)) return QWEN_HIP_EINVAL;
     const long units = (long)(a->heads + a->kv_heads) * a->S;
-    if ((units + 3) / 4 > 0x7fffffffL) return QWEN_HIP_EINVAL;
-    rope_append<<<(unsigned)((units + 3) / 4), 256, 0, s>>>(*a);
+    if ((units + 15) / 16 > 0x7fffffffL) return QWEN_HIP_EINVAL;
+    if (a->nsum > 1) rope_append<QK_GEMM_MAX_SPLIT><<<(unsigned)((units + 15) / 16), 256, 0, s>>>(*a);
+    else rope_append<1><<<(unsigned)((units + 15) / 16), 256, 0, s>>>(*a);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
 }
 

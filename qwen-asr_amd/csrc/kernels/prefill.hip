@@ -705,10 +705,11 @@ __global__ __launch_bounds__(ring_waves(BM, BN) * 64) void gemm_hilo_ring(const 
 // on the product, reference qwen_asr_decoder.c:270-300): a 64 x 128 tile is
 // 64 rows of one head (Q heads, then K heads, then V heads along N).  The
 // tile goes to LDS (the ring is free after the k walk), then each wave takes
-// 16 rows and runs rope_append's per-row code on them: per-head RMSNorm and
-// NeoX rotation of dims (d, d + 64) for Q and K (Q to q_out, K to the cache),
-// V copied to the cache.  The sums and products are rope_append's, so the
-// result equals GEMM (STORE, one split) + rope_append bit for bit.
+// 16 rows, four at a time on its four 16-lane groups, and runs rope_append's
+// per-row code on them (norm_rope_row16): per-head RMSNorm and NeoX rotation
+// of dims (d, d + 64) for Q and K (Q to q_out, K to the cache), V copied to
+// the cache.  The sums and products are rope_append's, so the result equals
+// GEMM (STORE, one split) + rope_append bit for bit.
 #define RP_ROW (QWEN_HIP_HEAD_DIM + 4)        // floats per row of the staged tile
 __global__ __launch_bounds__(256) void gemm_hilo_ring_rope(const uint16_t *__restrict__ ahi,
                                                            const uint16_t *__restrict__ alo,
@@ -717,25 +718,27 @@ __global__ __launch_bounds__(256) void gemm_hilo_ring_rope(const uint16_t *__res
     using RS = RingShape<64, QWEN_HIP_HEAD_DIM>;
     constexpr int WGN = RS::WGN, WTN = RS::WTN, TM = RS::TM, TN = RS::TN, hd = QWEN_HIP_HEAD_DIM, half = hd / 2;
     __shared__ __attribute__((aligned(1024))) unsigned char lds[QK_GEMM_RING_NST * RS::STAGE];
-    static_assert(64 * RP_ROW * sizeof(float) <= sizeof(lds), "staged tile");
+    static_assert(64 * RP_ROW * sizeof(float) <= sizeof(lds) && RP_ROW % 4 == 0, "staged tile");
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     const int m0 = blockIdx.y * 64, head = blockIdx.x;
     const int nqk = ra.heads + ra.kv_heads, qd = ra.heads * hd;
     const bool is_q = head < ra.heads, is_k = !is_q && head < nqk;
-    const int rl0 = 16 * wave;                        // this wave's 16 rows of the tile
+    // this wave's 16 rows of the tile: row rl0 + 4 k + g in pass k for the
+    // 16-lane group g, whose lane c holds dims 4c .. 4c+3 and 64+4c .. 64+4c+3
+    const int rl0 = 16 * wave, g = lane >> 4, c = lane & 15;
     // the epilogue's operands (the rows' cos / sin, the norm weights) are
     // loaded before the k walk, so their latency passes under it
-    float cv[16], sv[16], w1 = 0.f, w2 = 0.f;
+    float4 cv[4], sv[4], wl = make_float4(0.f, 0.f, 0.f, 0.f), wh = wl;
     if (is_q || is_k) {
         const float *nw = is_q ? ra.q_norm : ra.k_norm;
-        w1 = nw[lane];
-        w2 = nw[lane + half];
+        wl = *reinterpret_cast<const float4 *>(nw + 4 * c);
+        wh = *reinterpret_cast<const float4 *>(nw + half + 4 * c);
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const size_t p = (size_t)ra.start + min(m0 + rl0 + k, M - 1);
-            cv[k] = ra.rope_cos[p * hd + lane];
-            sv[k] = ra.rope_sin[p * hd + lane];
+        for (int k = 0; k < 4; k++) {
+            const size_t p = (size_t)ra.start + min(m0 + rl0 + 4 * k + g, M - 1);
+            cv[k] = *reinterpret_cast<const float4 *>(ra.rope_cos + p * hd + 4 * c);
+            sv[k] = *reinterpret_cast<const float4 *>(ra.rope_sin + p * hd + 4 * c);
         }
     }
     f32x4 acc[TM][TN];
@@ -752,42 +755,23 @@ __global__ __launch_bounds__(256) void gemm_hilo_ring_rope(const uint16_t *__res
                 T[(wm * 32 + i * 16 + 4 * (lane >> 4) + r) * RP_ROW + wn * WTN + j * 16 + (lane & 15)] = acc[i][j][r];
     __syncthreads();
 
-    if (is_q || is_k) {
-        // the 16 rows' sums first (independent reductions, interleaved), then
-        // the per-row norm, rotation and stores; rows past M are computed on
-        // the tile's (finite) contents and not stored
-        float x1[16], x2[16], ss[16];
+    // rows past M are computed on the tile's (finite) contents and not stored
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            x1[k] = T[(rl0 + k) * RP_ROW + lane];
-            x2[k] = T[(rl0 + k) * RP_ROW + lane + half];
-            ss[k] = fmaf(x1[k], x1[k], x2[k] * x2[k]);
+    for (int k = 0; k < 4; k++) {
+        const int rl = rl0 + 4 * k + g, srow = m0 + rl;
+        float4 lo = *reinterpret_cast<const float4 *>(T + rl * RP_ROW + 4 * c);
+        float4 hi = *reinterpret_cast<const float4 *>(T + rl * RP_ROW + half + 4 * c);
+        float *d;
+        if (is_q || is_k) {
+            norm_rope_row16(lo, hi, wl, wh, cv[k], sv[k], ra.eps);
+            d = is_q ? ra.q_out + (size_t)srow * qd + head * hd
+                     : ra.k_cache + ((size_t)(head - ra.heads) * ra.cap + ra.start + srow) * hd;
+        } else {
+            d = ra.v_cache + ((size_t)(head - nqk) * ra.cap + ra.start + srow) * hd;
         }
-#pragma unroll
-        for (int k = 0; k < 16; k++) ss[k] = wave_sum(ss[k]);
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const int srow = m0 + rl0 + k;
-            const float rinv = 1.0f / sqrtf(ss[k] / (float)hd + ra.eps);
-            const float y1 = (x1[k] * w1) * rinv, y2 = (x2[k] * w2) * rinv;
-            const float r1 = fmaf(y1, cv[k], -(y2 * sv[k]));
-            const float r2 = fmaf(y2, cv[k], y1 * sv[k]);
-            if (srow < M) {                           // wave-uniform
-                float *d = is_q ? ra.q_out + (size_t)srow * qd + head * hd
-                                : ra.k_cache + ((size_t)(head - ra.heads) * ra.cap + ra.start + srow) * hd;
-                d[lane] = r1;
-                d[lane + half] = r2;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const int rl = rl0 + k, srow = m0 + rl;
-            if (srow < M) {
-                float *d = ra.v_cache + ((size_t)(head - nqk) * ra.cap + ra.start + srow) * hd;
-                d[lane] = T[rl * RP_ROW + lane];
-                d[lane + half] = T[rl * RP_ROW + lane + half];
-            }
+        if (srow < M) {
+            *reinterpret_cast<float4 *>(d + 4 * c) = lo;
+            *reinterpret_cast<float4 *>(d + half + 4 * c) = hi;
         }
     }
 }
@@ -802,6 +786,10 @@ extern "C" int qk_gemm_rope_launch(const uint16_t *a_hi, const uint16_t *a_lo, c
         p->kc < K || ra->S != M || ra->pos_dev || ra->nsum > 1 || ra->heads <= 0 || ra->kv_heads <= 0 ||
         ra->heads % ra->kv_heads || !ra->q_norm || !ra->k_norm || !ra->rope_cos || !ra->rope_sin ||
         !ra->k_cache || !ra->v_cache || !ra->q_out || ra->start < 0 || ra->start + M > ra->cap)
+        return QWEN_HIP_EINVAL;
+    // 16-byte accesses in the epilogue
+    if (((uintptr_t)ra->q_norm | (uintptr_t)ra->k_norm | (uintptr_t)ra->rope_cos | (uintptr_t)ra->rope_sin |
+         (uintptr_t)ra->k_cache | (uintptr_t)ra->v_cache | (uintptr_t)ra->q_out) % 16)
         return QWEN_HIP_EINVAL;
     const dim3 grid(ra->heads + 2 * ra->kv_heads, (M + 63) / 64);
     gemm_hilo_ring_rope<<<grid, 256, 0, s>>>(a_hi, a_lo, W, M, K, *ra);
