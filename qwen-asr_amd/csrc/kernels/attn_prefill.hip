@@ -14,9 +14,9 @@
 // + i] and B[8 (l >> 4) + i][l & 15], i = 0..7; the result D[4 (l >> 4) + r][l & 15],
 // r = 0..3, lands in lane l.
 //
-// A block owns one kv head, 64 consecutive queries of both query heads that
-// share it (4 waves: head = wave & 1, queries 32 (wave >> 1) .. + 32) and one
-// split of the key range.  Per 32-key tile staged in LDS (K rows and V^T,
+// A block owns one kv head, 64 (or 128) consecutive queries of both query
+// heads that share it (4 or 8 waves: head = wave & 1, queries 32 (wave >> 1)
+// .. + 32) and one split of the key range.  Per 32-key tile staged in LDS (K rows and V^T,
 // split into hi / lo once per block):
 //   S^T = K Q^T   A = K rows (keys), B = this wave's queries, 32 dims per
 //                 k-step; Q is split once, in registers.
@@ -83,42 +83,50 @@ __device__ __forceinline__ f32x4 pf_mfma3(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x
 // store instruction a wave covers 8 dims x 8 key groups, which the swizzled
 // V^T rows take without bank conflicts (the 32 lanes of a half wave land in
 // 32 distinct bank pairs).
+// NW waves stage a tile (NW = 4 or 8): per thread 16 / NW K float4s and
+// 16 / NW V groups of 4 keys.
+template <int NW>
 struct PfStage {
-    float4 k[4];     // K rows: float4 (tid + 256 i): key (.. >> 5), dims 4 (.. & 31)
-    float v[16];     // V: dim pf_vdim(wave, lane, j), keys 4 pf_vgrp(lane) + e
+    float4 k[16 / NW];   // K rows: float4 (tid + 64 NW i): key (.. >> 5), dims 4 (.. & 31)
+    float v[64 / NW];    // V: dim pf_vdim<NW>(wave, lane, j), keys 4 pf_vgrp(lane) + e
 };
 
 __device__ __forceinline__ int pf_vgrp(int lane) { return (lane >> 2) & 7; }
-__device__ __forceinline__ int pf_vdim(int wave, int lane, int j) { return 8 * (wave + 4 * j) + (lane & 3) + 4 * (lane >> 5); }
+template <int NW>
+__device__ __forceinline__ int pf_vdim(int wave, int lane, int j) {
+    return 8 * (wave + NW * j) + (lane & 3) + 4 * (lane >> 5);
+}
 
-__device__ __forceinline__ void pf_load(PfStage &st, const float *kb, const float *vb, long ps, int k0, int kend,
+template <int NW>
+__device__ __forceinline__ void pf_load(PfStage<NW> &st, const float *kb, const float *vb, long ps, int k0, int kend,
                                         int tid) {
+    constexpr int NI = 16 / NW;
     if (k0 + PF_KT <= kend) {                       // a whole tile (block-uniform): no bounds tests
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int idx = tid + 256 * i;
+        for (int i = 0; i < NI; i++) {
+            const int idx = tid + 64 * NW * i;
             st.k[i] = *reinterpret_cast<const float4 *>(kb + (size_t)(k0 + (idx >> 5)) * ps + (idx & 31) * 4);
         }
         const int wave = tid >> 6, lane = tid & 63;
         const float *vr = vb + (size_t)(k0 + 4 * pf_vgrp(lane)) * ps;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int d = pf_vdim(wave, lane, j);
+        for (int j = 0; j < NI; j++) {
+            const int d = pf_vdim<NW>(wave, lane, j);
 #pragma unroll
             for (int e = 0; e < 4; e++) st.v[4 * j + e] = vr[(size_t)e * ps + d];
         }
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int idx = tid + 256 * i, key = k0 + (idx >> 5);
+    for (int i = 0; i < NI; i++) {
+        const int idx = tid + 64 * NW * i, key = k0 + (idx >> 5);
         st.k[i] = key < kend ? *reinterpret_cast<const float4 *>(kb + (size_t)key * ps + (idx & 31) * 4)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const int wave = tid >> 6, lane = tid & 63, g = pf_vgrp(lane);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int d = pf_vdim(wave, lane, j);
+    for (int j = 0; j < NI; j++) {
+        const int d = pf_vdim<NW>(wave, lane, j);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int key = k0 + 4 * g + e;
@@ -129,11 +137,13 @@ __device__ __forceinline__ void pf_load(PfStage &st, const float *kb, const floa
 
 __device__ __forceinline__ int pf_kslot(int key, int c) { return key * 32 + 8 * (c ^ ((key >> 1) & 3)); }
 
-__device__ __forceinline__ void pf_store(const PfStage &st, __bf16 (*sKh)[PF_KSL], __bf16 (*sKl)[PF_KSL],
+template <int NW>
+__device__ __forceinline__ void pf_store(const PfStage<NW> &st, __bf16 (*sKh)[PF_KSL], __bf16 (*sKl)[PF_KSL],
                                          __bf16 (*sVh)[PF_VLDB], __bf16 (*sVl)[PF_VLDB], int tid) {
+    constexpr int NI = 16 / NW;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int idx = tid + 256 * i;
+    for (int i = 0; i < NI; i++) {
+        const int idx = tid + 64 * NW * i;
         pf_bf16x4 h, l;
         pf_split4(st.k[i], h, l);
         // dims 4 (idx & 31) .. + 3 of key idx >> 5: slice (idx & 31) / 8, chunk (idx & 7) / 2, half idx & 1
@@ -145,8 +155,8 @@ __device__ __forceinline__ void pf_store(const PfStage &st, __bf16 (*sKh)[PF_KSL
     // of the MFMA's k slots, see the header)
     const int wave = tid >> 6, lane = tid & 63, g = pf_vgrp(lane);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int d = pf_vdim(wave, lane, j);
+    for (int j = 0; j < NI; j++) {
+        const int d = pf_vdim<NW>(wave, lane, j);
         const int o = 8 * ((g & 3) ^ ((d >> 1) & 3)) + 4 * (g >> 2);
         pf_bf16x4 h, l;
         pf_split4(make_float4(st.v[4 * j], st.v[4 * j + 1], st.v[4 * j + 2], st.v[4 * j + 3]), h, l);
@@ -175,7 +185,12 @@ __device__ __forceinline__ void pf_write_out(const qk_attn_args &a, size_t base,
     }
 }
 
-__global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
+// NW waves: 16 NW queries per block (64 with 4 waves, two blocks per CU; 128
+// with 8 waves, one block per CU, for long unsplit prefills: each staged K/V
+// tile, split once, then serves twice the queries)
+template <int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_prefill(qk_attn_args a) {
+    constexpr int QT = 16 * NW;                           // queries per block
     constexpr int hd = QWEN_HIP_HEAD_DIM;
     __shared__ __attribute__((aligned(16))) __bf16 sKh[4][PF_KSL];
     __shared__ __attribute__((aligned(16))) __bf16 sKl[4][PF_KSL];
@@ -183,13 +198,13 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
     __shared__ __attribute__((aligned(16))) __bf16 sVl[hd][PF_VLDB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, kq = lane >> 4;
-    const int nq = (a.seq_q + PF_Q - 1) / PF_Q;
+    const int nq = (a.seq_q + QT - 1) / QT;
     // blocks go out in x order: query tiles longest first, all kv heads of a
     // tile next to each other, so the causal triangle's long tiles start first
     const int t = nq - 1 - (int)blockIdx.x / a.kv_heads;
     const int g = (int)blockIdx.x % a.kv_heads, split = blockIdx.z;
-    const int q0 = t * PF_Q;
-    const int qn = min(PF_Q, a.seq_q - q0);
+    const int q0 = t * QT;
+    const int qn = min(QT, a.seq_q - q0);
     const int kend_tile = min(a.seq_k, a.q_offset + q0 + qn);
     const int ks0 = split * a.chunk;
     if (ks0 >= kend_tile) return;                         // block-uniform
@@ -224,13 +239,13 @@ __global__ __launch_bounds__(256, 2) void attn_prefill(qk_attn_args a) {
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
     float m[2] = {PF_MINIT, PF_MINIT}, l[2] = {0.f, 0.f};
 
-    PfStage st;
-    pf_load(st, kb, vb, a.pos_stride, ks0, ks1, tid);
+    PfStage<NW> st;
+    pf_load<NW>(st, kb, vb, a.pos_stride, ks0, ks1, tid);
     for (int k0 = ks0; k0 < ks1; k0 += PF_KT) {
         __syncthreads();                                  // previous tile fully consumed
-        pf_store(st, sKh, sKl, sVh, sVl, tid);
+        pf_store<NW>(st, sKh, sKl, sVh, sVl, tid);
         __syncthreads();
-        if (k0 + PF_KT < ks1) pf_load(st, kb, vb, a.pos_stride, k0 + PF_KT, ks1, tid);
+        if (k0 + PF_KT < ks1) pf_load<NW>(st, kb, vb, a.pos_stride, k0 + PF_KT, ks1, tid);
         if (!wave_on) continue;
 
         // scores: s[qt][kt][r] = q(query qs + 16 qt + ql) . k(key k0 + 16 kt + 4 kq + r)
@@ -508,7 +523,12 @@ extern "C" int qk_attn_prefill_launch(const qk_attn_args *a, hipStream_t s) {
     // every key the last query tile sees must fall in some split
     const int kmax = a->seq_k < a->q_offset + a->seq_q ? a->seq_k : a->q_offset + a->seq_q;
     if ((long)a->chunk * a->nsplit < kmax) return QWEN_HIP_EINVAL;
-    attn_prefill<<<dim3(nq * a->kv_heads, 1, a->nsplit), 256, 0, s>>>(*a);
+    // unsplit prefills with 128-query tiles enough for every CU: 8-wave blocks
+    const int nq8 = (a->seq_q + 127) / 128;
+    if (a->nsplit == 1 && (long)nq8 * a->kv_heads >= 256)
+        attn_prefill<8><<<dim3(nq8 * a->kv_heads, 1, 1), 512, 0, s>>>(*a);
+    else
+        attn_prefill<4><<<dim3(nq * a->kv_heads, 1, a->nsplit), 256, 0, s>>>(*a);
     if (a->nsplit > 1)
         attn_prefill_merge<<<(unsigned)(((long)a->seq_q * a->heads + 7) / 8), 256, 0, s>>>(*a);
     return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
