@@ -52,7 +52,10 @@ WORKLOADS = {
 }
 C5_CHUNKS, C5_AUDIO, C5_ROLLBACK, C5_STEPS, C5_CAP, C5_HEAD, C5_KEEP = 60, 26, 5, 24, 1024, 9, 3
 HBM_PEAK_GBS = 8000.0
-CPU_MAX_PREFILL, CPU_SAMPLE_ROWS = 1536, 1024   # CPU baseline: longer prefills are sampled
+# CPU baseline: prefills longer than the first figure are sampled to the
+# second (the reference's non-BLAS prefill runs ~60 rows/s on 0.6B and ~8.5
+# rows/s on 1.7B with 16 threads, so a sample stays within ~30 s)
+CPU_PREFILL_BOUND = {False: (1536, 1024), True: (256, 256)}   # keyed by "1.7B model"
 PREFILL_REPS = 5
 
 
@@ -405,12 +408,14 @@ def cpu_baseline(wl, rows, first_token, threads, decode_steps):
     t0 = time.time()
     m = P.SynthModel(cfg, seed=0)
     r = P.RefModel(m, threads=threads)
-    # a long prefill (C4: 8191 rows) would take the reference's non-BLAS loop
-    # many minutes: the sample then prefills the first CPU_SAMPLE_ROWS rows
+    # a long prefill (C4: 8191 rows of 0.6B, C3: 1515 rows of 1.7B) would take
+    # the reference's non-BLAS loop minutes: the sample then prefills the
+    # first rows only (CPU_PREFILL_BOUND)
     n = rows.shape[0] - 1
-    sampled = n > CPU_MAX_PREFILL
-    pre = rows[:CPU_SAMPLE_ROWS] if sampled else rows[:-1]
-    last = rows[CPU_SAMPLE_ROWS] if sampled else rows[-1]
+    max_rows, sample_rows = CPU_PREFILL_BOUND[bool(wl["model_b"])]
+    sampled = n > max_rows
+    pre = rows[:sample_rows] if sampled else rows[:-1]
+    last = rows[sample_rows] if sampled else rows[-1]
     log(f"[cpu] weights generated in {time.time() - t0:.1f}s; prefill {pre.shape[0]} rows on {threads} threads")
     tp = r.time_prefill(pre)
     tok, _, _ = r.forward(last)
