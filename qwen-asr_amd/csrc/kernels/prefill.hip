@@ -90,6 +90,11 @@ __global__ __launch_bounds__(256) void rmsnorm_split_rows(float *x, const float 
     const int row = 4 * blockIdx.x + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= S) return;                                   // whole wave
     float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * D) + lane;
+    // the weights first: their loads pass under the row's
+    float4 wv[Q];
+    const float4 *w4 = w ? reinterpret_cast<const float4 *>(w) + lane : nullptr;
+#pragma unroll
+    for (int j = 0; j < Q; j++) wv[j] = w ? w4[64 * j] : make_float4(1.f, 1.f, 1.f, 1.f);
     float4 v[Q];
 #pragma unroll
     for (int j = 0; j < Q; j++) v[j] = xr[64 * j];
@@ -135,10 +140,9 @@ __global__ __launch_bounds__(256) void rmsnorm_split_rows(float *x, const float 
     if (!hi) return;
     uint2 *h = reinterpret_cast<uint2 *>(hi + (size_t)row * D) + lane;
     uint2 *l = reinterpret_cast<uint2 *>(lo + (size_t)row * D) + lane;
-    const float4 *w4 = w ? reinterpret_cast<const float4 *>(w) + lane : nullptr;
 #pragma unroll
     for (int j = 0; j < Q; j++) {
-        const float4 ww = w ? w4[64 * j] : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 ww = wv[j];
         const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w}, we[4] = {ww.x, ww.y, ww.z, ww.w};
         uint16_t hh[4], ll[4];
 #pragma unroll
@@ -199,6 +203,11 @@ __global__ __launch_bounds__(256) void rmsnorm_split_vec(float *x, const float *
     constexpr int D = 1024 * V4;
     __shared__ float red[4];
     float4 *xr = reinterpret_cast<float4 *>(x + (size_t)blockIdx.x * D) + threadIdx.x;
+    // the weights first: their loads pass under the row's
+    float4 wv[V4];
+    const float4 *w4 = w ? reinterpret_cast<const float4 *>(w) + threadIdx.x : nullptr;
+#pragma unroll
+    for (int e = 0; e < V4; e++) wv[e] = w ? w4[256 * e] : make_float4(1.f, 1.f, 1.f, 1.f);
     float4 v[V4];
 #pragma unroll
     for (int e = 0; e < V4; e++) v[e] = xr[256 * e];
@@ -235,10 +244,9 @@ __global__ __launch_bounds__(256) void rmsnorm_split_vec(float *x, const float *
     if (!hi) return;
     uint2 *h = reinterpret_cast<uint2 *>(hi + (size_t)blockIdx.x * D) + threadIdx.x;
     uint2 *l = reinterpret_cast<uint2 *>(lo + (size_t)blockIdx.x * D) + threadIdx.x;
-    const float4 *w4 = w ? reinterpret_cast<const float4 *>(w) + threadIdx.x : nullptr;
 #pragma unroll
     for (int e = 0; e < V4; e++) {
-        const float4 ww = w ? w4[256 * e] : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 ww = wv[e];
         const float el[4] = {v[e].x, v[e].y, v[e].z, v[e].w}, we[4] = {ww.x, ww.y, ww.z, ww.w};
         uint16_t hh[4], ll[4];
 #pragma unroll
