@@ -347,8 +347,9 @@ def test_causal_attention_long_walk(P, qa, gpu, sq):
     """Long prefills.  3000 query rows (47 query tiles x 8 kv heads, fewer than
     two blocks per CU): the plan caps a block's walk at a sixth of the longest
     query tile, so blocks walk 512 keys and the merge combines six splits.
-    6400 rows (800 blocks): no split, the last query tiles walk all 6400 keys
-    in one block (the path the 8k-row prefill takes).  Checked against a
+    6400 rows (800 blocks of 64 queries): no split, so the kernel runs 8-wave
+    blocks of 128 queries (400 of them) and the last query tiles walk all
+    6400 keys in one block (the path the 8k-row prefill takes).  Checked against a
     float64 causal softmax attention computed with torch on the same device
     (the CPU oracle is too slow at this size)."""
     sk = sq
