@@ -342,24 +342,26 @@ def test_causal_attention(P, qa, gpu, sq, sk, q_off):
     np.testing.assert_allclose(host(dout), exp, atol=3e-5, rtol=1e-4)
 
 
-@pytest.mark.parametrize("sq", [3000, 6400])
-def test_causal_attention_long_walk(P, qa, gpu, sq):
+@pytest.mark.parametrize("sq,sk", [(3000, 3000), (6400, 6400), (4096, 5000)])
+def test_causal_attention_long_walk(P, qa, gpu, sq, sk):
     """Long prefills.  3000 query rows (47 query tiles x 8 kv heads, fewer than
     two blocks per CU): the plan caps a block's walk at a sixth of the longest
     query tile, so blocks walk 512 keys and the merge combines six splits.
     6400 rows (800 blocks of 64 queries): no split, so the kernel runs 8-wave
     blocks of 128 queries (400 of them) and the last query tiles walk all
-    6400 keys in one block (the path the 8k-row prefill takes).  Checked against a
-    float64 causal softmax attention computed with torch on the same device
-    (the CPU oracle is too slow at this size)."""
-    sk = sq
+    6400 keys in one block (the path the 8k-row prefill takes).  4096 rows
+    after 904 cached keys (query i sees keys j <= 904 + i): the 8-wave blocks
+    with a query offset, as a long continuation prefill runs them.  Checked
+    against a float64 causal softmax attention computed with torch on the
+    same device (the CPU oracle is too slow at this size)."""
+    q_off = sk - sq
     nh, nkv, hd = 16, 8, 128
     chunk, nsplit = C.c_int(), C.c_int()
-    qa.lib().qk_attn_prefill_plan(sq, sk, 0, nh, nkv, C.byref(chunk), C.byref(nsplit))
+    qa.lib().qk_attn_prefill_plan(sq, sk, q_off, nh, nkv, C.byref(chunk), C.byref(nsplit))
     if sq == 3000:
         assert chunk.value == 512 and nsplit.value == 6, (chunk.value, nsplit.value)
     else:
-        assert chunk.value == sq and nsplit.value == 1, (chunk.value, nsplit.value)
+        assert chunk.value >= sk and nsplit.value == 1, (chunk.value, nsplit.value)
     g = gpu.Generator(device="cuda").manual_seed(11)
     Q = gpu.randn((sq, nh * hd), generator=g, device="cuda", dtype=gpu.float32)
     K = gpu.randn((sk, nkv * hd), generator=g, device="cuda", dtype=gpu.float32)
@@ -367,9 +369,9 @@ def test_causal_attention_long_walk(P, qa, gpu, sq):
     scale = 1.0 / np.sqrt(128.0)
     out = gpu.empty((sq, nh * hd), dtype=gpu.float32, device="cuda")
     qa.check(qa.lib().qwen_hip_causal_attention(ptr(out), ptr(Q), ptr(K), ptr(V), sq, sk, nh, nkv, hd,
-                                                scale, 0, None), "attention")
+                                                scale, q_off, None), "attention")
     gpu.cuda.synchronize()
-    mask = gpu.triu(gpu.ones((sq, sk), dtype=gpu.bool, device="cuda"), diagonal=1)
+    mask = gpu.triu(gpu.ones((sq, sk), dtype=gpu.bool, device="cuda"), diagonal=1 + q_off)
     worst = 0.0
     for h in range(0, nh, 3):
         q = Q[:, h * hd:(h + 1) * hd].double()
