@@ -69,6 +69,8 @@ typedef struct {
     float *q_out;             /* [S][q_dim] normed + rotated queries */
 } qk_rope_append_args;
 
+/* Every pointer 16-byte aligned and pstride a multiple of 4 when nsum > 1
+ * (the kernel's accesses are 16-byte vectors); QWEN_HIP_EINVAL otherwise. */
 int qk_rope_append_launch(const qk_rope_append_args *a, hipStream_t s);
 
 /* ---- causal GQA attention -------------------------------------------- */
@@ -250,8 +252,9 @@ int qk_gemm_reduce_launch(const float *part, int nsum, int M, int N, int epi, fl
                           uint16_t *out_lo, hipStream_t s);
 /* Q|K|V product (A hi/lo [M][K] . W[(heads + 2 kv_heads) 128][K]^T) with
  * rope_append's work as its epilogue (qkv / nsum unused, pos_dev NULL, S ==
- * M): bit for bit qk_gemm_launch(STORE) + qk_rope_append_launch.  Only for
- * plans with qk_gemm_rope_fusable (64 x 128 ring tiles, one split). */
+ * M, the other pointers 16-byte aligned): bit for bit qk_gemm_launch(STORE)
+ * + qk_rope_append_launch.  Only for plans with qk_gemm_rope_fusable (64 x
+ * 128 ring tiles, one split). */
 int qk_gemm_rope_fusable(const qk_gemm_plan *p);
 int qk_gemm_rope_launch(const uint16_t *a_hi, const uint16_t *a_lo, const uint16_t *W, int M, int K,
                         const qk_gemm_plan *p, const qk_rope_append_args *ra, hipStream_t s);
