@@ -111,3 +111,37 @@ def test_attention_plan_invariants(qa, seq_q, seq_k, q_offset):
         assert nsplit.value == 1
     # partial buffer: (o[128], m, l) per split, query and head, only when split
     assert part == (nsplit.value * seq_q * 16 * 130 if nsplit.value > 1 else 0)
+
+
+class RopeArgs(C.Structure):
+    _fields_ = [("qkv", C.c_void_p), ("nsum", C.c_int), ("pstride", C.c_long), ("q_norm", C.c_void_p),
+                ("k_norm", C.c_void_p), ("eps", C.c_float), ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+                ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("cap", C.c_int), ("pos_dev", C.c_void_p),
+                ("start", C.c_int), ("S", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int), ("q_out", C.c_void_p)]
+
+
+@pytest.mark.parametrize("field", ["qkv", "q_norm", "rope_cos", "k_cache", "q_out"])
+def test_rope_launches_refuse_unaligned_pointers(qa, field):
+    """The q/k norm + RoPE kernels move 16-byte vectors: a pointer off a
+    16-byte boundary, or split partials a non-multiple of 4 floats apart, is
+    refused with QWEN_HIP_EINVAL before anything is launched (host-side
+    checks; the addresses are never dereferenced)."""
+    lib = qa.lib()
+    lib.qk_rope_append_launch.argtypes = [C.c_void_p, C.c_void_p]
+    lib.qk_gemm_rope_launch.argtypes = [C.c_void_p] * 3 + [C.c_int] * 2 + [C.c_void_p] * 3
+    base = 1 << 20
+    good = {f: base + (i << 16) for i, f in enumerate(["qkv", "q_norm", "k_norm", "rope_cos", "rope_sin", "k_cache",
+                                                       "v_cache", "q_out"])}
+
+    def args(**over):
+        v = dict(good, **over)
+        return RopeArgs(v["qkv"], 1, 0, v["q_norm"], v["k_norm"], 1e-6, v["rope_cos"], v["rope_sin"], v["k_cache"],
+                        v["v_cache"], 64, None, 0, 64, 16, 8, v["q_out"])
+    bad = args(**{field: good[field] + 4})
+    assert lib.qk_rope_append_launch(C.byref(bad), None) == -1
+    split = args()
+    split.nsum, split.pstride = 2, 64 * 4096 + 2
+    assert lib.qk_rope_append_launch(C.byref(split), None) == -1
+    if field != "qkv":               # the fused kernel reads the product from its own tiles
+        p = GemmPlan(64, 1, 1024, 128, 4)
+        assert lib.qk_gemm_rope_launch(base, base, base, 64, 1024, C.byref(p), C.byref(bad), None) == -1
