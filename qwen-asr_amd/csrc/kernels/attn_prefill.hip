@@ -505,6 +505,10 @@ extern "C" size_t qk_attn_prefill_plan(int seq_q, int seq_k, int q_offset, int h
         long q4 = (kmax / 4 + PF_KT / 2) / PF_KT * PF_KT;
         if (c < q4) c = q4;
     }
+    // one query tile (a short continuation prefill over a long cache): 64-key
+    // splits at least, half the partials of 32-key ones for the merge (C5's
+    // 31 rows after ~1000 keys: 17.3 -> 15.7 us with the merge)
+    if (nq == 1 && c < 2 * PF_KT) c = 2 * PF_KT;
     // with two (query tile, kv head) blocks per CU or more, the longest-first
     // order alone balances the CUs: no split, so no partials and no merge pass
     if ((long)nq * kv_heads >= 2L * 256) c = (kmax + PF_KT - 1) / PF_KT * PF_KT;

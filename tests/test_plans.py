@@ -6,8 +6,9 @@ invariants are what the kernels rely on: slices cover K exactly once in whole
 chunks are whole 32-key tiles, cover the longest query tile, and no block
 walks more than max(256, a sixth of it) keys, except that with four or more
 query tiles and up to 2048 keys a split covers a quarter of the longest range
-at least, and a prefill with at least two (64-query tile, kv head) blocks per
-CU is not split at all."""
+at least, a single query tile (a short continuation prefill) splits its keys
+64 at a time at least, and a prefill with at least two (64-query tile, kv
+head) blocks per CU is not split at all."""
 import ctypes as C
 
 import pytest
@@ -109,6 +110,8 @@ def test_attention_plan_invariants(qa, seq_q, seq_k, q_offset):
         assert chunk.value >= min(q4, -(-kmax // 32) * 32)
     if nq * 8 >= 512:
         assert nsplit.value == 1
+    if nq == 1:                                       # one query tile: 64-key splits at least
+        assert chunk.value >= min(64, -(-kmax // 32) * 32)
     # partial buffer: (o[128], m, l) per split, query and head, only when split
     assert part == (nsplit.value * seq_q * 16 * 130 if nsplit.value > 1 else 0)
 
