@@ -193,6 +193,37 @@ int qwen_hip_decoder_set_wait_limit(qwen_hip_decoder *dec, double seconds);
 int qwen_hip_decoder_set_trace(qwen_hip_decoder *dec, int step);
 int qwen_hip_decoder_read_trace(qwen_hip_decoder *dec, uint64_t *out, size_t n);
 
+/* The persistent engine has two kernels.  The split kernel (any supported
+ * shape) has every CU stream its share of every layer.  The relay kernel (the
+ * 0.6B shape; default where available) splits each XCD's CUs into two teams
+ * that take the layers in turn: one team computes a layer from weights it
+ * holds in registers while the other streams the next layer's weights, so a
+ * computing CU's hand-overs never wait behind its own weight loads.  It keeps
+ * each attention split's cached K/V rows in LDS, which bounds it to launches
+ * whose positions stay below QWEN_HIP_RELAY_MAX_POS; longer contexts run on
+ * the split kernel.  Both compute the same arithmetic (bf16 weights, fp32
+ * activations and sums; the relay kernel's products run on the matrix cores
+ * with each fp32 activation split exactly into three bf16 terms), so tokens
+ * agree with the reference either way.  set_relay(0) forces the split kernel.
+ * last_kernel: the kernel of the last persistent launch (its trace layout):
+ * QWEN_HIP_KERNEL_SPLIT or QWEN_HIP_KERNEL_RELAY, 0 before any.
+ *
+ * Relay trace layout (read_trace returns 512 words per block): for layer l
+ * of the block's team (team 0 even layers, team 1 odd), words 16*l + {0 input
+ * wait entered, 1 cross-XCD half of the input residual in, 2 input residual
+ * gathered, 3 Q stored, 4 q|k|v gathered, 5 split partials stored, 6 merge
+ * slices in, 7 merged attention gathered, 8 O stored, 9 cross-XCD half of the
+ * post-attention residual in, 10 post-attention residual gathered, 11 SwiGLU
+ * stored, 12 SwiGLU outputs gathered, 13 down stored, 14 next layer's loads
+ * issued}; then 16*layers + {0 LM entered, 1 final residual cross half in,
+ * 2 gathered, 3 candidate stored, 4 token ready (team 0 only)}.  No
+ * reference counterpart (the reference decodes on the CPU). */
+#define QWEN_HIP_KERNEL_SPLIT 1
+#define QWEN_HIP_KERNEL_RELAY 2
+#define QWEN_HIP_RELAY_MAX_POS 1024
+int qwen_hip_decoder_set_relay(qwen_hip_decoder *dec, int on);
+int qwen_hip_decoder_last_kernel(const qwen_hip_decoder *dec);
+
 /* The stream the decoder launches on (for event timing by callers). */
 hipStream_t qwen_hip_decoder_stream(const qwen_hip_decoder *dec);
 

@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(HERE, "libqwen_asr_hip.so")
 QWEN_HIP_TOKEN_ENDOFTEXT = 151643
 QWEN_HIP_TOKEN_IM_END = 151645
 ERRORS = {0: "OK", -1: "EINVAL", -2: "ENOMEM", -3: "EDEVICE", -4: "ESTATE"}
+KERNEL_SPLIT, KERNEL_RELAY, RELAY_MAX_POS = 1, 2, 1024   # QWEN_HIP_KERNEL_*, QWEN_HIP_RELAY_MAX_POS
 
 
 class HipConfig(C.Structure):
@@ -69,6 +70,8 @@ SIGNATURES = [
     ("qwen_hip_decoder_set_wait_limit", _i, [_vp, _d]),
     ("qwen_hip_decoder_set_trace", _i, [_vp, _i]),
     ("qwen_hip_decoder_read_trace", _i, [_vp, _vp, C.c_size_t]),
+    ("qwen_hip_decoder_set_relay", _i, [_vp, _i]),
+    ("qwen_hip_decoder_last_kernel", _i, [_vp]),
     ("qwen_hip_decoder_stream", _vp, [_vp]),
     ("qwen_hip_decoder_step_bytes", _d, [_vp, _i]),
     ("qwen_hip_last_error", C.c_char_p, []),
@@ -489,10 +492,20 @@ class Decoder:
         check(lib().qwen_hip_decoder_set_trace(self.h, int(step)), "set_trace")
 
     def read_trace(self):
-        """[256 blocks][704] wall-clock stamps (100 MHz) of the traced step."""
+        """Wall-clock stamps (100 MHz) of the traced step: [256 blocks][704] for the
+        split kernel, [256 blocks][512] for the relay kernel (see last_kernel)."""
         out = np.zeros((256, 704), np.uint64)
-        check(lib().qwen_hip_decoder_read_trace(self.h, _ptr(out), out.size), "read_trace")
-        return out
+        words = check(lib().qwen_hip_decoder_read_trace(self.h, _ptr(out), out.size), "read_trace")
+        return out.reshape(-1)[:256 * words].reshape(256, words).copy()
+
+    def set_relay(self, on):
+        """on (default where available): persistent launches whose positions stay
+        below RELAY_MAX_POS run the relay kernel; off: always the split kernel."""
+        check(lib().qwen_hip_decoder_set_relay(self.h, 1 if on else 0), "set_relay")
+
+    def last_kernel(self):
+        """Kernel of the last persistent launch: KERNEL_SPLIT (1), KERNEL_RELAY (2), 0 before any."""
+        return check(lib().qwen_hip_decoder_last_kernel(self.h), "last_kernel")
 
     def read_hidden(self):
         out = np.empty(self.cfg.hidden, np.float32)

@@ -123,6 +123,14 @@ struct qwen_hip_decoder {
     double px_ticks_per_s;
     int px_fallback;                /* 1: a failed persistent launch is redone by the graph engine */
     int px_fallbacks;               /* number of such fallbacks */
+
+    /* relay kernel (0.6B shape): tiled weights and its own exchange words */
+    int rl_ok, rl_on;
+    char *wt;                       /* QK_RL_LAYER_BYTES per layer */
+    unsigned long long *rl_buf;
+    size_t rl_words;
+    unsigned long long *rq, *ra, *rm, *ro, *rla, *rh, *rd, *rs, *rlb, *rc, *rv;
+    int last_kernel;                /* QWEN_HIP_KERNEL_* of the last persistent launch */
 };
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -285,6 +293,32 @@ static int px_alloc(qwen_hip_decoder *d) {
     return 0;
 }
 
+/* The relay kernel's tiled weights and exchange words (zero-initialised). */
+static int rl_alloc(qwen_hip_decoder *d) {
+    const size_t T = 2 * QK_PX_XCD, H = d->cfg.hidden;
+    const size_t n_q = T * 512, n_a = T * QK_RL_TEAM * QK_RL_PART, n_m = T * 256, n_h = T * H;
+    const size_t n_i = T * (d->cfg.intermediate / QK_PX_XCD), n_c = (size_t)QK_PX_BLOCKS * QK_RL_LINE;
+    d->rl_words = n_q + n_a + n_m + 5 * n_h + n_i + 2 * n_c;
+    QK_TRY(dev_alloc((void **)&d->wt, (size_t)d->cfg.layers * QK_RL_LAYER_BYTES));
+    QK_TRY(dev_alloc((void **)&d->rl_buf, d->rl_words * 8));
+    unsigned long long *p = d->rl_buf;
+    d->rq = p;  p += n_q;
+    d->ra = p;  p += n_a;
+    d->rm = p;  p += n_m;
+    d->ro = p;  p += n_h;
+    d->rla = p; p += n_h;
+    d->rd = p;  p += n_h;
+    d->rs = p;  p += n_h;
+    d->rlb = p; p += n_h;
+    d->rh = p;  p += n_i;
+    d->rc = p;  p += n_c;
+    d->rv = p;
+    QK_HIP(hipMemset(d->rl_buf, 0, d->rl_words * 8));
+    d->rl_ok = 1;
+    d->rl_on = 1;
+    return 0;
+}
+
 qwen_hip_decoder *qwen_hip_decoder_create(const qwen_hip_config *cfg, int device, int kv_capacity) {
     if (!check_cfg(cfg)) {
         qk_set_err("unsupported decoder configuration (head_dim must be 128; hidden, "
@@ -364,6 +398,8 @@ qwen_hip_decoder *qwen_hip_decoder_create(const qwen_hip_config *cfg, int device
         if (px_alloc(d)) goto fail;
         d->px_ok = 1;
         d->engine = ENGINE_PERSIST;
+        if (qk_relay_supported(cfg->hidden, cfg->intermediate, cfg->heads, cfg->kv_heads, device) && rl_alloc(d))
+            goto fail;
     }
     return d;
 fail:
@@ -397,6 +433,7 @@ void qwen_hip_decoder_destroy(qwen_hip_decoder *d) {
     dev_free(d->attn_out); dev_free(d->h); dev_free(d->hidden); dev_free(d->logits);
     dev_free(d->cand_val); dev_free(d->cand_idx); dev_free(d->ctl); dev_free(d->d_log);
     dev_free(d->px_buf); dev_free(d->px_ctl); dev_free(d->px_trace);
+    dev_free(d->wt); dev_free(d->rl_buf);
     prefill_free(d);
     if (d->h_row) (void)hipHostFree(d->h_row);
     if (d->h_int) (void)hipHostFree(d->h_int);
@@ -429,6 +466,11 @@ int qwen_hip_decoder_load_layer(qwen_hip_decoder *d, int l, const qwen_hip_layer
     QK_HIP(hipMemcpy(d->n_post[l], w->post_attn_norm, D * 4, hipMemcpyHostToDevice));
     QK_HIP(hipMemcpy(d->n_q[l], w->q_norm, hd * 4, hipMemcpyHostToDevice));
     QK_HIP(hipMemcpy(d->n_k[l], w->k_norm, hd * 4, hipMemcpyHostToDevice));
+    if (d->rl_ok) {   /* the relay kernel's tiled copy of the four matrices */
+        QK_TRY(qk_relay_pack(d->wt + (size_t)l * QK_RL_LAYER_BYTES, d->w_qkv[l], d->w_o[l], d->w_gu[l], d->w_down[l],
+                             d->stream));
+        QK_HIP(hipStreamSynchronize(d->stream));
+    }
     d->loaded[l] = 1;
     return 0;
 }
@@ -727,17 +769,28 @@ static int log_reserve(qwen_hip_decoder *d, int n) {
     return 0;
 }
 
-/* The persistent engine: n steps from position kv_len in one persistent
- * launch; the first input is emb[first_tok] or, for first_tok < 0, the row
- * staged in d->x.  Synchronises and checks the kernel's error bits. */
-static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
+/* the relay kernel (rl_decode): two teams of CUs take the layers in turn */
+static int rl_launch(qwen_hip_decoder *d, int first_tok, int n) {
     const qwen_hip_config *c = &d->cfg;
-    const unsigned need = QK_PX_TAGS(c->layers, n);
-    if (d->px_epoch > 0xFFFFFF00u - need) {       /* tag space exhausted: start over on zeroed words */
-        QK_HIP(hipMemsetAsync(d->px_buf, 0, d->px_words * 8, d->stream));
-        d->px_epoch = 1;
-    }
-    QK_HIP(hipMemsetAsync(d->px_ctl, 0, 64 * sizeof(unsigned), d->stream));
+    const char *l0 = (const char *)d->n_in[0];
+    qk_relay_args a = {
+        .wt = d->wt, .layer0 = l0,
+        .layer_stride = c->layers > 1 ? (long)((const char *)d->n_in[1] - l0) : 0,
+        .off_nin = 0, .off_npost = (const char *)d->n_post[0] - l0, .off_nq = (const char *)d->n_q[0] - l0,
+        .off_nk = (const char *)d->n_k[0] - l0, .emb = d->emb, .fnorm = d->fnorm, .k_cache = d->kc, .v_cache = d->vc,
+        .cap = d->kv_cap, .rope_cos = d->rope_cos, .rope_sin = d->rope_sin, .layers = c->layers, .vocab = c->vocab,
+        .eps = c->rms_eps, .scale = d->scale, .xq = d->rq, .xa = d->ra, .xm = d->rm, .xo = d->ro, .xla = d->rla,
+        .xh = d->rh, .xd = d->rd, .xs = d->rs, .xlb = d->rlb, .xc = d->rc, .xv = d->rv, .cnt = d->px_ctl,
+        .err = d->px_ctl + 16, .epoch = d->px_epoch, .wait_ticks = d->px_wait_ticks, .pos0 = d->kv_len, .n_steps = n,
+        .first_tok = first_tok, .x_in = d->x, .log = d->d_log, .tok_out = d->d_tok, .pos_out = d->d_pos,
+        .hidden_out = d->hidden, .logits = d->keep_logits ? d->logits : NULL,
+        .trace = d->px_trace_step >= 0 && d->px_trace_step < n ? d->px_trace : NULL, .trace_step = d->px_trace_step};
+    return qk_relay_launch(&a, d->stream);
+}
+
+/* the split kernel (px_decode): every CU streams every layer's share */
+static int sp_launch(qwen_hip_decoder *d, int first_tok, int n) {
+    const qwen_hip_config *c = &d->cfg;
     const char *l0 = (const char *)d->w_qkv[0];
     qk_persist_args a = {
         .layer0 = l0, .layer_stride = c->layers > 1 ? (long)((const char *)d->w_qkv[1] - l0) : 0,
@@ -754,7 +807,26 @@ static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
         .tok_out = d->d_tok, .pos_out = d->d_pos, .hidden_out = d->hidden,
         .logits = d->keep_logits ? d->logits : NULL,
         .trace = d->px_trace_step >= 0 && d->px_trace_step < n ? d->px_trace : NULL, .trace_step = d->px_trace_step};
-    QK_TRY(qk_persist_launch(&a, c->hidden, c->intermediate, d->stream));
+    return qk_persist_launch(&a, c->hidden, c->intermediate, d->stream);
+}
+
+/* The persistent engine: n steps from position kv_len in one persistent
+ * launch of the relay kernel (where it is available, enabled and every
+ * position stays below QK_RL_MAX_SEQ) or else the split kernel; the first
+ * input is emb[first_tok] or, for first_tok < 0, the row staged in d->x.
+ * Synchronises and checks the kernel's error bits. */
+static int px_run(qwen_hip_decoder *d, int first_tok, int n) {
+    const qwen_hip_config *c = &d->cfg;
+    const int relay = d->rl_ok && d->rl_on && d->kv_len + n <= QK_RL_MAX_SEQ;
+    const unsigned need = relay ? QK_RL_TAGS(c->layers, n) : QK_PX_TAGS(c->layers, n);
+    if (d->px_epoch > 0xFFFFFF00u - need) {       /* tag space exhausted: start over on zeroed words */
+        QK_HIP(hipMemsetAsync(d->px_buf, 0, d->px_words * 8, d->stream));
+        if (d->rl_buf) QK_HIP(hipMemsetAsync(d->rl_buf, 0, d->rl_words * 8, d->stream));
+        d->px_epoch = 1;
+    }
+    QK_HIP(hipMemsetAsync(d->px_ctl, 0, 64 * sizeof(unsigned), d->stream));
+    QK_TRY(relay ? rl_launch(d, first_tok, n) : sp_launch(d, first_tok, n));
+    d->last_kernel = relay ? QWEN_HIP_KERNEL_RELAY : QWEN_HIP_KERNEL_SPLIT;
     d->px_epoch += need;
     QK_HIP(hipMemcpyAsync(&d->h_int[16], d->px_ctl + 16, sizeof(int), hipMemcpyDeviceToHost, d->stream));
     QK_HIP(hipStreamSynchronize(d->stream));
@@ -907,6 +979,7 @@ int qwen_hip_decoder_set_trace(qwen_hip_decoder *d, int step) {
     if (step >= 0 && !d->px_trace) {
         QK_TRY(dev_alloc((void **)&d->px_trace, (size_t)QK_PX_BLOCKS * QK_PX_TRACE * 8));
         QK_HIP(hipMemset(d->px_trace, 0, (size_t)QK_PX_BLOCKS * QK_PX_TRACE * 8));
+        /* the relay kernel writes QK_RL_TRACE words per block into the same buffer */
     }
     d->px_trace_step = step < 0 ? -1 : step;
     return 0;
@@ -917,9 +990,26 @@ int qwen_hip_decoder_read_trace(qwen_hip_decoder *d, uint64_t *out, size_t n) {
     if (!d || !out || n < need) { qk_set_err("read_trace: need %zu words", need); return QWEN_HIP_EINVAL; }
     if (!d->px_trace) { qk_set_err("read_trace: tracing was never enabled"); return QWEN_HIP_ESTATE; }
     QK_TRY(use_device(d));
+    if (d->last_kernel == QWEN_HIP_KERNEL_RELAY) {
+        /* relay records are QK_RL_TRACE words per block */
+        QK_HIP(hipMemcpy(out, d->px_trace, (size_t)QK_PX_BLOCKS * QK_RL_TRACE * 8, hipMemcpyDeviceToHost));
+        return (int)QK_RL_TRACE;
+    }
     QK_HIP(hipMemcpy(out, d->px_trace, need * 8, hipMemcpyDeviceToHost));
     return (int)QK_PX_TRACE;
 }
+
+int qwen_hip_decoder_set_relay(qwen_hip_decoder *d, int on) {
+    if (!d) return QWEN_HIP_EINVAL;
+    if (on && !d->rl_ok) {
+        qk_set_err("set_relay: the relay kernel needs the 0.6B shape, the persistent engine and 256 CUs");
+        return QWEN_HIP_EINVAL;
+    }
+    d->rl_on = on != 0;
+    return 0;
+}
+
+int qwen_hip_decoder_last_kernel(const qwen_hip_decoder *d) { return d ? d->last_kernel : QWEN_HIP_EINVAL; }
 
 int qwen_hip_decoder_read_hidden(qwen_hip_decoder *d, float *out) {
     if (!d || !out) return QWEN_HIP_EINVAL;

@@ -215,6 +215,87 @@ typedef struct {
 int qk_persist_supported(int hidden, int inter, int heads, int kv_heads, int device);
 int qk_persist_launch(const qk_persist_args *a, int hidden, int inter, hipStream_t s);
 
+/* ---- relay decode (0.6B shape): two teams of CUs take the layers in turn --
+ * Blocks of XCD g with ticket rank r < 16 form team 0 (even layers), the
+ * others team 1 (odd layers).  A team computes its layer from weights already
+ * held in registers while the other team streams the next layer's weights
+ * (and its K/V rows) from HBM, so no hand-over of the computing team waits
+ * behind weight loads of its own CU.  Weights come pre-tiled (qk_relay_pack):
+ * per layer, per (XCD, team rank, wave) QK_RL_TILES tiles of 1 KB, each the
+ * B operand of one v_mfma_f32_16x16x32_bf16 (16 rows x 32 columns; lane l
+ * holds row l % 16, columns 8 (l / 16) .. + 8). */
+#define QK_RL_TEAM 16                      /* blocks of one team on one XCD */
+#define QK_RL_WAVES 4                      /* waves per block (one per SIMD) */
+#define QK_RL_TILES 60                     /* weight tiles per wave per layer */
+#define QK_RL_TILE_BYTES 1024
+#define QK_RL_KVP 64                       /* cached positions per split (held in LDS) */
+#define QK_RL_MIN_CHUNK 32                 /* positions per split, at least */
+#define QK_RL_MAX_SEQ (QK_RL_TEAM * QK_RL_KVP) /* the kernel attends over at most this many keys */
+#define QK_RL_TPL 8                        /* exchange tags per layer */
+#define QK_RL_PART 260                     /* words per split: 2 heads x (m, l, o[128]) */
+#define QK_RL_TRACE 704                    /* trace words per block */
+#define QK_RL_LINE 16                      /* words per cross-XCD single-word slot (one 128-byte line) */
+/* bytes of one layer's tiled weights */
+#define QK_RL_LAYER_BYTES ((long)QK_PX_XCD * QK_RL_TEAM * QK_RL_WAVES * QK_RL_TILES * QK_RL_TILE_BYTES)
+
+typedef struct {
+    const char *wt;            /* tiled weights, QK_RL_LAYER_BYTES per layer */
+    /* norms of layer l at layer0 + l * layer_stride + off_* (bytes) */
+    const char *layer0;
+    long layer_stride;
+    long off_nin, off_npost, off_nq, off_nk;
+    const uint16_t *emb;       /* [vocab][1024] tied embedding / LM head */
+    const float *fnorm;
+    float *k_cache, *v_cache;  /* [layer][kv_head][cap][128] */
+    int cap;
+    const float *rope_cos, *rope_sin;
+    int layers, vocab;
+    float eps, scale;
+    /* exchange words (zero-initialised); [2 teams][8 XCDs][...] unless noted */
+    unsigned long long *xq;    /* [2][8][512] q|q|k|v of the group */
+    unsigned long long *xa;    /* [2][8][16][QK_RL_PART] attention split partials */
+    unsigned long long *xm;    /* [2][8][256] merged attention output of the group */
+    unsigned long long *xo;    /* [2][8][1024] O-projection split-K partials (cross-XCD) */
+    unsigned long long *xla;   /* [2][8][1024] residual after attention, republished */
+    unsigned long long *xh;    /* [2][8][384] SwiGLU outputs of the group */
+    unsigned long long *xd;    /* [2][8][1024] down-projection split-K partials (cross-XCD) */
+    unsigned long long *xs;    /* [2][8][1024] residual after attention, slices for the next team */
+    unsigned long long *xlb;   /* [2][8][1024] input residual of a layer, republished */
+    unsigned long long *xc;    /* [256][QK_RL_LINE] LM-head candidates (value, index) */
+    unsigned long long *xv;    /* [256][QK_RL_LINE] launch check-in words */
+    unsigned *cnt;             /* [16] per-XCD tickets, zeroed before every launch */
+    unsigned *err;             /* QK_PX_ERR_* bits, zeroed before every launch */
+    unsigned epoch;            /* first tag of this launch (>= 1) */
+    unsigned long long wait_ticks;
+    int pos0, n_steps;
+    int first_tok;             /* >= 0: step 0 input is emb[first_tok] */
+    const float *x_in;         /* first_tok < 0: step 0 input row [1024] */
+    int *log, *tok_out, *pos_out;
+    float *hidden_out, *logits;
+    unsigned long long *trace; /* optional [256][QK_RL_TRACE] stamps of step trace_step */
+    int trace_step;
+} qk_relay_args;
+
+/* Trace points per block (100 MHz wall clock), written by wave 0 for the
+ * block's own layers l at 16*l + {0: input wait entered, 1: cross-XCD half of
+ * the input residual in, 2: input residual gathered, 3: Q stored, 4: q|k|v
+ * gathered, 5: split partials stored, 6: merge slices in, 7: merged output
+ * gathered, 8: O stored, 9: cross-XCD half of the post-attention residual in,
+ * 10: post-attention residual gathered, 11: SwiGLU stored, 12: SwiGLU outputs
+ * gathered, 13: down stored, 14: next layer's loads issued}; and at
+ * 16*layers + {0: LM entered, 1: final residual cross half in, 2: final
+ * residual gathered, 3: candidates stored, 4: token ready (team 0)}. */
+
+/* tags one launch of n steps consumes */
+#define QK_RL_TAGS(layers, n) (1u + (unsigned)(n) * (QK_RL_TPL * ((unsigned)(layers) + 1u)))
+
+int qk_relay_supported(int hidden, int inter, int heads, int kv_heads, int device);
+int qk_relay_launch(const qk_relay_args *a, hipStream_t s);
+/* Tile layer l's row-major weights (stacked Wqkv, W_o, interleaved gate|up,
+ * W_down; 0.6B shape) into dst (QK_RL_LAYER_BYTES). */
+int qk_relay_pack(char *dst, const uint16_t *wqkv, const uint16_t *wo, const uint16_t *wgu, const uint16_t *wdown,
+                  hipStream_t s);
+
 /* ---- prefill (MFMA) ---------------------------------------------------- */
 /* Optionally x += part[0] + ... + part[nsum-1] (rows of pstride floats apart,
  * in place, split order), then hi/lo = bf16 split of rms_norm(x)*w (w NULL:
