@@ -67,20 +67,20 @@ GRAPH_KERNELS = ("gemv_kernel", "attn_decode_fused", "attn_merge", "argmax_finis
 PMC_STEPS = 16
 
 
-def pmc_pass(counter, workload, timeout=150):
+def pmc_pass(counter, workload, timeout=150, extra=None):
     """One child run of this script under rocprofv3 --pmc <counter>: a short
     decode of PMC_STEPS steps (plus a 256 MiB calibration copy kernel).
     Returns (KiB per decode step, calibration factor), or None.  Persistent
-    engine: the counter of the last px_decode dispatch (the timed launch of
-    PMC_STEPS steps) / PMC_STEPS.  Graph engine: the step's kernels summed,
-    per argmax_finish."""
+    engine: the counter of the last persistent-kernel dispatch (rl_decode or
+    px_decode: the timed launch of PMC_STEPS steps) / PMC_STEPS.  Graph engine:
+    the step's kernels summed, per argmax_finish."""
     exe = shutil.which("rocprofv3")
     if not exe:
         return None
     out = tempfile.mkdtemp(prefix="qk_pmc_")
     cmd = [exe, "--pmc", counter, "-d", out, "-o", "run", "--output-format", "csv", "--",
-           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--steps", str(PMC_STEPS),
-           "--warmup", "2", "--calib-copy-mb", "256", "--workload", workload]
+           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--no-c3", "--steps", str(PMC_STEPS),
+           "--warmup", "2", "--calib-copy-mb", "256", "--workload", workload] + list(extra or [])
     env = dict(os.environ, TMPDIR="/tmp")
     errlog = os.path.join(out, "child.err")
     try:
@@ -114,7 +114,7 @@ def pmc_pass(counter, workload, timeout=150):
         if not cal:
             return None
         factor = 256 * 1024 / cal
-        px = sorted(d for d, n in names.items() if "px_decode" in n)
+        px = sorted(d for d, n in names.items() if "px_decode" in n or "rl_decode" in n)
         if px:
             return per_dispatch[px[-1]] / PMC_STEPS * factor, factor
         total = sum(v for d, v in per_dispatch.items() if any(k in names[d] for k in GRAPH_KERNELS))
@@ -446,17 +446,73 @@ def cpu_baseline(wl, rows, first_token, threads, decode_steps):
             "first_token_matches_gpu": None if sampled else bool(tok == first_token)}
 
 
-def launch_fields(engine, K, step_bytes, gpu_ms):
+KERNEL_NAMES = {1: "px_decode (split persistent kernel: every CU streams its share of every layer)",
+                2: "rl_decode (relay persistent kernel: two teams of 16 CUs per XCD take the layers in turn, "
+                   "one computing from register-held weights while the other streams the next layer)"}
+
+
+def launch_fields(engine, K, step_bytes, gpu_ms, kernel=0):
     """What one launch of the dominant kernel is: the persistent engine runs the
-    K timed steps in one px_decode dispatch; the graph engine replays one graph
-    (per-layer GEMV/attention kernels + LM head argmax) per step."""
+    K timed steps in one rl_decode / px_decode dispatch; the graph engine
+    replays one graph (per-layer GEMV/attention kernels + LM head argmax) per
+    step."""
     if engine == 2:
-        return {"kernel": f"px_decode (persistent kernel, one block per CU: {K} greedy decode steps per launch)",
+        return {"kernel": f"{KERNEL_NAMES.get(kernel, 'persistent kernel')}, one block per CU: {K} greedy decode "
+                          f"steps per launch",
                 "steps_per_launch": K, "bytes_per_launch": round(sum(step_bytes)),
                 "launch_us": round(gpu_ms * 1e3, 3), "step_us": round(gpu_ms * 1e3 / K, 3)}
     return {"kernel": "decode step graph (one token: all layers + LM head argmax)", "steps_per_launch": 1,
             "bytes_per_launch": round(sum(step_bytes) / K), "launch_us": round(gpu_ms * 1e3 / K, 3),
             "step_us": round(gpu_ms * 1e3 / K, 3)}
+
+
+C3_LINE_STEPS = 64
+
+
+def run_c3_decode(qa, K=C3_LINE_STEPS, W=8):
+    """The 1.7B decode carried in the default (C1) line: the C3 shape (1500 audio
+    rows + 16 ids, prefill 1515 rows, forward the last row), then K timed
+    greedy steps from position 1516 in one persistent launch; HIP events on
+    the decoder's stream.  No CPU leg and no counter passes (those are in
+    --workload c3)."""
+    import numpy as np
+    import torch
+    wl = WORKLOADS["c3"]
+    cfg = qa.preset(wl["model_b"])
+    n_rows = wl["n_audio"] + wl["n_ids"]
+    d = qa.Decoder(cfg, 0, n_rows + K + W + 64)
+    d.set_fallback(False)
+    t0 = time.time()
+    d.load_synthetic(0, 0.02, 0.0)
+    rows, _, _ = qa.prompt_rows(cfg, wl["n_audio"], wl["n_ids"])
+    d.prefill(rows[:-1])
+    first = d.forward(rows[-1])
+    base = d.kv_len()
+    d.generate(first, W)
+    d.set_kv_len(base)
+    stream = torch.cuda.ExternalStream(d.stream())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    tw0 = time.perf_counter()
+    toks = d.generate(first, K)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - tw0
+    gpu_ms = e0.elapsed_time(e1)
+    step_bytes = [d.step_bytes(base + i) for i in range(K)]
+    achieved = float(np.mean(step_bytes)) / (gpu_ms * 1e-3 / K) / 1e9
+    kernel = d.last_kernel() if d.engine() == 2 else 0
+    d.close()
+    log(f"[gpu] c3 decode in the line: {K} steps {K / wall:.1f} tok/s ({gpu_ms * 1e3 / K:.1f} us/step, "
+        f"{achieved / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s); setup {time.time() - t0:.1f}s")
+    return {"workload": "C3 Qwen3-ASR-1.7B decoder: prefill 1515 rows (1500 audio + 16 ids), forward, then greedy decode",
+            "steps": K, "decode_positions": [base, base + K - 1], "value": round(K / wall, 3), "unit": "tok/s",
+            "step_us": round(gpu_ms * 1e3 / K, 3),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         **launch_fields(2 if kernel else 0, K, step_bytes, gpu_ms, kernel)},
+            "tokens_head": [int(first)] + [int(t) for t in toks[:7]]}
 
 
 def main():
@@ -468,7 +524,10 @@ def main():
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c1")
     ap.add_argument("--engine", type=int, default=None,
                     help="0 graph of fused kernels, 1 eager, 2 persistent kernel (default where supported)")
+    ap.add_argument("--kernel", choices=("auto", "split", "relay"), default="auto",
+                    help="persistent kernel: relay where available and the positions fit (default), or force one")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c3", action="store_true", help="default (C1) line: skip the 1.7B decode block")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc child runs")
     ap.add_argument("--cpu-steps", type=int, default=48)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
@@ -540,6 +599,8 @@ def main():
     d = qa.Decoder(cfg, 0, n_rows + K + W + 1024)
     if args.engine is not None:
         d.set_engine(args.engine)
+    if args.kernel != "auto":
+        d.set_relay(args.kernel == "relay")
     d.set_fallback(False)          # a failed persistent launch fails the run instead of being redone
     t0 = time.time()
     d.load_synthetic(0, 0.02, 0.0)
@@ -592,12 +653,15 @@ def main():
 
     traffic = None
     traffic_note = None
+    engine = d.engine()
+    kernel = d.last_kernel() if engine == 2 else 0
     if not args.no_traffic:
-        fr = pmc_pass("FETCH_SIZE", args.workload)
-        wr = pmc_pass("WRITE_SIZE", args.workload)
+        extra = ["--kernel", args.kernel]
+        fr = pmc_pass("FETCH_SIZE", args.workload, extra=extra)
+        wr = pmc_pass("WRITE_SIZE", args.workload, extra=extra)
         if fr and wr:
             per_step = (fr[0] + wr[0]) * 1024
-            per_launch = K if d.engine() == 2 else 1
+            per_launch = K if engine == 2 else 1
             traffic = round(per_step * per_launch)
             traffic_note = (f"per launch = {per_launch} x the per-step HBM bytes measured over {PMC_STEPS} decode "
                             f"steps at positions {n_rows}-{n_rows + PMC_STEPS + 1}: FETCH_SIZE x {fr[1]:.4f} + "
@@ -611,6 +675,9 @@ def main():
         threads = min(os.cpu_count() or 1, 16)
         cpu = cpu_baseline(wl, rows, first, threads, args.cpu_steps)
 
+    d.close()
+    c3 = run_c3_decode(qa) if args.workload == "c1" and not args.no_c3 else None
+
     out = {
         "metric": "decode tok/s at batch 1 (0.6B, 1.7B) + % of peak HBM GB/s; prefill tok/s",
         "value": round(value, 3), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -619,16 +686,18 @@ def main():
         "config": {"workload": wl["desc"], "batch": 1, "weights": "bf16 N(0,0.02) seed 0, norms 1.0",
                    "activations": "fp32, fp32 accumulation", "kv_cache": "fp32",
                    "prefill_rows": n_rows - 1, "decode_positions": [base, base + K - 1],
-                   "engine": {0: "graph", 1: "eager", 2: "persistent"}.get(d.engine(), d.engine())},
+                   "engine": {0: "graph", 1: "eager", 2: "persistent"}.get(engine, engine),
+                   "kernel": {0: None, 1: "split", 2: "relay"}.get(kernel)},
         "prefill_tok_s": round((n_rows - 1) / prefill_s, 2),
         "prefill": prefill_rates(cfg, n_rows - 1, prefill_s),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
-                     **launch_fields(d.engine(), K, step_bytes, gpu_ms)},
+                     **launch_fields(engine, K, step_bytes, gpu_ms, kernel)},
         "cpu_baseline": cpu,
         "tokens_head": [int(first)] + [int(t) for t in toks[:7]],
     }
-    d.close()
+    if c3:
+        out["c3_decode"] = c3
     print(json.dumps(out), flush=True)
 
 
