@@ -145,6 +145,16 @@ __device__ __forceinline__ bool rl_poll(const qk_relay_args &a, const u64 *base,
     }
 }
 
+// rl_poll over a contiguous range of exactly 64 * PER words with lane ln
+// owning words [i0 + PER ln, + PER): on success v[j] holds word i0 + PER ln + j.
+template <int PER>
+__device__ __forceinline__ bool rl_poll_vec(const qk_relay_args &a, const u64 *base, int i0, unsigned tag,
+                                            float (&v)[PER], int lane) {
+    return rl_poll<PER>(
+        a, base, [&](int i) { const int k = i - i0; return i0 + PER * (k & 63) + (k >> 6); }, i0, i0 + 64 * PER, tag,
+        [&](int i, float x) { v[(i - i0) >> 6] = x; }, lane);
+}
+
 // ---------------------------------------------------------------------------
 // weights and products
 // ---------------------------------------------------------------------------
@@ -358,7 +368,6 @@ struct RlShared {
     float nqk[256];                 // q norm | k norm
     float rope[256];                // cos | sin at the layer's position
     float qkv[512];                 // the group's raw q|q|k|v
-    float qr[2][128], kr[128], vr[128];
     union {
         struct {
             float sm_m[RL_NG][2], sm_l[RL_NG][2];
@@ -417,11 +426,14 @@ __device__ __forceinline__ void rl_load_layer(const qk_relay_args &a, RlShared &
 // partials at part + g' * 1024 + 64 q (tag tp; the base from bsrc (tag tb)
 // when given, else the block's own S.xs), republished at xl (tag tx); then
 // the XCD's whole residual gathered into S.xs with per-wave sums of squares in
-// S.ssq.  Order of the sum: x + (P_0 + ... + P_7), as x += o in
-// qwen_asr_decoder.c:458, :468.
+// S.ssq and, when w is given, the planes of x o w in S.xp (the next product's
+// operand; its rows take the 1/rms factor in their epilogue, rl_rinv).  Wave
+// w gathers elements [256 w, 256 w + 256), the norm-weight range its own
+// load-phase DMA filled.  Order of the sum: x + (P_0 + ... + P_7), as x += o
+// in qwen_asr_decoder.c:458, :468.
 __device__ __forceinline__ bool rl_residual(const qk_relay_args &a, RlShared &S, const u64 *part, unsigned tp,
-                                            const u64 *bsrc, unsigned tb, u64 *xl, unsigned tx, int q, int wave,
-                                            int lane, u64 *tr1, u64 *tr2) {
+                                            const u64 *bsrc, unsigned tb, u64 *xl, unsigned tx, const float *w, int q,
+                                            int wave, int lane, u64 *tr1, u64 *tr2) {
     // wave w: the slices of XCDs 2w, 2w + 1
     bool ok = rl_poll<2>(
         a, part, [&](int i) { return (2 * wave + (i >> 6)) * RL_H + RL_SO * q + (i & 63); }, 0, 2 * RL_SO, tp,
@@ -440,14 +452,22 @@ __device__ __forceinline__ bool rl_residual(const qk_relay_args &a, RlShared &S,
         for (int gg = 1; gg < RL_XCD; gg++) o += S.ysum[gg][lane];
         rl_put_local(xl + RL_SO * q + lane, S.xs[RL_SO * q + lane] + o, tx);
     }
+    float v[4];
+    ok = rl_poll_vec<4>(a, xl, 256 * wave, tx, v, lane);
     float ss = 0.0f;
-    ok = rl_poll<4>(
-        a, xl, [&](int i) { return i; }, 256 * wave, 256 * wave + 256, tx,
-        [&](int i, float v) {
-            S.xs[i] = v;
-            ss = fmaf(v, v, ss);
-        },
-        lane);
+    if (ok) {
+        const int i = 256 * wave + 4 * lane;
+        *reinterpret_cast<float4 *>(&S.xs[i]) = make_float4(v[0], v[1], v[2], v[3]);
+        ss = fmaf(v[0], v[0], ss);
+        ss = fmaf(v[1], v[1], ss);
+        ss = fmaf(v[2], v[2], ss);
+        ss = fmaf(v[3], v[3], ss);
+        if (w) {
+            const float4 wv = *reinterpret_cast<const float4 *>(&w[i]);
+            rl_plane2(S.xp, i, v[0] * wv.x, v[1] * wv.y);
+            rl_plane2(S.xp, i + 2, v[2] * wv.z, v[3] * wv.w);
+        }
+    }
     ss = wave_sum(ss);
     if (lane == 0) S.ssq[wave] = ss;
     if (!ok) S.abort_ = 1;
@@ -455,6 +475,16 @@ __device__ __forceinline__ bool rl_residual(const qk_relay_args &a, RlShared &S,
     if (S.abort_) return false;
     if (tr2) *tr2 = wall_clock64();
     return true;
+}
+
+// 1 / rms of S.xs from the per-wave sums of squares (qwen_rms_norm,
+// qwen_asr_kernels.c:750-809): a product over the planes of x o w times this
+// is the product over rms_norm(x) * w.
+__device__ __forceinline__ float rl_rinv(const qk_relay_args &a, const RlShared &S) {
+    float ss = S.ssq[0];
+#pragma unroll
+    for (int i = 1; i < RL_NW; i++) ss += S.ssq[i];
+    return 1.0f / sqrtf(ss / (float)RL_H + a.eps);
 }
 
 // rms_norm(S.xs) * w (qwen_rms_norm, qwen_asr_kernels.c:750-809) from the
@@ -559,20 +589,21 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                 ss = fmaf(x.w, x.w, ss);
                 ss = wave_sum(ss);
                 if (lane == 0) S.ssq[wave] = ss;
-                rl_wait_vm();   // this layer's operands have landed
+                rl_wait_vm();   // this layer's operands have landed (this wave's DMA filled nin[256 wave ..])
+                const float4 nw = *reinterpret_cast<const float4 *>(&S.nin[i]);
+                rl_plane2(S.xp, i, x.x * nw.x, x.y * nw.y);
+                rl_plane2(S.xp, i + 2, x.z * nw.z, x.w * nw.w);
                 rl_sync();
                 mark(RL_TM * l + 1);
                 mark(RL_TM * l + 2);
             } else {
                 const unsigned tp = rl_tag(a, s, l - 1, 6);
                 const bool ok = rl_residual(a, S, a.xd + ((1 - t) * WG) * RL_H, tp, a.xs + ((1 - t) * WG + g) * RL_H, tp,
-                                            a.xlb + (t * WG + g) * RL_H, T(7), q, wave, lane,
+                                            a.xlb + (t * WG + g) * RL_H, T(7), S.nin, q, wave, lane,
                                             tracing ? trb + RL_TM * l + 1 : nullptr, tracing ? trb + RL_TM * l + 2 : nullptr);
                 if (!ok) return;
                 rl_wait_vm();
             }
-            rl_norm(a, S, S.nin, &S.xp, nullptr, wave, lane);
-            rl_sync();
             mark(RL_TM * l + 3);
 
             // ---- Q: 32 rows of the group's Q|K|V (qwen_linear_nobias_bf16_qkv, qwen_asr_kernels.c:434-460) ----
@@ -594,7 +625,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
             rl_sync();
             if (wave == 0 && lane < 32) {
                 const int rt = lane >> 4, n = lane & 15;
-                const float y = S.red[rt][n] + S.red[rt + 2][n];
+                const float y = (S.red[rt][n] + S.red[rt + 2][n]) * rl_rinv(a, S);
                 rl_put_local(a.xq + (t * WG + g) * 512 + qrow + lane, y, T(0));
             }
             mark(RL_TM * l + 4);
@@ -612,42 +643,26 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
             const RlSplit sp(pos, q);
             float *kcl = a.k_cache + ((long)l * RL_XCD + g) * (long)a.cap * 128;
             float *vcl = a.v_cache + ((long)l * RL_XCD + g) * (long)a.cap * 128;
-            if (wave < 3) {
-                // rms_norm_per_head (qwen_asr_kernels.c:811-873) + apply_rope_neox (:1182-1247)
-                const float *src = S.qkv + wave * 128;
-                const float *nw = S.nqk + (wave < 2 ? 0 : 128);
-                float x1 = src[lane], x2 = src[lane + 64];
-                norm_rope_pair(x1, x2, nw, a.eps, S.rope[lane], S.rope[128 + lane], lane);
-                float *dst = wave < 2 ? S.qr[wave] : S.kr;
-                dst[lane] = x1;
-                dst[lane + 64] = x2;
-                if (wave == 2 && sp.last) {   // K store at pos (qwen_asr_decoder.c:446)
-                    kcl[(long)pos * 128 + lane] = x1;
-                    kcl[(long)pos * 128 + lane + 64] = x2;
-                }
-            } else if (wave == 3) {
-                const float v1 = S.qkv[384 + lane], v2 = S.qkv[448 + lane];
-                S.vr[lane] = v1;
-                S.vr[lane + 64] = v2;
-                if (sp.last) {                // V store at pos (:447)
-                    vcl[(long)pos * 128 + lane] = v1;
-                    vcl[(long)pos * 128 + lane + 64] = v2;
-                }
-            }
-            rl_sync();
             mark(RL_TM * l + 6);
             // causal attention of the group's two query heads over this block's
             // positions (qwen_causal_attention_heads, qwen_asr_kernels.c:1050-1097):
             // 16-lane group gid folds positions s0 + gid + 16 j from LDS; lane c
             // of the group owns dims 4c .. 4c+3 and 64+4c .. 64+4c+3, so a group's
             // 16-byte reads of one K or V row cover 256 contiguous bytes
+            // Every group normalises and rotates the two query heads itself (no
+            // stage of its own): rms_norm_per_head (qwen_asr_kernels.c:811-873) +
+            // apply_rope_neox (:1182-1247); the RoPE pair (d, d + 64) sits in one lane.
             if (sp.active) {
                 const int gid = wave * 4 + (lane >> 4), gl = lane & 15, d0 = 4 * gl, d1 = 64 + 4 * gl;
+                const float4 c4 = *reinterpret_cast<const float4 *>(&S.rope[d0]);
+                const float4 s4 = *reinterpret_cast<const float4 *>(&S.rope[128 + d0]);
                 float qv[2][8];
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const float4 lo = *reinterpret_cast<const float4 *>(&S.qr[h][d0]);
-                    const float4 hi = *reinterpret_cast<const float4 *>(&S.qr[h][d1]);
+                    float4 lo = *reinterpret_cast<const float4 *>(&S.qkv[h * 128 + d0]);
+                    float4 hi = *reinterpret_cast<const float4 *>(&S.qkv[h * 128 + d1]);
+                    norm_rope_row16(lo, hi, *reinterpret_cast<const float4 *>(&S.nqk[d0]),
+                                    *reinterpret_cast<const float4 *>(&S.nqk[d1]), c4, s4, a.eps);
                     qv[h][0] = lo.x; qv[h][1] = lo.y; qv[h][2] = lo.z; qv[h][3] = lo.w;
                     qv[h][4] = hi.x; qv[h][5] = hi.y; qv[h][6] = hi.z; qv[h][7] = hi.w;
                 }
@@ -659,6 +674,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                 const int nc = sp.cend - sp.s0;
 #pragma unroll
                 for (int half = 0; half < 2; half++) {
+                    if (half == 1 && nc <= 2 * RL_NG) break;   // block-uniform: no position of the second half
                     float4 kk[2][2], vv[2][2];
                     bool in[2];
 #pragma unroll
@@ -673,11 +689,17 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                     }
                     rl_fold_n<2>(qv, kk, vv, in, a.scale, m, ls, o);
                 }
-                if (sp.last && gid == 0) {   // position pos: this step's k/v
-                    const float4 k0 = *reinterpret_cast<const float4 *>(&S.kr[d0]);
-                    const float4 k1 = *reinterpret_cast<const float4 *>(&S.kr[d1]);
-                    const float4 v0 = *reinterpret_cast<const float4 *>(&S.vr[d0]);
-                    const float4 v1 = *reinterpret_cast<const float4 *>(&S.vr[d1]);
+                if (sp.last && gid == 0) {   // position pos: this step's k/v, appended to the cache (qwen_asr_decoder.c:446-447)
+                    float4 k0 = *reinterpret_cast<const float4 *>(&S.qkv[256 + d0]);
+                    float4 k1 = *reinterpret_cast<const float4 *>(&S.qkv[256 + d1]);
+                    norm_rope_row16(k0, k1, *reinterpret_cast<const float4 *>(&S.nqk[128 + d0]),
+                                    *reinterpret_cast<const float4 *>(&S.nqk[128 + d1]), c4, s4, a.eps);
+                    const float4 v0 = *reinterpret_cast<const float4 *>(&S.qkv[384 + d0]);
+                    const float4 v1 = *reinterpret_cast<const float4 *>(&S.qkv[384 + d1]);
+                    *reinterpret_cast<float4 *>(kcl + (long)pos * 128 + d0) = k0;
+                    *reinterpret_cast<float4 *>(kcl + (long)pos * 128 + d1) = k1;
+                    *reinterpret_cast<float4 *>(vcl + (long)pos * 128 + d0) = v0;
+                    *reinterpret_cast<float4 *>(vcl + (long)pos * 128 + d1) = v1;
                     rl_fold1(qv, k0, k1, v0, v1, a.scale, m, ls, o);
                 }
 #pragma unroll
@@ -707,7 +729,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                 }
                 // the K/V row stored at pos is read by other blocks of this XCD
                 // in later steps: the stores retire before this block publishes
-                if (sp.last && (wave == 2 || wave == 3)) rl_wait_vm();
+                if (sp.last && wave == 0) rl_wait_vm();
                 u64 *dst = a.xa + ((t * WG + g) * QK_RL_TEAM + q) * (long)QK_RL_PART + h * 130;
                 rl_put_local(dst + 2 + d, acc, T(1));
                 if (d == 0) {
@@ -734,34 +756,22 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                 rl_sync();
                 if (S.abort_) return;
                 mark(RL_TM * l + 9);
-                if (wave == 0 && lane < 16) {
-                    float M = -INFINITY, Lh = 0.0f, acc = 0.0f;
-                    for (int c0 = 0; c0 < sp.nsplit; c0 += 8) {
-                        float mv[8], lv[8], ov[8];
-#pragma unroll
-                        for (int j = 0; j < 8; j++) {
-                            const bool in = c0 + j < sp.nsplit;
-                            const float *pp = S.part + (in ? c0 + j : 0) * 18;
-                            mv[j] = in ? pp[0] : -INFINITY;
-                            lv[j] = in ? pp[1] : 0.0f;
-                            ov[j] = in ? pp[2 + lane] : 0.0f;
-                        }
-                        float Mc = M;
-#pragma unroll
-                        for (int j = 0; j < 8; j++) Mc = fmaxf(Mc, mv[j]);
-                        const float sc = (M == -INFINITY) ? 0.0f : __expf(M - Mc);
-                        Lh *= sc;
-                        acc *= sc;
-#pragma unroll
-                        for (int j = 0; j < 8; j++) {
-                            const float e = (mv[j] == -INFINITY) ? 0.0f : __expf(mv[j] - Mc);
-                            Lh = fmaf(lv[j], e, Lh);
-                            acc = fmaf(ov[j], e, acc);
-                        }
-                        M = Mc;
-                    }
+                {
+                    // 16 dims x 16 splits on the block's 256 lanes: lane (4 wave + lane / 16, lane % 16) holds
+                    // split lane % 16 of dim d0 + 4 wave + lane / 16; max, sum and weighted sum over the 16-lane
+                    // row (the online merge of qwen_causal_attention_heads' running max and sum,
+                    // qwen_asr_kernels.c:1073-1094, taken over the splits at once)
+                    const int dl = 4 * wave + (lane >> 4), si = lane & 15;
+                    const bool in = si < sp.nsplit;
+                    const float mv = in ? S.part[si * 18] : -INFINITY;
+                    const float lv = in ? S.part[si * 18 + 1] : 0.0f;
+                    const float ov = in ? S.part[si * 18 + 2 + dl] : 0.0f;
+                    const float M = group_max<16>(mv);
+                    const float e = (mv == -INFINITY) ? 0.0f : __expf(mv - M);
+                    const float Lh = group_sum<16>(lv * e);
+                    const float acc = group_sum<16>(ov * e);
                     // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
-                    rl_put_local(a.xm + (t * WG + g) * 256 + h * 128 + d0 + lane, acc * (1.0f / Lh), T(2));
+                    if (si == 0) rl_put_local(a.xm + (t * WG + g) * 256 + h * 128 + d0 + dl, acc * (1.0f / Lh), T(2));
                 }
                 mark(RL_TM * l + 10);
                 const bool ok2 = rl_poll<1>(
@@ -795,12 +805,10 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
             // ---- F: x' = x + O; rms_norm; 48 gate|up rows + SwiGLU (qwen_asr_decoder.c:458-466) ----
             {
                 const bool ok = rl_residual(a, S, a.xo + (t * WG) * RL_H, T(3), nullptr, 0u, a.xla + (t * WG + g) * RL_H,
-                                            T(4), q, wave, lane, tracing ? trb + RL_TM * l + 13 : nullptr,
+                                            T(4), S.npost, q, wave, lane, tracing ? trb + RL_TM * l + 13 : nullptr,
                                             tracing ? trb + RL_TM * l + 14 : nullptr);
                 if (!ok) return;
             }
-            rl_norm(a, S, S.npost, &S.xp, nullptr, wave, lane);
-            rl_sync();
             mark(RL_TM * l + 15);
             {
                 // wave w: row tiles 0..2 over k tiles [8 w, 8 w + 8)
@@ -822,7 +830,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
             rl_sync();
             mark(RL_TM * l + 16);
             if (wave == 0 && lane < 48) {
-                const float y = ((S.red[0][lane] + S.red[1][lane]) + S.red[2][lane]) + S.red[3][lane];
+                const float y = (((S.red[0][lane] + S.red[1][lane]) + S.red[2][lane]) + S.red[3][lane]) * rl_rinv(a, S);
                 // rows 2i (gate), 2i+1 (up) sit in adjacent lanes (qwen_swiglu_multiply, qwen_asr_kernels.c:930-931)
                 const float up = __shfl_xor(y, 1, 64);
                 if ((lane & 1) == 0)
@@ -885,7 +893,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
             }
             const unsigned tp = rl_tag(a, s, L - 1, 6);
             const bool ok = rl_residual(a, S, a.xd + (tl * WG) * RL_H, tp, a.xs + (tl * WG + g) * RL_H, tp,
-                                        a.xlb + (team * WG + g) * RL_H, rl_tag(a, s, L, 7), q, wave, lane,
+                                        a.xlb + (team * WG + g) * RL_H, rl_tag(a, s, L, 7), nullptr, q, wave, lane,
                                         tracing ? trb + RL_TM * L + 1 : nullptr, tracing ? trb + RL_TM * L + 2 : nullptr);
             if (!ok) return;
             rl_wait_vm();
