@@ -208,15 +208,18 @@ int qwen_hip_decoder_read_trace(qwen_hip_decoder *dec, uint64_t *out, size_t n);
  * last_kernel: the kernel of the last persistent launch (its trace layout):
  * QWEN_HIP_KERNEL_SPLIT or QWEN_HIP_KERNEL_RELAY, 0 before any.
  *
- * Relay trace layout (read_trace returns 512 words per block): for layer l
- * of the block's team (team 0 even layers, team 1 odd), words 16*l + {0 input
+ * Relay trace layout (read_trace returns 704 words per block): for layer l
+ * of the block's team (team 0 even layers, team 1 odd), words 24*l + {0 input
  * wait entered, 1 cross-XCD half of the input residual in, 2 input residual
- * gathered, 3 Q stored, 4 q|k|v gathered, 5 split partials stored, 6 merge
- * slices in, 7 merged attention gathered, 8 O stored, 9 cross-XCD half of the
- * post-attention residual in, 10 post-attention residual gathered, 11 SwiGLU
- * stored, 12 SwiGLU outputs gathered, 13 down stored, 14 next layer's loads
- * issued}; then 16*layers + {0 LM entered, 1 final residual cross half in,
- * 2 gathered, 3 candidate stored, 4 token ready (team 0 only)}.  No
+ * gathered, 4 Q stored, 5 q|k|v gathered, 6 attention entered, 7 fold done,
+ * 8 split partials stored, 9 merge slices in, 10 merged dims stored,
+ * 11 merged attention gathered, 12 O stored, 13 cross-XCD half of the
+ * post-attention residual in, 14 post-attention residual gathered, 16 gate|up
+ * products reduced, 17 SwiGLU stored, 18 SwiGLU outputs gathered, 19 down
+ * stored, 20 next layer's loads issued} (3 and 15 repeat 2 and 14); then
+ * 24*layers + {0 LM entered, 1 final residual cross half in, 2 gathered,
+ * 3 candidate stored, 4 token ready (team 0 only)}.  A record holds one
+ * launch: set_trace clears it.  No
  * reference counterpart (the reference decodes on the CPU). */
 #define QWEN_HIP_KERNEL_SPLIT 1
 #define QWEN_HIP_KERNEL_RELAY 2

@@ -976,11 +976,10 @@ int qwen_hip_decoder_set_trace(qwen_hip_decoder *d, int step) {
     if (!d) return QWEN_HIP_EINVAL;
     if (!d->px_ok) { qk_set_err("set_trace: the persistent engine is not available"); return QWEN_HIP_ESTATE; }
     QK_TRY(use_device(d));
-    if (step >= 0 && !d->px_trace) {
-        QK_TRY(dev_alloc((void **)&d->px_trace, (size_t)QK_PX_BLOCKS * QK_PX_TRACE * 8));
-        QK_HIP(hipMemset(d->px_trace, 0, (size_t)QK_PX_BLOCKS * QK_PX_TRACE * 8));
-        /* the relay kernel writes QK_RL_TRACE words per block into the same buffer */
-    }
+    /* the relay kernel writes QK_RL_TRACE words per block into the same buffer;
+     * cleared whenever tracing is (re)enabled, so a record holds one launch's stamps */
+    if (step >= 0 && !d->px_trace) QK_TRY(dev_alloc((void **)&d->px_trace, (size_t)QK_PX_BLOCKS * QK_PX_TRACE * 8));
+    if (step >= 0) QK_HIP(hipMemset(d->px_trace, 0, (size_t)QK_PX_BLOCKS * QK_PX_TRACE * 8));
     d->px_trace_step = step < 0 ? -1 : step;
     return 0;
 }

@@ -277,14 +277,16 @@ typedef struct {
 } qk_relay_args;
 
 /* Trace points per block (100 MHz wall clock), written by wave 0 for the
- * block's own layers l at 16*l + {0: input wait entered, 1: cross-XCD half of
- * the input residual in, 2: input residual gathered, 3: Q stored, 4: q|k|v
- * gathered, 5: split partials stored, 6: merge slices in, 7: merged output
- * gathered, 8: O stored, 9: cross-XCD half of the post-attention residual in,
- * 10: post-attention residual gathered, 11: SwiGLU stored, 12: SwiGLU outputs
- * gathered, 13: down stored, 14: next layer's loads issued}; and at
- * 16*layers + {0: LM entered, 1: final residual cross half in, 2: final
- * residual gathered, 3: candidates stored, 4: token ready (team 0)}. */
+ * block's own layers l at 24*l + {0: input wait entered, 1: cross-XCD half of
+ * the input residual in, 2: input residual gathered (planes of x*w written),
+ * 3: = 2, 4: Q stored, 5: q|k|v gathered, 6: attention entered, 7: fold done,
+ * 8: split partials stored, 9: merge slices in, 10: merged dims stored,
+ * 11: merged output gathered, 12: O stored, 13: cross-XCD half of the
+ * post-attention residual in, 14: post-attention residual gathered, 15: = 14,
+ * 16: gate|up products reduced, 17: SwiGLU stored, 18: SwiGLU outputs
+ * gathered, 19: down stored, 20: next layer's loads issued}; and at
+ * 24*layers + {0: LM entered, 1: final residual cross half in, 2: final
+ * residual gathered, 3: candidate stored, 4: token ready (team 0)}. */
 
 /* tags one launch of n steps consumes */
 #define QK_RL_TAGS(layers, n) (1u + (unsigned)(n) * (QK_RL_TPL * ((unsigned)(layers) + 1u)))

@@ -61,6 +61,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 #define RL_SO (RL_H / QK_RL_TEAM)   // 64 O / down rows per block
 #define RL_NG 16                    // 16-lane attention groups (waves 0-3)
 #define RL_TM 24                    // trace stamps per layer
+static_assert(QK_RL_TRACE <= QK_PX_TRACE, "the two persistent kernels share one trace buffer");
 
 static_assert(QK_RL_TEAM == 16 && RL_NW == 4 && QK_RL_TILES == 60, "layout constants");
 static_assert(QK_RL_KVP * QK_RL_TEAM >= QK_RL_MAX_SEQ && QK_RL_MAX_SEQ == QWEN_HIP_RELAY_MAX_POS, "split capacity");

@@ -291,19 +291,35 @@ def free_run(d, rows, g):
     return len(toks)
 
 
-@pytest.mark.parametrize("engine", [0, 2])
+# decode paths: (engine, relay kernel on/off); the relay kernel runs the
+# persistent engine's launches whose positions stay below 1024 (the goldens')
+PATHS = {"graph": (0, None), "split": (2, False), "relay": (2, True)}
+
+
+def set_path(d, path):
+    engine, relay = PATHS[path]
+    d.set_engine(engine)
+    if relay is not None:
+        d.set_relay(relay)
+    return engine
+
+
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("name", ["c1_short", "c1_full"])
-def test_06b_golden(P, model06, name, engine):
+def test_06b_golden(P, model06, name, path):
     g = np.load(os.path.join(GOLD, f"{name}.npz"))
     d, emb = model06
-    d.set_engine(engine)
+    engine = set_path(d, path)
     assert P.checksum_u16(emb) == int(g["emb_checksum"])
     rows, ids = prompt(P, P.CFG_06B, emb, int(g["n_audio"]), int(g["n_ids"]))
     assert np.array_equal(ids, g["ids"])
     worst, near = teacher_forced(d, rows, g)
     agree = free_run(d, rows, g)
     assert d.engine() == engine, "the engine fell back during the run"
-    print(f"{name} engine {engine}: max |dlogit| on reference top-8 = {worst:.3e}; near-tie steps {near}; "
+    if engine == 2:
+        assert d.last_kernel() == {"split": 1, "relay": 2}[path], "the persistent launches ran another kernel"
+    d.set_relay(True)
+    print(f"{name} {path}: max |dlogit| on reference top-8 = {worst:.3e}; near-tie steps {near}; "
           f"free run agrees for {agree}/{len(g['tokens'])} tokens")
 
 

@@ -106,7 +106,11 @@ def test_c4_long_context_vs_oracle(qa, c4, engine):
 
 
 # ----------------------------------------------------------------- C5
-C5_HEAD, C5_AUDIO, C5_BACK, C5_STEPS, C5_CHUNKS, C5_CAP, C5_KEEP = 9, 26, 5, 24, 8, 260, 3
+# C5 at its real window: the cache capped at 1024 positions, 24 chunks.  Each
+# chunk adds 49 positions (roll back 5, prefill 30, 24 forwards); a 21-row head
+# makes the cache reach 21 + 25 + 24 + 19 x 49 = 1001 positions before the
+# first window reset (a 9-row head would peak at 989)
+C5_HEAD, C5_AUDIO, C5_BACK, C5_STEPS, C5_CHUNKS, C5_CAP, C5_KEEP = 21, 26, 5, 24, 24, 1024, 3
 
 
 def c5_ops(P, m):
@@ -116,7 +120,7 @@ def c5_ops(P, m):
     return head, audio
 
 
-def run_c5(dec, embed, head, audio, forced=None):
+def run_c5(dec, embed, head, audio, forced=None, peak=None):
     """The C5 op list on a decoder (GPU or oracle).  forced: per chunk the
     tokens to feed (teacher forcing); None: the decoder's own greedy tokens.
     Returns per step (token, logits) and the number of window resets."""
@@ -138,6 +142,8 @@ def run_c5(dec, embed, head, audio, forced=None):
         for i in range(C5_STEPS):
             feed = rows[-1] if i == 0 else embed(forced[c][i - 1] if forced else chunk[-1][0])
             chunk.append(dec.step(feed))
+        if peak is not None:
+            peak.append(dec.kv_len())
         out.append(chunk)
         prev = forced[c] if forced else [t for t, _ in chunk]
     return out, resets
@@ -172,24 +178,34 @@ def c5(P, gpu):
     m = P.SynthModel(P.Config(*CFG06_2L), seed=5)
     head, audio = c5_ops(P, m)
     o = _OracleSteps(P.Oracle(m, threads=ORACLE_THREADS))
-    ref, resets = run_c5(o, m.embed, head, audio)
+    peak = []
+    ref, resets = run_c5(o, m.embed, head, audio, peak=peak)
     o.close()
     assert resets >= 1, "the window reset path was not exercised"
+    assert max(peak) > 1000, f"the cache never passed 1000 positions (peak {max(peak)})"
     return m, head, audio, ref
 
 
-@pytest.mark.parametrize("engine", [0, 2])
-def test_c5_streaming_oplist_vs_oracle(qa, c5, engine):
+@pytest.mark.parametrize("path", ["graph", "split", "relay"])
+def test_c5_streaming_oplist_vs_oracle(qa, c5, path):
+    """All three decode paths: the graph engine, the split persistent kernel and
+    the relay persistent kernel (which serves every C5 launch: the positions
+    stay below 1024)."""
     m, head, audio, ref = c5
+    engine = 0 if path == "graph" else 2
     d = _GpuSteps(gpu_decoder(qa, m, C5_CAP + 64, engine))
+    if engine == 2:
+        d.set_relay(path == "relay")
     forced = [[t for t, _ in chunk] for chunk in ref]
     got, resets = run_c5(d, m.embed, head, audio, forced)
     assert resets >= 1 and d.engine() == engine and d.fallbacks() == 0
+    if engine == 2:
+        assert d.last_kernel() == (2 if path == "relay" else 1)
     worst = 0.0
     for c, (gc, rc) in enumerate(zip(got, ref)):
         for i, ((t, lg), (ot, lo)) in enumerate(zip(gc, rc)):
-            worst = max(worst, check_step(lg, lo, t, ot, f"engine {engine} chunk {c} step {i}"))
-    print(f"C5 engine {engine}: {len(audio)} chunks x {C5_STEPS} steps, {resets} window reset(s): "
+            worst = max(worst, check_step(lg, lo, t, ot, f"{path} chunk {c} step {i}"))
+    print(f"C5 {path}: {len(audio)} chunks x {C5_STEPS} steps, {resets} window reset(s), cap {C5_CAP}: "
           f"max |dlogit| {worst:.2e}")
     d.close()
 

@@ -179,6 +179,140 @@ def test_persistent_vs_graph_17b(qa, gpu):
     d.close()
 
 
+def test_relay_kernel_selection(qa, dec06):
+    """The relay kernel runs persistent launches whose positions stay below
+    RELAY_MAX_POS, the split kernel the others and every launch after
+    set_relay(0)."""
+    d, rows = dec06
+    d.set_engine(ENGINE_PERSIST)
+    d.set_kv_len(0)
+    d.prefill(rows[:-1])
+    base = d.kv_len()
+    first = d.forward(rows[-1])
+    assert d.last_kernel() == qa.KERNEL_RELAY
+    d.set_relay(False)
+    d.forward_token(first)
+    assert d.last_kernel() == qa.KERNEL_SPLIT
+    d.set_relay(True)
+    d.set_kv_len(base + 1)
+    extra, _, _ = qa.prompt_rows(qa.preset(0), qa.RELAY_MAX_POS - 3 - (base + 1), 0, seed=11)
+    d.prefill(extra)
+    assert d.kv_len() == qa.RELAY_MAX_POS - 3
+    d.generate(first, 3)                     # positions 1021..1023: still relay
+    assert d.last_kernel() == qa.KERNEL_RELAY
+    d.set_kv_len(qa.RELAY_MAX_POS - 2)
+    d.generate(first, 3)                     # position 1024 is past the relay kernel's LDS splits
+    assert d.last_kernel() == qa.KERNEL_SPLIT
+    assert d.fallbacks() == 0
+
+
+def test_relay_vs_split_teacher_forced_06b(qa, dec06):
+    """The two persistent kernels on the same teacher-forced steps: the same
+    arithmetic (bf16 weights, fp32 sums; the relay kernel's matrix-core
+    products take each fp32 activation as three exact bf16 terms), different
+    summation orders."""
+    d, rows = dec06
+    d.set_engine(ENGINE_PERSIST)
+    d.set_kv_len(0)
+    d.prefill(rows[:-1])
+    base = d.kv_len()
+    teach = [int(t) for t in np.random.default_rng(9).integers(0, 151643, 20)]
+    d.set_relay(False)
+    ts, ls, hs = teacher_run(d, ENGINE_PERSIST, base, rows[-1], teach)
+    assert d.last_kernel() == qa.KERNEL_SPLIT
+    d.set_relay(True)
+    tr, lr, hr = teacher_run(d, ENGINE_PERSIST, base, rows[-1], teach)
+    assert d.last_kernel() == qa.KERNEL_RELAY
+    err, herr = float(np.abs(lr - ls).max()), float(np.abs(hr - hs).max())
+    print(f"relay vs split, {len(teach) + 1} teacher-forced steps: max |dlogit| {err:.2e}, max |dhidden| {herr:.2e}")
+    assert err < AGREE and herr < 1e-3, (err, herr)
+    first_divergence(ts, tr, ls)
+
+
+@pytest.mark.parametrize("relay", [False, True])
+def test_generate_equals_single_steps_both_kernels(qa, dec06, relay):
+    """one launch of n steps == n launches of one step, bit for bit, on each
+    persistent kernel; and the two kernels' greedy continuations agree"""
+    d, rows = dec06
+    d.set_engine(ENGINE_PERSIST)
+    d.set_relay(relay)
+    try:
+        d.set_kv_len(0)
+        d.prefill(rows[:-1])
+        base = d.kv_len()
+        first = d.forward(rows[-1])
+        gen = d.generate(first, 32)
+        assert d.last_kernel() == (qa.KERNEL_RELAY if relay else qa.KERNEL_SPLIT)
+        d.set_kv_len(base + 1)
+        t, steps = first, []
+        for _ in range(32):
+            t = d.forward_token(t)
+            steps.append(t)
+        assert list(gen) == steps
+    finally:
+        d.set_relay(True)
+
+
+@pytest.mark.parametrize("layers", [1, 2, 3])
+def test_relay_short_models(qa, gpu, layers):
+    """Layer counts where one team has no layer (1) or the teams hold unequal
+    counts (3): every block still joins the LM head and the token feedback;
+    against the split kernel, teacher-forced and free-running."""
+    cfg = qa.preset(0)
+    cfg.layers = layers
+    d = qa.Decoder(cfg, 0, 512)
+    d.set_fallback(False)
+    d.load_synthetic(3, 0.02, 0.0)
+    rows, _, _ = qa.prompt_rows(cfg, 60, 4, seed=layers)
+    d.prefill(rows[:-1])
+    base = d.kv_len()
+    teach = [int(t) for t in np.random.default_rng(layers).integers(0, 151643, 6)]
+    d.set_relay(False)
+    ts, ls, _ = teacher_run(d, ENGINE_PERSIST, base, rows[-1], teach)
+    d.set_relay(True)
+    tr, lr, _ = teacher_run(d, ENGINE_PERSIST, base, rows[-1], teach)
+    assert d.last_kernel() == qa.KERNEL_RELAY
+    err = float(np.abs(lr - ls).max())
+    assert err < AGREE, err
+    first_divergence(ts, tr, ls)
+    out = {}
+    for relay in (False, True):
+        d.set_relay(relay)
+        d.set_kv_len(base + 1)
+        out[relay] = list(d.generate(int(ts[0]), 24))
+    assert out[False] == out[True], f"{layers} layers: free runs differ"
+    assert d.fallbacks() == 0
+    d.close()
+
+
+def test_relay_trace_layout(qa, dec06):
+    """read_trace after a relay launch: 704 words per block in the relay
+    layout; each block stamped its own team's layers and the LM head."""
+    d, rows = dec06
+    d.set_engine(ENGINE_PERSIST)
+    d.set_kv_len(0)
+    d.prefill(rows[:-1])
+    first = d.forward(rows[-1])
+    d.set_trace(2)
+    try:
+        d.generate(first, 4)
+    finally:
+        d.set_trace(-1)
+    assert d.last_kernel() == qa.KERNEL_RELAY
+    tr = d.read_trace().astype(np.int64)
+    L, TM = 28, 24
+    assert tr.shape == (256, 704)
+    team0 = tr[:, 0] > 0                  # layer 0's first stamp: team 0 blocks
+    team1 = tr[:, TM] > 0                 # layer 1's
+    assert team0.sum() == 128 and team1.sum() == 128 and not np.any(team0 & team1)
+    for l in range(L):
+        own = team0 if l % 2 == 0 else team1
+        assert np.all(tr[own, TM * l + 19] > 0) and np.all(tr[~own, TM * l + 19] == 0), l
+        assert np.all(tr[own, TM * l + 19] >= tr[own, TM * l + 4])     # down stored after Q stored
+    assert np.all(tr[:, TM * L + 3] > 0)                               # every block's LM candidate
+    assert np.all(tr[team0, TM * L + 4] > 0) and np.all(tr[team1, TM * L + 4] == 0)
+
+
 def test_engine_errors(qa, gpu):
     """set_engine range check; the persistent engine is refused for shapes it
     does not cover (the tiny test model) and the decoder stays usable."""
