@@ -427,10 +427,14 @@ int qwen_hip_linear_nobias_bf16(float *y, const float *x, const uint16_t *W_bf16
  * kernels and results, but it never allocates or frees memory and never
  * synchronises; it only enqueues on s.  Its temporary memory is one fixed
  * per-GPU device array of qwen_hip_linear_noalloc_max_bytes() bytes (32 MiB),
- * held from library load to process exit.  A call whose seq > 1 product
- * needs more (about 4*seq*in bytes, plus split-K partials for small products)
- * returns QWEN_HIP_EINVAL.  All calls on one GPU share that array: calls
- * whose kernels overlap in time on one GPU race, so order them (one stream). */
+ * held from library load to process exit.  A seq > 1 call needs 4*seq*in
+ * bytes (the bf16 hi and lo halves of x, rounded up to 256), plus
+ * 4*nsplit*seq*out bytes of split-K partials where the product splits K: only
+ * products with fewer than 256 output tiles of 128 columns (32 rows for
+ * seq <= 32, 64 up to 512 rows, 128 above) and an even out do, with nsplit at
+ * most 16.  A call needing more than the array returns QWEN_HIP_EINVAL.  All
+ * calls on one GPU share that array: calls whose kernels overlap in time on
+ * one GPU race, so order them (one stream). */
 int qwen_hip_linear_nobias_bf16_noalloc(float *y, const float *x, const uint16_t *W_bf16,
                                         int seq_len, int in_dim, int out_dim, hipStream_t s);
 size_t qwen_hip_linear_noalloc_max_bytes(void);

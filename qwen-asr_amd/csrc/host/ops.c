@@ -70,11 +70,15 @@ int qwen_hip_swiglu_multiply(float *out, const float *gu, int S, int inter, hipS
     return qk_swiglu_launch(out, gu, S, inter, s);
 }
 
-/* Plan of the seq > 1 product: tiling as qk_gemm_plan_for, except that an odd
- * output width keeps one split (the split-K reduce works on column pairs). */
+/* Plan of the seq > 1 product: tiling as qk_gemm_plan_for, except that one
+ * split is kept where the output tiles alone number QK_GEMM_TARGET or more
+ * (they fill the chip, and the partials of a split plan would be at least
+ * 2 x seq x out floats) and where the output width is odd (the split-K reduce
+ * works on column pairs).  So the op splits K only for small tile grids. */
 static void linear_plan(int S, int in_dim, int out_dim, qk_gemm_plan *p) {
     qk_gemm_plan_for(S, out_dim, in_dim, p);
-    if (p->nsplit > 1 && (out_dim & 1)) {
+    const long tiles = (long)((S + p->bm - 1) / p->bm) * ((out_dim + p->bn - 1) / p->bn);
+    if (p->nsplit > 1 && ((out_dim & 1) || tiles >= QK_GEMM_TARGET)) {
         p->kc = ((in_dim + 63) / 64) * 64;
         p->nsplit = 1;
     }

@@ -309,9 +309,15 @@ int qk_rmsnorm_split_launch(float *x, const float *part, int nsum, long pstride,
 enum { QK_GEMM_STORE = 0, QK_GEMM_ADD = 1, QK_GEMM_SWIGLU = 2, QK_GEMM_ROPE = 3 /* plans only */ };
 /* Tiling of one M x N x K product: block rows bm x columns bn (32 / 64 x
  * QK_GEMM_BN on the LDS ring of nst stages, 128 x QK_GEMM_BN on a 3-stage
- * ring for SwiGLU products above 512 rows, 32 / 64 / 128 x QK_GEMM_BN
- * register-staged (nst 0), or 128 / 256 x 256 for large M), and nsplit slices
- * of kc (a multiple of 64) along K so a launch has enough blocks. */
+ * ring for STORE and SwiGLU products above 512 rows, 32 / 64 / 128 x
+ * QK_GEMM_BN register-staged (nst 0), or 128 / 256 x 256 for large M), and
+ * nsplit slices of kc (a multiple of 64) along K so a launch has enough
+ * blocks.  Split rule on the ring: about QK_GEMM_RING_TARGET blocks, and two
+ * splits at least for k walks of QK_GEMM_RING_KSPLIT or more; a STORE product
+ * on the 128 x 128 tiles takes two splits per 4096 of K whatever its grid; a
+ * SwiGLU product and a Q|K|V product with the RoPE epilogue split only to
+ * fill the chip.  The op-level linear (qwen_hip_linear_nobias_bf16) keeps one
+ * split where its output tiles alone number QK_GEMM_TARGET or more. */
 #define QK_GEMM_BN 128
 #define QK_GEMM_TARGET 256
 #define QK_GEMM_MAX_SPLIT 16

@@ -148,3 +148,31 @@ def test_rope_launches_refuse_unaligned_pointers(qa, field):
     if field != "qkv":               # the fused kernel reads the product from its own tiles
         p = GemmPlan(64, 1, 1024, 128, 4)
         assert lib.qk_gemm_rope_launch(base, base, base, 64, 1024, C.byref(p), C.byref(bad), None) == -1
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_linear_op_workspace(qa, M, N, K):
+    """The op-level linear (qwen_hip_linear_nobias_bf16 and its no-alloc
+    variant) splits K only where its output tiles number fewer than 256 and
+    the width is even: its workspace is the bf16 hi/lo halves of x (4*M*K
+    bytes, rounded up to 256) plus, for such small grids only, the split-K
+    partials.  A 1024-row product into 4096 columns therefore fits the
+    no-alloc entry point's 32 MiB array (4 MiB of x halves, no partials)."""
+    lib = qa.lib()
+    lib.qk_linear_ws_bytes.restype = C.c_size_t
+    p = GemmPlan()
+    lib.qk_gemm_plan_for(M, N, K, C.byref(p))
+    tiles = -(-M // p.bm) * -(-N // p.bn)
+    halves = -(-4 * M * K // 256) * 256
+    need = lib.qk_linear_ws_bytes(M, K, N)
+    if tiles >= 256 or N % 2 or p.nsplit == 1:
+        assert need == halves
+    else:
+        assert need == halves + 4 * p.nsplit * M * N
+
+
+def test_linear_op_workspace_advice_case(qa):
+    lib = qa.lib()
+    lib.qk_linear_ws_bytes.restype = C.c_size_t
+    assert lib.qk_linear_ws_bytes(1024, 1024, 4096) == 4 * 1024 * 1024      # x halves only
+    assert lib.qk_linear_ws_bytes(1024, 1024, 4096) <= lib.qwen_hip_linear_noalloc_max_bytes()
