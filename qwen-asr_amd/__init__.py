@@ -492,8 +492,8 @@ class Decoder:
         check(lib().qwen_hip_decoder_set_trace(self.h, int(step)), "set_trace")
 
     def read_trace(self):
-        """Wall-clock stamps (100 MHz) of the traced step: [256 blocks][704] for the
-        split kernel, [256 blocks][512] for the relay kernel (see last_kernel)."""
+        """Wall-clock stamps (100 MHz) of the traced step: [256 blocks][704] in the
+        layout of the kernel that ran (see last_kernel and the header)."""
         out = np.zeros((256, 704), np.uint64)
         words = check(lib().qwen_hip_decoder_read_trace(self.h, _ptr(out), out.size), "read_trace")
         return out.reshape(-1)[:256 * words].reshape(256, words).copy()
@@ -573,3 +573,56 @@ class Stream:
             self.close()
         except Exception:
             pass
+
+
+# Intervals of the relay kernel's per-layer trace (words 24 l + i, header
+# layout): name, first stamp, last stamp.  Each is the median over the blocks of
+# the team that computes the layer.
+RELAY_STAGES = (
+    ("input: residual gathered, planes written", 1, 3),
+    ("Q product stored", 3, 4),
+    ("hop Q -> attention (512 words)", 4, 5),
+    ("attention: q/k norm + RoPE + fold", 5, 7),
+    ("attention: merge of 16 groups, partials stored", 7, 8),
+    ("hop split partials -> merge slices", 8, 9),
+    ("merge over the splits, stored", 9, 10),
+    ("hop merged dims -> every block (256 words)", 10, 11),
+    ("O product stored", 11, 12),
+    ("hop O partials: cross-XCD half in", 12, 13),
+    ("post-attention residual gathered, planes written", 13, 15),
+    ("gate|up products reduced", 15, 16),
+    ("SwiGLU stored", 16, 17),
+    ("hop SwiGLU -> down (384 words)", 17, 18),
+    ("down product stored", 18, 19),
+)
+
+
+def relay_stage_us(tr, layers):
+    """Per-layer stage times (microseconds) of one traced relay step: the median
+    over layers 2 .. layers-3 of each stage's median over the computing team's
+    blocks; plus the hand-over between layers (the last block's down store of
+    layer l-1 to the median block's cross-XCD half of layer l's input), the
+    layer period, and the LM head (rows of the median / slowest block).  tr is
+    read_trace()'s [256][704] array of 100 MHz stamps."""
+    tr = np.asarray(tr).astype(np.int64)
+    TM = 24
+    t = (tr - tr[tr > 0].min()) * 0.01
+    out = {}
+    ls = list(range(2, layers - 2))
+    for name, a, b in RELAY_STAGES:
+        v = [np.median(t[tr[:, TM * l] > 0, TM * l + b] - t[tr[:, TM * l] > 0, TM * l + a]) for l in ls]
+        out[name] = round(float(np.mean(v)), 3)
+    hx, per = [], []
+    for l in ls:
+        cb, pb, nb = tr[:, TM * l] > 0, tr[:, TM * (l - 1)] > 0, tr[:, TM * (l + 1)] > 0
+        hx.append(np.median(t[cb, TM * l + 1]) - t[pb, TM * (l - 1) + 19].max())
+        per.append(np.median(t[nb, TM * (l + 1) + 3]) - np.median(t[cb, TM * l + 3]))
+    out["hop between layers: last down store -> cross-XCD half of the input in"] = round(float(np.mean(hx)), 3)
+    out["layer period"] = round(float(np.mean(per)), 3)
+    blk = tr[:, TM * layers] > 0
+    lm = t[blk, TM * layers + 3] - t[blk, TM * layers + 2]
+    out["LM head rows: median block"] = round(float(np.median(lm)), 3)
+    out["LM head rows: slowest block"] = round(float(np.max(lm)), 3)
+    tb = tr[:, TM * layers + 4] > 0
+    out["token: last candidate -> median token"] = round(float(np.median(t[tb, TM * layers + 4]) - t[blk, TM * layers + 3].max()), 3)
+    return out
