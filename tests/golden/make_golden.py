@@ -92,11 +92,35 @@ def free_run(name, cfg, n_audio, n_ids, n_forwards):
                  "forwards": n_forwards, "prefill_s": round(tp, 2), "total_s": round(time.time() - t0, 1)})
 
 
+def logits_run(name, cfg, n_audio, n_ids, n_forwards):
+    """Full fp32 logits (every vocabulary row) of the first n_forwards greedy
+    forwards of fixture `name`'s run, written to {name}_logits.npz beside the
+    top-8 fixture (same model, rows and step convention as free_run)."""
+    t0 = time.time()
+    m = P.SynthModel(cfg, seed=0)
+    rows, ids = P.prompt_rows(m, n_audio, n_ids)
+    r = P.RefModel(m, threads=1)
+    r.prefill(rows[:-1])
+    x = rows[-1]
+    toks, logits = [], []
+    for i in range(n_forwards):
+        t, lg, _ = r.forward(x, True)
+        toks.append(t); logits.append(lg.astype(np.float32))
+        x = r.embed(t)
+    np.savez_compressed(os.path.join(HERE, f"{name}_logits.npz"), ids=ids, tokens=np.array(toks, np.int32),
+                        logits=np.array(logits), emb_checksum=np.uint64(P.checksum_u16(m.emb)),
+                        n_audio=np.int32(n_audio), n_ids=np.int32(n_ids))
+    return meta({"config": f"{name}_logits", "hidden": cfg.hidden, "prefill_rows": int(rows.shape[0] - 1),
+                 "forwards": n_forwards, "total_s": round(time.time() - t0, 1)})
+
+
 FIXTURES = {
     "tiny_teacher": tiny_teacher,
     "c1_short": lambda: free_run("c1_short", P.CFG_06B, 40, 12, 17),
     "c1_full": lambda: free_run("c1_full", P.CFG_06B, 390, 12, 128),
     "c3_short": lambda: free_run("c3_short", P.CFG_17B, 30, 16, 9),
+    "c1_full_logits": lambda: logits_run("c1_full", P.CFG_06B, 390, 12, 4),
+    "c3_short_logits": lambda: logits_run("c3_short", P.CFG_17B, 30, 16, 4),
 }
 
 

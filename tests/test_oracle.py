@@ -301,6 +301,25 @@ def test_oracle_matches_reference_golden_full_shape(P, name, cfg_name, n_audio, 
         x = o.embed(t)
 
 
+@pytest.mark.parametrize("name,cfg_name", [("c1_full", "CFG_06B"), ("c3_short", "CFG_17B")])
+def test_oracle_matches_reference_full_logits(P, name, cfg_name):
+    """Every vocabulary row's logit of the reference's first forwards
+    (tests/golden/*_logits.npz) against the oracle's."""
+    g = np.load(os.path.join(GOLD, f"{name}_logits.npz"))
+    m = P.SynthModel(getattr(P, cfg_name), seed=0)
+    assert P.checksum_u16(m.emb) == int(g["emb_checksum"])
+    rows, ids = P.prompt_rows(m, int(g["n_audio"]), int(g["n_ids"]))
+    assert np.array_equal(ids, g["ids"])
+    o = P.Oracle(m)
+    o.prefill(rows[:-1])
+    x = rows[-1]
+    for i, ref in enumerate(g["logits"]):
+        t, lg, _ = o.forward(x, True)
+        np.testing.assert_allclose(lg, ref, atol=1e-4, rtol=0)
+        assert t == g["tokens"][i]
+        x = o.embed(t)
+
+
 def test_oracle_prefill_split_and_rollback(P):
     """prefill(n) == prefill(k) + prefill(n-k); forwards row by row == prefill;
     truncating the KV and re-prefilling reproduces the same logits."""
