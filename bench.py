@@ -79,7 +79,8 @@ def pmc_pass(counter, workload, timeout=150, extra=None):
         return None
     out = tempfile.mkdtemp(prefix="qk_pmc_")
     cmd = [exe, "--pmc", counter, "-d", out, "-o", "run", "--output-format", "csv", "--",
-           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--no-c3", "--steps", str(PMC_STEPS),
+           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--no-c3", "--no-stages",
+           "--steps", str(PMC_STEPS),
            "--warmup", "2", "--calib-copy-mb", "256", "--workload", workload] + list(extra or [])
     env = dict(os.environ, TMPDIR="/tmp")
     errlog = os.path.join(out, "child.err")
@@ -128,11 +129,48 @@ def pmc_pass(counter, workload, timeout=150, extra=None):
         shutil.rmtree(out, ignore_errors=True)
 
 
+def kernel_trace_pass(args_list, timeout=300):
+    """One child run of this script under rocprofv3 --kernel-trace; returns the
+    (kernel name, duration in us) of every dispatch in dispatch order, or None."""
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        return None
+    out = tempfile.mkdtemp(prefix="qk_kt_")
+    cmd = [exe, "--kernel-trace", "-d", out, "-o", "run", "--output-format", "csv", "--",
+           sys.executable, os.path.abspath(__file__)] + list(args_list)
+    try:
+        with open(os.path.join(out, "child.err"), "w") as ef:
+            p = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
+                                 stderr=ef, start_new_session=True)
+            try:
+                rc = p.wait(timeout=timeout)
+            except subprocess.TimeoutExpired:
+                os.killpg(p.pid, 9)
+                p.wait()
+                rc = "timeout"
+        files = glob.glob(os.path.join(out, "**", "*kernel_trace.csv"), recursive=True)
+        if rc != 0 or not files:
+            log(f"[gpu] rocprofv3 --kernel-trace pass: exit {rc}, {len(files)} trace files")
+            return None
+        rows = [(int(r["Dispatch_Id"]), r["Kernel_Name"],
+                 (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3) for r in csv.DictReader(open(files[0]))]
+        return [(n, d) for _, n, d in sorted(rows)]
+    except (subprocess.SubprocessError, OSError, KeyError, ValueError):
+        return None
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
+C2_TRACE_REPS = 40
 C2_SHAPES = [(2048, 1024), (1024, 2048), (6144, 1024), (1024, 3072), (151936, 1024), (4096, 2048),
              (2048, 4096), (12288, 2048), (2048, 6144), (151936, 2048), (2048, 2048)]
 
 
-def run_gemv_sweep(qa, threads, with_cpu):
+def c2_copies(wbytes):
+    return max(4, -(-(1 << 30) // wbytes))
+
+
+def run_gemv_sweep(qa, threads, with_cpu, trace_reps=0):
     """C2: y = W x for each (rows, cols), W bf16 N(0, 0.02), x U[-1, 1].  GPU:
     the op-level GEMV (qwen_hip_linear_nobias_bf16 at seq 1, the reference's
     qwen_linear_nobias_bf16 decode path, qwen_asr_kernels.c:462-466), timed
@@ -155,7 +193,7 @@ def run_gemv_sweep(qa, threads, with_cpu):
         W = qa.synth_bf16(R * Cc, 0, 9000 + R + Cc).reshape(R, Cc)
         x = qa.synth_uniform(Cc, 0, 9100 + Cc)
         wbytes = 2 * R * Cc
-        copies = max(4, -(-(1 << 30) // wbytes))
+        copies = c2_copies(wbytes)
         dW0 = torch.from_numpy(W.view(np.int16)).to("cuda")
         dWs = [dW0] + [dW0.clone() for _ in range(copies - 1)]
         dx = torch.from_numpy(x).to("cuda")
@@ -164,7 +202,7 @@ def run_gemv_sweep(qa, threads, with_cpu):
         call = lambda w: lib.qwen_hip_linear_nobias_bf16(dy.data_ptr(), dx.data_ptr(), w.data_ptr(), 1, Cc, R, None)
         for i in range(copies):
             qa.check(call(dWs[i]), "gemv")
-        reps = max(copies * 4, min(400, int(4e9 // wbytes)))
+        reps = trace_reps or max(copies * 4, min(400, int(4e9 // wbytes)))
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -395,6 +433,87 @@ REF_BLAS = ("none: the reference's BLAS build (Makefile:47-48, cblas_sgemm in qw
             "(qwen_asr_kernels.c:211-222) and its decode (seq 1, never BLAS) is unaffected")
 
 
+def cpu_prefill_blas(P, r, m, pre, threads):
+    """The reference's BLAS-build prefill (make blas: USE_BLAS, cblas_sgemm,
+    Makefile:47-48), composed on this host because that build needs cblas.h,
+    which the image lacks: qwen_decoder_prefill's operator sequence
+    (qwen_asr_decoder.c:262-359) over the same rows, with the reference's own
+    compiled operators (oracle/_ref: rms_norm, per-head norm, RoPE, causal
+    attention, SwiGLU, residual adds) and, for each qwen_linear_nobias_bf16,
+    what its BLAS path does (qwen_asr_kernels.c:196-202, :320-330): widen the
+    bf16 weight to fp32 (the reference's loop, one thread) and one sgemm,
+    here OpenBLAS (numpy's bundled scipy-openblas: the library family the
+    reference's Linux BLAS build links) on `threads` threads.  Returns the
+    seconds per part; None if a piece is missing."""
+    import ctypes as C
+    import numpy as np
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:
+        return None
+    lib, c = r.lib, m.cfg
+    fp = C.POINTER(C.c_float)
+    f = lambda a: a.ctypes.data_as(fp)
+    for n_, at in (("qwen_rms_norm", [fp, fp, fp, C.c_int, C.c_int, C.c_float]),
+                   ("qwen_rms_norm_per_head", [fp, fp, C.c_int, C.c_int, C.c_int, C.c_float]),
+                   ("qwen_apply_rope_neox", [fp, fp, fp, C.c_int, C.c_int, C.c_int]),
+                   ("qwen_causal_attention", [fp, fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                              C.c_float, C.c_int]),
+                   ("qwen_swiglu_multiply", [fp, fp, C.c_int, C.c_int]),
+                   ("qwen_add_inplace", [fp, fp, C.c_int])):
+        getattr(lib, n_).argtypes = at
+        getattr(lib, n_).restype = None
+    S, D, H, KV, HD, I = pre.shape[0], c.hidden, c.heads, c.kv_heads, c.head_dim, c.intermediate
+    qd, kvd = H * HD, KV * HD
+    x = np.ascontiguousarray(pre, np.float32).copy()
+    xn, q, k, v = (np.empty((S, n), np.float32) for n in (D, qd, kvd, kvd))
+    att, proj, gu, gate, ffn = (np.empty((S, n), np.float32) for n in (qd, D, 2 * I, I, D))
+    inv = 1.0 / np.power(c.theta, np.arange(0, HD, 2, dtype=np.float64) / HD)
+    ang = np.arange(S, dtype=np.float64)[:, None] * inv[None]
+    cs = np.ascontiguousarray(np.concatenate([np.cos(ang)] * 2, 1), np.float32)
+    sn = np.ascontiguousarray(np.concatenate([np.sin(ang)] * 2, 1), np.float32)
+    wide = np.empty(max(2 * I * D, qd * D, D * I), np.float32)
+    t = {"widen": 0.0, "sgemm": 0.0, "other": 0.0}
+
+    def linear(y, xin, w16):
+        out_dim, in_dim = w16.shape
+        n = out_dim * in_dim
+        t0 = time.perf_counter()
+        lib.ref_bf16_widen(wide.ctypes.data, w16.ctypes.data, n)
+        t1 = time.perf_counter()
+        np.matmul(xin, wide[:n].reshape(out_dim, in_dim).T, out=y)
+        t["widen"] += t1 - t0
+        t["sgemm"] += time.perf_counter() - t1
+
+    def op(fn, *a):
+        t0 = time.perf_counter()
+        fn(*a)
+        t["other"] += time.perf_counter() - t0
+
+    with threadpool_limits(threads, user_api="blas"):
+        for l in range(c.layers):
+            L = m.layers[l]
+            gu16 = np.empty((2 * I, D), np.uint16)          # the loader's gate/up interleave (:95-107)
+            gu16[0::2], gu16[1::2] = L[P.GATE], L[P.UP]
+            op(lib.qwen_rms_norm, f(xn), f(x), f(L[P.INNORM]), S, D, c.eps)
+            linear(q, xn, L[P.WQ])
+            linear(k, xn, L[P.WK])
+            linear(v, xn, L[P.WV])
+            op(lib.qwen_rms_norm_per_head, f(q), f(L[P.QNORM]), S, H, HD, c.eps)
+            op(lib.qwen_rms_norm_per_head, f(k), f(L[P.KNORM]), S, KV, HD, c.eps)
+            op(lib.qwen_apply_rope_neox, f(q), f(cs), f(sn), S, H, HD)
+            op(lib.qwen_apply_rope_neox, f(k), f(cs), f(sn), S, KV, HD)
+            op(lib.qwen_causal_attention, f(att), f(q), f(k), f(v), S, S, H, KV, HD, 1.0 / np.sqrt(HD), 0)
+            linear(proj, att, L[P.WO])
+            op(lib.qwen_add_inplace, f(x), f(proj), S * D)
+            op(lib.qwen_rms_norm, f(xn), f(x), f(L[P.POSTNORM]), S, D, c.eps)
+            linear(gu, xn, gu16)
+            op(lib.qwen_swiglu_multiply, f(gate), f(gu), S, I)
+            linear(ffn, gate, L[P.DOWN])
+            op(lib.qwen_add_inplace, f(x), f(ffn), S * D)
+    return t
+
+
 def cpu_baseline(wl, rows, first_token, threads, decode_steps):
     """Reference decoder (oracle/_ref) on this host: prefill of the same rows
     and `decode_steps` greedy forwards from the same first token on `threads`
@@ -425,13 +544,40 @@ def cpu_baseline(wl, rows, first_token, threads, decode_steps):
     r.lib.ref_set_threads(1)
     toks1, td1 = r.generate(first_token, CPU_1T_STEPS)
     r.lib.ref_set_threads(threads)
+    at_gpu = None
+    if sampled:
+        # the same number of decode steps at the GPU's positions (n + 1 ..): the
+        # cache is extended with zero rows, so the attention walks the GPU's
+        # context length (its cost depends on the length only); tokens not compared
+        r.extend_kv(n + 1, last)
+        _, tdg = r.generate(first_token, decode_steps)
+        at_gpu = decode_steps / tdg
+        log(f"[cpu] {decode_steps} decode steps at positions {n + 1}+: {tdg:.2f}s ({at_gpu:.2f} tok/s)")
+    blas = cpu_prefill_blas(P, r, m, pre, threads)
     host = P.host_info()
     bw = P.stream_gbs(threads)
     bw1 = P.stream_gbs(1)
     log(f"[cpu] prefill {tp:.1f}s, {decode_steps} decode steps {td:.2f}s (first token {tok}); 1 thread: "
         f"{CPU_1T_STEPS} steps {td1:.2f}s; triad {bw:.1f} GB/s ({threads} thr), {bw1:.1f} GB/s (1 thr); {host}")
-    return {"value": round(decode_steps / td, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+    pb = None
+    if blas:
+        tb = sum(blas.values())
+        log(f"[cpu] BLAS-path prefill estimate {pre.shape[0]} rows: {tb:.2f}s "
+            + ", ".join(f"{k} {v:.2f}s" for k, v in blas.items()))
+        pb = {"tok_s": round(pre.shape[0] / tb, 2), "rows": int(pre.shape[0]), "cores": threads,
+              "kind": "composed",
+              "seconds": {k: round(v, 3) for k, v in blas.items()},
+              "what": "the reference's BLAS-build prefill (make blas) composed from its parts: qwen_decoder_prefill's "
+                      "operator sequence (qwen_asr_decoder.c:262-359) with the reference's own compiled operators "
+                      "(oracle/_ref) for norms, RoPE, attention, SwiGLU and adds, and per linear its BLAS path "
+                      "(qwen_asr_kernels.c:196-202, :320-330): the reference's bf16 -> fp32 widening on one thread, "
+                      "then one OpenBLAS sgemm (numpy's bundled scipy-openblas) on the same threads; the build itself "
+                      "needs cblas.h, which the image lacks"}
+    dec_value = at_gpu if sampled else decode_steps / td
+    return {"value": round(dec_value, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "at_sample_context": round(decode_steps / td, 3) if sampled else None,
             "prefill_tok_s": round(pre.shape[0] / tp, 2),
+            "prefill_blas": pb,
             "one_thread": {"value": round(CPU_1T_STEPS / td1, 3), "unit": "tok/s", "cores": 1,
                            "steps": CPU_1T_STEPS,
                            "same_tokens": bool(list(toks1[:len(toks)]) == list(toks[:len(toks1)]))},
@@ -439,10 +585,13 @@ def cpu_baseline(wl, rows, first_token, threads, decode_steps):
             "host_triad_gb_s": {str(threads): round(bw, 1), "1": round(bw1, 1)},
             "blas": REF_BLAS,
             "sample": (f"reference decoder (oracle/_ref, no BLAS) on the same weights/rows: prefill "
-                       f"{pre.shape[0]} rows" + (f" (the first {pre.shape[0]} of the {n}: a bounded sample, so its decode "
-                                                  f"steps run at {pre.shape[0] + 1}+ positions against the GPU's {n + 1}+)"
-                                                  if sampled else "") +
-                       f", then {decode_steps} greedy decode steps; decode tok/s over those steps"),
+                       f"{pre.shape[0]} rows" + (f" (the first {pre.shape[0]} of the {n}: a bounded sample), "
+                                                  f"{decode_steps} greedy decode steps after it (at_sample_context), "
+                                                  f"then {decode_steps} more at the GPU's positions {n + 1}+ with the "
+                                                  f"KV cache extended by zero rows (value; tokens not compared)"
+                                                  if sampled else
+                                                  f", then {decode_steps} greedy decode steps; decode tok/s over "
+                                                  f"those steps")),
             "first_token_matches_gpu": None if sampled else bool(tok == first_token)}
 
 
@@ -529,6 +678,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c3", action="store_true", help="default (C1) line: skip the 1.7B decode block")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc child runs")
+    ap.add_argument("--c2-trace-reps", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--no-stages", action="store_true",
+                    help="skip the relay kernel's stage-trace launch (the counter passes read the last launch)")
     ap.add_argument("--cpu-steps", type=int, default=48)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="before timing, run one copy kernel (torch.mul by 1) over this many MiB: a "
@@ -546,7 +698,27 @@ def main():
     cfg = qa.preset(wl["model_b"])
     if args.workload == "c2":
         threads = min(os.cpu_count() or 1, 16)
+        if args.c2_trace_reps:          # the kernel-trace child: timed launches only
+            run_gemv_sweep(qa, threads, False, args.c2_trace_reps)
+            return
         rows = run_gemv_sweep(qa, threads, not args.no_cpu)
+        kt = None if args.no_traffic else kernel_trace_pass(
+            ["--workload", "c2", "--no-cpu", "--no-traffic", "--c2-trace-reps", str(C2_TRACE_REPS)])
+        if kt:
+            # each shape: its warm-up launch per weight copy, then the timed launches
+            gv = [d for n, d in kt if n.startswith(("void gemv_kernel", "void gemv_ks"))]
+            i = 0
+            for r in rows:
+                i += c2_copies(2 * r["rows"] * r["cols"])
+                durs = sorted(gv[i:i + C2_TRACE_REPS])
+                i += C2_TRACE_REPS
+                if len(durs) == C2_TRACE_REPS:
+                    kus = durs[len(durs) // 2]
+                    r["kernel_us"] = round(kus, 3)
+                    r["kernel_gb_s"] = round(r["bytes"] / (kus * 1e-6) / 1e9, 1)
+                    r["kernel_frac"] = round(r["kernel_gb_s"] / HBM_PEAK_GBS, 4)
+                    log(f"[gpu] gemv {r['rows']}x{r['cols']}: kernel {kus:.2f} us ({r['kernel_gb_s']:.0f} GB/s, "
+                        f"{r['kernel_frac'] * 100:.1f}% of 8 TB/s)")
         tot_b = sum(r["bytes"] for r in rows)
         tot_us = sum(r["us"] for r in rows)
         big = max(rows, key=lambda r: r["bytes"])
@@ -567,7 +739,12 @@ def main():
             "roofline": {"bound": "hbm", "achieved": big["gb_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": big["frac"], "traffic": None,
                          "kernel": f"gemv {big['rows']}x{big['cols']} (largest shape)"},
-            "per_shape": rows, "lm_head_shard_share": shard, "cpu_baseline": cpu}), flush=True)
+            "per_shape": rows,
+            "per_shape_note": "us / gb_s / frac: HIP events over back-to-back eager launches (launch gaps "
+                              "included); kernel_us / kernel_gb_s / kernel_frac: the median rocprofv3 kernel-trace "
+                              f"duration of {C2_TRACE_REPS} launches per shape in a child run (cold weights, the "
+                              "kernel alone)",
+            "lm_head_shard_share": shard, "cpu_baseline": cpu}), flush=True)
         return
     if args.workload == "enc":
         run_encoder(qa, args, wl)
@@ -656,7 +833,7 @@ def main():
     engine = d.engine()
     kernel = d.last_kernel() if engine == 2 else 0
     stages = None
-    if kernel == qa.KERNEL_RELAY:
+    if kernel == qa.KERNEL_RELAY and not args.no_stages:
         # the kernel's own stage stamps for one step (step 6 of a 10-step launch
         # from the same position; outside the timed region)
         d.set_kv_len(base)

@@ -44,11 +44,16 @@ __device__ __forceinline__ void gemv_load(uint4 (&w)[ROWS][NC], const uint16_t *
     }
 }
 
-template <int NC, int ROWS, int EPI>
-__global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
+// MERGE: the input is merged from attention splits (the O projection);
+// only the argmax epilogue walks several row groups per wave (iters), so the
+// other instances hold no second weight buffer and no merge registers.
+template <int NC, int ROWS, int EPI, bool MERGE>
+__global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters_arg) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int K = a.K, R = a.rows;
+    constexpr bool LOOP = EPI == QK_EPI_ARGMAX;
+    const int iters = LOOP ? iters_arg : 1;
 
     // The first rows' weights do not depend on the input row: issue their
     // loads before the prologue so HBM latency overlaps the gather / norm.
@@ -61,7 +66,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
     float xr[NC][8];
     int tok = -1;
     if (a.tok) tok = *a.tok;
-    if (a.merge_o) {
+    if constexpr (MERGE) {
         // The input is the attention output, merged here from its position
         // splits (m, l, o): x = (sum_s o_s e^(m_s - M)) * (1 / sum_s l_s e^(m_s - M)).
         // Thread t merges columns [8t, 8t + 8) into LDS for the whole block.
@@ -180,7 +185,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
     for (int it = 0; it < iters; it++) {
         if (rbase >= R) break;
         const int rnext = rbase + 4 * ROWS;
-        const bool more = (it + 1 < iters) && (rnext < R);
+        const bool more = LOOP && (it + 1 < iters) && (rnext < R);
         uint4 wn[ROWS][NC];
         if (more) gemv_load<NC, ROWS>(wn, a.W, R, K, rnext, lane);
 
@@ -242,6 +247,85 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters) {
     }
 }
 
+// Long rows (STORE or ADD, plain x; gemv_ks_fits): the block's four waves split
+// each row's 512-column chunks (wave w takes chunks w, w + 4, w + 8, ...) for
+// the block's ROWS rows, so x is held once per block instead of once per wave
+// and a wave needs a quarter of the registers; the four partial sums of a row
+// meet in LDS and are added in wave order.
+template <int NCW, int ROWS, int EPI>
+__global__ __launch_bounds__(256) void gemv_ks(qk_gemv_args a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = a.K, R = a.rows;
+    const int r0 = blockIdx.x * ROWS;
+    uint4 w[ROWS][NCW];
+#pragma unroll
+    for (int j = 0; j < ROWS; j++)
+#pragma unroll
+        for (int c = 0; c < NCW; c++) {
+            const int col = (wave + 4 * c) * 512 + lane * 8, r = r0 + j;
+            w[j][c] = (r < R && col < K) ? ld_stream16(a.W + (size_t)r * K + col) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    float resid = 0.0f;
+    if (EPI == QK_EPI_ADD && threadIdx.x < ROWS && r0 + (int)threadIdx.x < R) resid = a.y[r0 + threadIdx.x];
+    float xr[NCW][8];
+#pragma unroll
+    for (int c = 0; c < NCW; c++) {
+        const int col = (wave + 4 * c) * 512 + lane * 8;
+        if (col < K) {
+            const float4 p0 = *reinterpret_cast<const float4 *>(a.x + col);
+            const float4 p1 = *reinterpret_cast<const float4 *>(a.x + col + 4);
+            xr[c][0] = p0.x; xr[c][1] = p0.y; xr[c][2] = p0.z; xr[c][3] = p0.w;
+            xr[c][4] = p1.x; xr[c][5] = p1.y; xr[c][6] = p1.z; xr[c][7] = p1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) xr[c][j] = 0.0f;
+        }
+    }
+    float acc[ROWS];
+#pragma unroll
+    for (int j = 0; j < ROWS; j++) {
+        acc[j] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCW; c++) acc[j] = dot8_bf16(w[j][c], xr[c], acc[j]);
+    }
+    reduce_rows<ROWS, 1>(acc, lane);            // lane l: row l / (64 / ROWS)
+    __shared__ float part[4][ROWS];
+    constexpr int span = 64 / ROWS;
+    if (lane % span == 0) part[wave][lane / span] = acc[0];
+    __syncthreads();
+    if (threadIdx.x < ROWS) {
+        const int t = threadIdx.x, r = r0 + t;
+        if (r < R) {
+            const float v = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
+            a.y[r] = EPI == QK_EPI_ADD ? resid + v : v;
+        }
+    }
+}
+
+// gemv_ks takes the product: a plain input row, STORE or ADD, rows longer
+// than 2048 columns, or of 2048 columns with 4096 rows or more (measured,
+// cold weights, eager launches: 2048 x 6144 7.07 -> 6.25 us, 12288 x 2048
+// 9.97 -> 9.14 us; 2048 x 2048 3.59 -> 3.78 us, so not below 4096 rows)
+static bool gemv_ks_fits(const qk_gemv_args *a) {
+    const bool shape = a->K > 4 * 512 || (a->K == 4 * 512 && a->rows >= 4096);
+    return shape && (a->epi == QK_EPI_STORE || a->epi == QK_EPI_ADD) && a->x && !a->tok && !a->merge_o &&
+           !a->norm_w && !a->normed_store && !a->x_store;
+}
+
+template <int NCW>
+static void gemv_ks_dispatch(const qk_gemv_args *a, hipStream_t s) {
+    // ROWS rows per block: at least 512 blocks where the rows allow
+    const int rows = a->rows >= 4 * 512 ? 4 : a->rows >= 2 * 512 ? 2 : 1;
+    const int blocks = (a->rows + rows - 1) / rows;
+#define QK_KS(RW)                                                                                   \
+    if (rows == RW) {                                                                                 \
+        if (a->epi == QK_EPI_STORE) gemv_ks<NCW, RW, QK_EPI_STORE><<<blocks, 256, 0, s>>>(*a);        \
+        else gemv_ks<NCW, RW, QK_EPI_ADD><<<blocks, 256, 0, s>>>(*a);                                 \
+    }
+    QK_KS(4) QK_KS(2) QK_KS(1)
+#undef QK_KS
+}
+
 static int gemv_pick_rows(int R, int epi) {
     if (epi == QK_EPI_ARGMAX) return 4;
     if (R / 16 >= 256) return 4;
@@ -262,13 +346,16 @@ extern "C" int qk_gemv_blocks(int rows, int K, int epi) {
 template <int NC, int ROWS>
 static void gemv_dispatch_epi(const qk_gemv_args *a, int iters, int blocks, hipStream_t s) {
     switch (a->epi) {
-    case QK_EPI_STORE: gemv_kernel<NC, ROWS, QK_EPI_STORE><<<blocks, 256, 0, s>>>(*a, iters); break;
-    case QK_EPI_ADD: gemv_kernel<NC, ROWS, QK_EPI_ADD><<<blocks, 256, 0, s>>>(*a, iters); break;
+    case QK_EPI_STORE: gemv_kernel<NC, ROWS, QK_EPI_STORE, false><<<blocks, 256, 0, s>>>(*a, iters); break;
+    case QK_EPI_ADD:
+        if (a->merge_o) gemv_kernel<NC, ROWS, QK_EPI_ADD, true><<<blocks, 256, 0, s>>>(*a, iters);
+        else gemv_kernel<NC, ROWS, QK_EPI_ADD, false><<<blocks, 256, 0, s>>>(*a, iters);
+        break;
     case QK_EPI_SWIGLU:
-        if (ROWS >= 2) gemv_kernel<NC, (ROWS >= 2 ? ROWS : 2), QK_EPI_SWIGLU><<<blocks, 256, 0, s>>>(*a, iters);
+        if (ROWS >= 2) gemv_kernel<NC, (ROWS >= 2 ? ROWS : 2), QK_EPI_SWIGLU, false><<<blocks, 256, 0, s>>>(*a, iters);
         break;
     default:
-        if (ROWS == 4) gemv_kernel<NC, 4, QK_EPI_ARGMAX><<<blocks, 256, 0, s>>>(*a, iters);
+        if (ROWS == 4) gemv_kernel<NC, 4, QK_EPI_ARGMAX, false><<<blocks, 256, 0, s>>>(*a, iters);
         break;
     }
 }
@@ -290,6 +377,13 @@ extern "C" int qk_gemv_launch(const qk_gemv_args *a, hipStream_t s) {
                        a->merge_nsplit > QK_MERGE_MAX_SPLIT || a->K > QK_MERGE_MAX_K || (a->K & 127) || a->tok))
         return QWEN_HIP_EINVAL;
     if (a->tok && !a->emb) return QWEN_HIP_EINVAL;
+    if (gemv_ks_fits(a)) {
+        const int ncw = (a->K + 4 * 512 - 1) / (4 * 512);
+        if (ncw == 1) gemv_ks_dispatch<1>(a, s);
+        else if (ncw == 2) gemv_ks_dispatch<2>(a, s);
+        else gemv_ks_dispatch<3>(a, s);
+        return hipGetLastError() == hipSuccess ? 0 : QWEN_HIP_EDEVICE;
+    }
     const int rows_pw = gemv_pick_rows(a->rows, a->epi);
     const int iters = gemv_pick_iters(a->K, a->epi);
     const int blocks = qk_gemv_blocks(a->rows, a->K, a->epi);
