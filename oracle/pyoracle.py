@@ -187,6 +187,9 @@ def ref_lib():
         lib.ref_embed_token.argtypes = [C.c_void_p, C.c_int, _f32p]
         lib.ref_kv_len.argtypes = [C.c_void_p]
         lib.ref_set_kv_len.argtypes = [C.c_void_p, C.c_int]
+        lib.ref_kv_max.argtypes = [C.c_void_p]
+        lib.ref_bf16_widen.argtypes = [C.c_void_p, C.c_void_p, C.c_long]
+        lib.ref_bf16_widen.restype = None
         lib.ref_generate.argtypes = [C.c_void_p, C.c_int, C.c_int, _i32p]
         lib.ref_generate.restype = C.c_double
         lib.ref_time_prefill.argtypes = [C.c_void_p, _f32p, C.c_int]
@@ -359,6 +362,18 @@ class RefModel(_Decoder):
         out = np.empty(n_steps, np.int32)
         secs = self.lib.ref_generate(self.h, int(first_token), int(n_steps), out)
         return out, secs
+
+    def extend_kv(self, n, row):
+        """Raise the KV length to n without prefilling, for timing decode steps
+        at a long context: the rows past the prefilled ones hold zeros (the
+        attention's cost depends on the length, not the values).  The length
+        is first stepped to the cache's capacity so that each growth of the
+        next forward (qwen_asr_decoder.c:403-406, :133-160) copies only rows
+        inside the old cache; `row` is that forward's input."""
+        while self.lib.ref_kv_max(self.h) <= n:
+            self.set_kv_len(self.lib.ref_kv_max(self.h))
+            self.forward(row)
+        self.set_kv_len(n)
 
     def time_prefill(self, rows):
         rows = np.ascontiguousarray(rows, np.float32).reshape(-1)

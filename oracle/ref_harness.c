@@ -124,6 +124,17 @@ void ref_embed_token(void *mp, int token, float *out) {
 }
 
 int ref_kv_len(void *mp) { return ((ref_model_t *)mp)->ctx->kv_cache_len; }
+/* The widening of bf16_to_f32_buf (qwen_asr_kernels.c:232-236, static
+ * there), which the reference's seq > 1 linear runs on every weight before
+ * its GEMM (bf16_get_f32_view, :322-330); for the CPU baseline's BLAS-path
+ * estimate. */
+void ref_bf16_widen(float *dst, const uint16_t *src, long n) {
+    uint32_t *d = (uint32_t *)(void *)dst;
+    for (long i = 0; i < n; i++) d[i] = ((uint32_t)src[i]) << 16;
+}
+
+/* Capacity of the reference's KV cache (kv_cache_max, qwen_asr_decoder.c:122-160). */
+int ref_kv_max(void *mp) { return ((ref_model_t *)mp)->ctx->kv_cache_max; }
 void ref_set_kv_len(void *mp, int n) { ((ref_model_t *)mp)->ctx->kv_cache_len = n; }
 
 /* Greedy loop of qwen_asr.c:729-759 without EOS stop: n_steps forwards, each
