@@ -385,8 +385,9 @@ def test_streaming_rollback_pattern(qa, dec06):
             assert s[-1] - s[-2] < TIE, (i, a, b)
 
 
-def test_wait_bound_gives_up(qa, dec06):
-    """Every wait inside the persistent kernel is bounded in wall-clock time.
+@pytest.mark.parametrize("relay", [True, False])
+def test_wait_bound_gives_up(qa, dec06, relay):
+    """Every wait inside either persistent kernel is bounded in wall-clock time.
     With a zero limit every wait that its first poll does not satisfy gives
     up: the launch still ends (every block leaves), and with the fallback off
     the call fails with QWEN_HIP_EDEVICE and leaves kv_len as it was; with the
@@ -396,11 +397,13 @@ def test_wait_bound_gives_up(qa, dec06):
     d, rows = dec06
     try:
         d.set_engine(ENGINE_PERSIST)
+        d.set_relay(relay)
         d.set_kv_len(0)
         d.prefill(rows[:-1])
         base = d.kv_len()
         first = d.forward(rows[-1])
         ref = list(d.generate(first, 6))
+        assert d.last_kernel() == (qa.KERNEL_RELAY if relay else qa.KERNEL_SPLIT)
         n0 = d.fallbacks()
         d.set_kv_len(base + 1)
         d.set_fallback(False)
@@ -419,8 +422,10 @@ def test_wait_bound_gives_up(qa, dec06):
         d.set_engine(ENGINE_PERSIST)
         d.set_kv_len(base + 1)
         assert list(d.generate(first, 6)) == ref
+        assert d.last_kernel() == (qa.KERNEL_RELAY if relay else qa.KERNEL_SPLIT)
         assert d.fallbacks() == n0 + 1
     finally:
         d.set_wait_limit(1.0)
         d.set_fallback(True)
         d.set_engine(ENGINE_PERSIST)
+        d.set_relay(True)
