@@ -737,9 +737,14 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
 
     const int L = a.layers, b = blockIdx.x, tid = threadIdx.x;
     const long WG = (long)QK_PX_XCD;
-    const int rpb = (a.vocab + QK_PX_BLOCKS - 1) / QK_PX_BLOCKS;
-    const int lm0 = b * rpb, lm1 = min(a.vocab, lm0 + rpb);
-    const int lmn = lm1 > lm0 ? (lm1 - lm0 + LMR - 1) / LMR : 0;
+    // LM head: groups of LMR rows dealt round-robin to the blocks (block b:
+    // groups b, b + 256, ...), so at any moment the grid streams one window of
+    // the table (C3 992.8 -> 1000.3 tok/s, C1 2114 -> 2134 against one
+    // contiguous range per block)
+    const int lmg = (a.vocab + LMR - 1) / LMR;
+    const int lmn = b < lmg ? (lmg - b + QK_PX_BLOCKS - 1) / QK_PX_BLOCKS : 0;
+    const int lm1 = a.vocab;
+    auto lrow = [&](int k, int j) { return (b + QK_PX_BLOCKS * k) * LMR + j; };
 
     // launch check-in
     if (tid == 0) {
@@ -1072,7 +1077,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
         uint4 lmw[LMR][SEGH];
 #pragma unroll
         for (int j = 0; j < LMR; j++) {
-            const int row = lm0 + wave * LMR + j;
+            const int row = lrow(wave, j);
 #pragma unroll
             for (int c = 0; c < SEGH; c++)
                 lmw[j][c] = px_ld16(a.emb + (long)min(row, lm1 - 1) * H + c * 512, (unsigned)lane * 16u);
@@ -1091,7 +1096,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 if (more) {
 #pragma unroll
                     for (int j = 0; j < LMR; j++) {
-                        const int row = lm0 + (k + NCW) * LMR + j;
+                        const int row = lrow(k + NCW, j);
 #pragma unroll
                         for (int c = 0; c < SEGH; c++)
                             nx[j][c] = px_ld16(a.emb + (long)min(row, lm1 - 1) * H + c * 512, (unsigned)lane * 16u);
@@ -1111,7 +1116,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     for (int j = 0; j < LMR; j++) acc[j] = dot8_bf16(lmw[j][c], xv, acc[j]);
                 }
                 reduce_rows<LMR, 1>(acc, lane);   // lane groups of 64/LMR hold row lane / (64/LMR)
-                const int row = lm0 + k * LMR + lane / (64 / LMR);
+                const int row = lrow(k, lane / (64 / LMR));
                 if (row < lm1) {
                     if (a.logits && (lane % (64 / LMR)) == 0) a.logits[row] = acc[0];
                     if (argmax_better(acc[0], row, bv, bi)) { bv = acc[0]; bi = row; }

@@ -557,10 +557,15 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
     RlW w;
     if (team < L) rl_load_layer(a, S, kv, w, team, a.pos0, g, q, wave, lane);
     // LM-head rows of this block
-    const int rpb = (a.vocab + 255) / 256;
-    const int lm0 = b * rpb, lm1 = min(a.vocab, lm0 + rpb);
+    // groups of LMR rows dealt round-robin to the blocks (block b: groups b,
+    // b + 256, ...; wave w: the block's groups w, w + 4, ...), so at any
+    // moment the grid streams one contiguous window of the table (C1: 2723 ->
+    // 2778 tok/s against one contiguous range per block)
     constexpr int LMR = 4;
-    const int lmn = lm1 > lm0 ? (lm1 - lm0 + LMR - 1) / LMR : 0;
+    const int lmg = (a.vocab + LMR - 1) / LMR;
+    const int lmn = b < lmg ? (lmg - b + 255) / 256 : 0;
+    const int lm1 = a.vocab;
+    auto lrow = [&](int k, int j) { return (b + 256 * k) * LMR + j; };
 
     for (int s = 0; s < a.n_steps; s++) {
         const int pos = a.pos0 + s;
@@ -887,7 +892,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
             uint4 lmw[LMR][2];
 #pragma unroll
             for (int j = 0; j < LMR; j++) {
-                const int row = lm0 + wave * LMR + j;
+                const int row = lrow(wave, j);
 #pragma unroll
                 for (int c = 0; c < 2; c++)
                     lmw[j][c] = ld_stream16(a.emb + (long)min(row, lm1 - 1) * RL_H + c * 512 + lane * 8);
@@ -913,7 +918,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                 if (more) {
 #pragma unroll
                     for (int j = 0; j < LMR; j++) {
-                        const int row = lm0 + (k + RL_NW) * LMR + j;
+                        const int row = lrow(k + RL_NW, j);
 #pragma unroll
                         for (int c = 0; c < 2; c++)
                             nx[j][c] = ld_stream16(a.emb + (long)min(row, lm1 - 1) * RL_H + c * 512 + lane * 8);
@@ -933,7 +938,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                     for (int j = 0; j < LMR; j++) acc[j] = dot8_bf16(lmw[j][c], xv, acc[j]);
                 }
                 reduce_rows<LMR, 1>(acc, lane);   // lane groups of 16 hold row lane / 16
-                const int row = lm0 + k * LMR + lane / (64 / LMR);
+                const int row = lrow(k, lane / (64 / LMR));
                 if (row < lm1) {
                     if (a.logits && (lane % (64 / LMR)) == 0) a.logits[row] = acc[0];
                     if (argmax_better(acc[0], row, bv, bi)) {
