@@ -92,15 +92,19 @@ def free_run(name, cfg, n_audio, n_ids, n_forwards):
                  "forwards": n_forwards, "prefill_s": round(tp, 2), "total_s": round(time.time() - t0, 1)})
 
 
-def logits_run(name, cfg, n_audio, n_ids, n_forwards):
+def logits_run(name, cfg, n_audio, n_ids, n_forwards, prefill_threads=1):
     """Full fp32 logits (every vocabulary row) of the first n_forwards greedy
     forwards of fixture `name`'s run, written to {name}_logits.npz beside the
-    top-8 fixture (same model, rows and step convention as free_run)."""
+    top-8 fixture (same model, rows and step convention as free_run).  The
+    prefill may use more threads: its linears run the reference's
+    single-threaded loop and its attention splits by head, so the thread count
+    changes no result there; the forwards run on one thread."""
     t0 = time.time()
     m = P.SynthModel(cfg, seed=0)
     rows, ids = P.prompt_rows(m, n_audio, n_ids)
-    r = P.RefModel(m, threads=1)
+    r = P.RefModel(m, threads=prefill_threads)
     r.prefill(rows[:-1])
+    r.lib.ref_set_threads(1)
     x = rows[-1]
     toks, logits = [], []
     for i in range(n_forwards):
@@ -111,7 +115,7 @@ def logits_run(name, cfg, n_audio, n_ids, n_forwards):
                         logits=np.array(logits), emb_checksum=np.uint64(P.checksum_u16(m.emb)),
                         n_audio=np.int32(n_audio), n_ids=np.int32(n_ids))
     return meta({"config": f"{name}_logits", "hidden": cfg.hidden, "prefill_rows": int(rows.shape[0] - 1),
-                 "forwards": n_forwards, "total_s": round(time.time() - t0, 1)})
+                 "forwards": n_forwards, "prefill_threads": prefill_threads, "total_s": round(time.time() - t0, 1)})
 
 
 FIXTURES = {
@@ -121,6 +125,8 @@ FIXTURES = {
     "c3_short": lambda: free_run("c3_short", P.CFG_17B, 30, 16, 9),
     "c1_full_logits": lambda: logits_run("c1_full", P.CFG_06B, 390, 12, 4),
     "c3_short_logits": lambda: logits_run("c3_short", P.CFG_17B, 30, 16, 4),
+    # C4's shape at full depth: 8191 prefill rows, then forwards at positions 8191-8193
+    "c4_long_logits": lambda: logits_run("c4_long", P.CFG_06B, 8192, 0, 3, prefill_threads=8),
 }
 
 

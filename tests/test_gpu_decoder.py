@@ -390,3 +390,43 @@ def test_full_logits_golden(P, request, name, path):
     if not big:
         d.set_relay(True)
     print(f"{name} {path}: {len(g['logits'])} steps x {cfg.vocab} logits, max |dlogit| = {worst:.3e}")
+
+
+@pytest.mark.parametrize("engine", [0, 2])
+def test_c4_depth_full_logits_golden(P, qa, gpu, engine):
+    """C4's shape at full depth against the reference itself: the 28-layer
+    0.6B model, an 8191-row prefill, then forwards at positions 8191-8193 fed
+    the reference's tokens; every one of the 151936 logits per step within
+    the north star's bound (2e-2 + 1e-2 |ref|) and within FULL_LOGIT_ATOL, on
+    the graph engine and the persistent engine (its split kernel: these
+    positions are past the relay kernel's range)."""
+    g = np.load(os.path.join(GOLD, "c4_long_logits.npz"))
+    cfg = P.CFG_06B
+    n = int(g["n_audio"]) + int(g["n_ids"])
+    assert int(g["n_ids"]) == 0
+    # P.prompt_rows with no ids: the audio rows alone
+    rows = P.synth_f32(n * cfg.hidden, 0, P.synth_audio_id(0)).reshape(n, cfg.hidden)
+    d = qa.Decoder(qa.preset(0), 0, n + 64)
+    try:
+        d.load_synthetic(0, 0.02, 0.0)
+        d.set_engine(engine)
+        d.set_fallback(False)
+        d.set_keep_logits(True)
+        d.prefill(rows[:-1])
+        worst = 0.0
+        for i, ref in enumerate(g["logits"]):
+            t = d.forward(rows[-1]) if i == 0 else d.forward_token(int(g["tokens"][i - 1]))
+            lg = d.read_logits()
+            assert close(lg, ref), (i, float(np.abs(lg - ref).max()))
+            dl = float(np.abs(lg - ref).max())
+            assert dl < FULL_LOGIT_ATOL, (i, dl)
+            worst = max(worst, dl)
+            top2 = np.sort(ref)[-2:]
+            assert t == int(g["tokens"][i]) or top2[1] - top2[0] < TIE, (i, t, int(g["tokens"][i]))
+        assert d.engine() == engine
+        if engine == 2:
+            assert d.last_kernel() == qa.KERNEL_SPLIT
+        print(f"c4 depth, engine {engine}: {len(g['logits'])} steps at positions {n - 1}+ x {cfg.vocab} logits, "
+              f"max |dlogit| = {worst:.3e}")
+    finally:
+        d.close()
