@@ -377,7 +377,6 @@ struct RlShared {
         float red[RL_NW][48];       // per-wave product partials
     };
     float part[QK_RL_TEAM * 18];    // (m, l, o[16]) of every split for this block's merge dims
-    float ysum[RL_XCD][RL_SO];      // cross-XCD split-K partials of this block's slice
     float cand[2 * 256];            // LM-head candidates
     float ssq[RL_NW];
     float wv[RL_NW];
@@ -435,41 +434,26 @@ __device__ __forceinline__ void rl_load_layer(const qk_relay_args &a, RlShared &
 __device__ __forceinline__ bool rl_residual(const qk_relay_args &a, RlShared &S, const u64 *part, unsigned tp,
                                             const u64 *bsrc, unsigned tb, u64 *xl, unsigned tx, const float *w, int q,
                                             int wave, int lane, u64 *tr1, u64 *tr2) {
+    // wave 0 polls the base rows (the other team's, when bsrc is given; else
+    // the block's own) and all 8 slices of its rows, sums them in slice order
+    // in registers and republishes at once, while the other waves go straight
+    // to the gather: no barrier on the way (C1 2771 -> 2831 tok/s against the
+    // four waves polling two slices each into LDS).  For its own base, wave 0
+    // reads the rows before it publishes them, and a wave whose gather range
+    // holds them overwrites them only after seeing that publication.
     bool ok = true;
-    if (!bsrc) {
-        // the base is the block's own residual: wave 0 polls all 8 slices of
-        // its rows, sums them in slice order in registers and republishes at
-        // once, while the other waves go straight to the gather (no barrier
-        // on the way: C1 2771 -> 2812 tok/s).  Wave 0 reads its base rows
-        // before it publishes them, and a wave whose gather range holds them
-        // overwrites them only after seeing that publication.
-        if (wave == 0) {
-            float o = 0.0f;
+    if (wave == 0) {
+        float o = 0.0f, base = 0.0f;
+        if (bsrc)   // XCD-local, published with the slices: first
+            ok = rl_poll<1>(
+                a, bsrc, [&](int i) { return RL_SO * q + i; }, 0, RL_SO, tb, [&](int, float v) { base = v; }, lane);
+        if (ok)
             ok = rl_poll<RL_XCD>(
                 a, part, [&](int i) { return (i >> 6) * RL_H + RL_SO * q + (i & 63); }, 0, RL_XCD * RL_SO, tp,
                 [&](int i, float v) { o = (i >> 6) == 0 ? v : o + v; }, lane);
-            if (ok) rl_put_local(xl + RL_SO * q + lane, S.xs[RL_SO * q + lane] + o, tx);
-            if (tr1) *tr1 = wall_clock64();
-        }
-    } else {
-        // wave w: the slices of XCDs 2w, 2w + 1; wave 3 also the base rows
-        ok = rl_poll<2>(
-            a, part, [&](int i) { return (2 * wave + (i >> 6)) * RL_H + RL_SO * q + (i & 63); }, 0, 2 * RL_SO, tp,
-            [&](int i, float v) { S.ysum[2 * wave + (i >> 6)][i & 63] = v; }, lane);
-        if (ok && wave == 3)
-            ok = rl_poll<1>(
-                a, bsrc, [&](int i) { return RL_SO * q + i; }, 0, RL_SO, tb,
-                [&](int i, float v) { S.xs[RL_SO * q + i] = v; }, lane);
-        if (!ok) S.abort_ = 1;
-        rl_sync();
-        if (S.abort_) return false;
+        if (!bsrc) base = S.xs[RL_SO * q + lane];
+        if (ok) rl_put_local(xl + RL_SO * q + lane, base + o, tx);
         if (tr1) *tr1 = wall_clock64();
-        if (wave == 0) {
-            float o = S.ysum[0][lane];
-#pragma unroll
-            for (int gg = 1; gg < RL_XCD; gg++) o += S.ysum[gg][lane];
-            rl_put_local(xl + RL_SO * q + lane, S.xs[RL_SO * q + lane] + o, tx);
-        }
     }
     float v[4];
     if (ok) ok = rl_poll_vec<4>(a, xl, 256 * wave, tx, v, lane);
