@@ -833,16 +833,21 @@ def main():
     engine = d.engine()
     kernel = d.last_kernel() if engine == 2 else 0
     stages = None
-    if kernel == qa.KERNEL_RELAY and not args.no_stages:
+    if kernel in (qa.KERNEL_RELAY, qa.KERNEL_SPLIT) and not args.no_stages:
         # the kernel's own stage stamps for one step (step 6 of a 10-step launch
         # from the same position; outside the timed region)
         d.set_kv_len(base)
         d.set_trace(6)
         d.generate(first, 10)
         d.set_trace(-1)
-        stages = qa.relay_stage_us(d.read_trace(), cfg.layers)
-        log(f"[gpu] relay stages (us per layer): period {stages['layer period']}, "
-            f"LM rows {stages['LM head rows: median block']} / {stages['LM head rows: slowest block']}")
+        if kernel == qa.KERNEL_RELAY:
+            stages = qa.relay_stage_us(d.read_trace(), cfg.layers)
+            log(f"[gpu] relay stages (us per layer): period {stages['layer period']}, "
+                f"LM rows {stages['LM head rows: median block']} / {stages['LM head rows: slowest block']}")
+        else:
+            stages = qa.split_stage_us(d.read_trace(), cfg.layers)
+            log(f"[gpu] split stages (us per layer): period {stages['layer period']}, "
+                + ", ".join(f"{k} {v}" for k, v in stages.items() if k.startswith("stage")))
     if not args.no_traffic:
         extra = ["--kernel", args.kernel]
         fr = pmc_pass("FETCH_SIZE", args.workload, extra=extra)
@@ -887,8 +892,9 @@ def main():
     if stages:
         out["roofline"]["stage_trace_us"] = stages
         out["roofline"]["stage_trace_note"] = (
-            "the kernel's wall-clock stamps (100 MHz) for one step at position ~408: per-layer stages as the "
-            "median over the computing team's blocks, averaged over layers 2-25 (qwen_asr_amd.relay_stage_us)")
+            f"the kernel's wall-clock stamps (100 MHz) for one step at position {base + 6}: per-layer stages as "
+            "the median over blocks, averaged over layers (qwen_asr_amd." +
+            ("relay_stage_us" if kernel == qa.KERNEL_RELAY else "split_stage_us") + ")")
     if c3:
         out["c3_decode"] = c3
     print(json.dumps(out), flush=True)

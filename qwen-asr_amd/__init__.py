@@ -626,3 +626,35 @@ def relay_stage_us(tr, layers):
     tb = tr[:, TM * layers + 4] > 0
     out["token: last candidate -> median token"] = round(float(np.median(t[tb, TM * layers + 4]) - t[blk, TM * layers + 3].max()), 3)
     return out
+
+
+def split_stage_us(tr, layers):
+    """Per-layer stage times (microseconds) of one traced split-kernel step
+    (the header's split trace layout): for each of the five stages (Q, A, O,
+    F, D) the sync wave's wait for its input and the compute that follows
+    (median over blocks, averaged over the layers), the LM head's wait and
+    compute, the token wait, and the cross-XCD half of the two residual
+    updates.  tr is read_trace()'s [256][704] array of 100 MHz stamps."""
+    tr = np.asarray(tr).astype(np.int64)
+    L = layers
+    t = (tr - tr[:, 0].min()) * 0.01
+    med = lambda x: float(np.median(x))
+    out = {}
+    for k, name in enumerate(("Q", "A", "O", "F", "D")):
+        w = c = 0.0
+        for l in range(L):
+            ent, rdy = t[:, 10 * l + 2 * k], t[:, 10 * l + 2 * k + 1]
+            nxt = t[:, 10 * l + 2 * k + 2] if (l < L - 1 or k < 4) else t[:, 10 * L]
+            w += med(rdy - ent)
+            c += med(nxt - rdy)
+        out[f"stage {name}: wait"] = round(w / L, 3)
+        out[f"stage {name}: compute"] = round(c / L, 3)
+    out["LM head: wait"] = round(med(t[:, 10 * L + 1] - t[:, 10 * L]), 3)
+    out["LM head: compute"] = round(med(t[:, 10 * L + 2] - t[:, 10 * L + 1]), 3)
+    out["token: wait"] = round(med(t[:, 10 * L + 3] - t[:, 10 * L + 2]), 3)
+    X = 640
+    ls = range(2, L - 1)
+    out["residual before Q: cross-XCD half"] = round(float(np.mean([med(t[:, X + 2 * l] - t[:, 10 * l]) for l in ls])), 3)
+    out["residual before F: cross-XCD half"] = round(float(np.mean([med(t[:, X + 2 * l + 1] - t[:, 10 * l + 6]) for l in ls])), 3)
+    out["layer period"] = round(float(np.mean([med(t[:, 10 * (l + 1)] - t[:, 10 * l]) for l in ls])), 3)
+    return out
