@@ -172,6 +172,14 @@ int qwen_hip_decoder_fallbacks(const qwen_hip_decoder *dec);
 /* seconds in [0, 60]; 0 makes every wait that is not satisfied by its first
  * poll give up (a test of the give-up path) */
 int qwen_hip_decoder_set_wait_limit(qwen_hip_decoder *dec, double seconds);
+/* Hand-over words carry a 32-bit tag that every launch takes from a running
+ * epoch (each launch advances it by the tags it uses); when the next launch
+ * would pass 0xFFFFFF00 the decoder zeroes the exchange words and starts again
+ * at 1.  set_tag_epoch (epoch >= 1) zeroes the words and sets the epoch, so a
+ * test can run launches at the top of the tag space and across the restart;
+ * tag_epoch reads it (0 for a NULL decoder). */
+int qwen_hip_decoder_set_tag_epoch(qwen_hip_decoder *dec, unsigned epoch);
+unsigned qwen_hip_decoder_tag_epoch(const qwen_hip_decoder *dec);
 
 /* Diagnostics of the persistent engine (no reference counterpart; the
  * reference only times whole phases with gettimeofday, qwen_asr.c:362-366).

@@ -68,6 +68,8 @@ SIGNATURES = [
     ("qwen_hip_decoder_set_fallback", _i, [_vp, _i]),
     ("qwen_hip_decoder_fallbacks", _i, [_vp]),
     ("qwen_hip_decoder_set_wait_limit", _i, [_vp, _d]),
+    ("qwen_hip_decoder_set_tag_epoch", _i, [_vp, C.c_uint]),
+    ("qwen_hip_decoder_tag_epoch", C.c_uint, [_vp]),
     ("qwen_hip_decoder_set_trace", _i, [_vp, _i]),
     ("qwen_hip_decoder_read_trace", _i, [_vp, _vp, C.c_size_t]),
     ("qwen_hip_decoder_set_relay", _i, [_vp, _i]),
@@ -487,6 +489,13 @@ class Decoder:
 
     def set_wait_limit(self, seconds):
         check(lib().qwen_hip_decoder_set_wait_limit(self.h, float(seconds)), "set_wait_limit")
+
+    def set_tag_epoch(self, epoch):
+        """Zero the persistent engine's exchange words and set the tag epoch."""
+        check(lib().qwen_hip_decoder_set_tag_epoch(self.h, int(epoch)), "set_tag_epoch")
+
+    def tag_epoch(self):
+        return int(lib().qwen_hip_decoder_tag_epoch(self.h))
 
     def set_trace(self, step):
         check(lib().qwen_hip_decoder_set_trace(self.h, int(step)), "set_trace")

@@ -972,6 +972,20 @@ int qwen_hip_decoder_set_wait_limit(qwen_hip_decoder *d, double seconds) {
     return 0;
 }
 
+int qwen_hip_decoder_set_tag_epoch(qwen_hip_decoder *d, unsigned epoch) {
+    if (!d || epoch == 0u) { qk_set_err("set_tag_epoch: epoch must be at least 1"); return QWEN_HIP_EINVAL; }
+    if (!d->px_ok) { qk_set_err("set_tag_epoch: the persistent engine is not available"); return QWEN_HIP_ESTATE; }
+    QK_TRY(use_device(d));
+    /* zeroed words carry tag 0, which no hand-over expects, so any epoch is safe after this */
+    QK_HIP(hipMemsetAsync(d->px_buf, 0, d->px_words * 8, d->stream));
+    if (d->rl_buf) QK_HIP(hipMemsetAsync(d->rl_buf, 0, d->rl_words * 8, d->stream));
+    QK_HIP(hipStreamSynchronize(d->stream));
+    d->px_epoch = epoch;
+    return 0;
+}
+
+unsigned qwen_hip_decoder_tag_epoch(const qwen_hip_decoder *d) { return d ? d->px_epoch : 0u; }
+
 int qwen_hip_decoder_set_trace(qwen_hip_decoder *d, int step) {
     if (!d) return QWEN_HIP_EINVAL;
     if (!d->px_ok) { qk_set_err("set_trace: the persistent engine is not available"); return QWEN_HIP_ESTATE; }

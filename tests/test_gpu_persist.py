@@ -429,3 +429,52 @@ def test_wait_bound_gives_up(qa, dec06, relay):
         d.set_fallback(True)
         d.set_engine(ENGINE_PERSIST)
         d.set_relay(True)
+
+
+@pytest.mark.parametrize("relay", [True, False])
+def test_tag_space_restart(qa, dec06, relay):
+    """Hand-over tags come from a 32-bit epoch that each launch advances by the
+    tags it uses; a launch that would pass 0xFFFFFF00 first zeroes the exchange
+    words and restarts at 1.  A launch that ends exactly at the limit (its
+    last tags the highest ever used), the restart after it, and single-step
+    launches across a restart all give the same tokens as at a low epoch."""
+    d, rows = dec06
+    top = 0xFFFFFF00
+    try:
+        d.set_engine(ENGINE_PERSIST)
+        d.set_relay(relay)
+        d.set_kv_len(0)
+        d.prefill(rows[:-1])
+        base = d.kv_len()
+        first = d.forward(rows[-1])
+        e0 = d.tag_epoch()
+        ref = list(d.generate(first, 8))
+        need = d.tag_epoch() - e0
+        assert d.last_kernel() == (qa.KERNEL_RELAY if relay else qa.KERNEL_SPLIT)
+        assert 0 < need < 1 << 20
+        # a launch whose tags end exactly at the limit: no restart
+        d.set_tag_epoch(top - need)
+        d.set_kv_len(base + 1)
+        assert list(d.generate(first, 8)) == ref
+        assert d.tag_epoch() == top
+        # the next launch restarts the tag space first
+        d.set_kv_len(base + 1)
+        assert list(d.generate(first, 8)) == ref
+        assert d.tag_epoch() == 1 + need
+        # one step per launch, restarting after the second launch
+        d.set_kv_len(base + 1)
+        e1 = d.tag_epoch()
+        t = d.forward_token(first)
+        one = d.tag_epoch() - e1
+        d.set_tag_epoch(top - 2 * one)
+        d.set_kv_len(base + 1)
+        t, steps = first, []
+        for _ in range(8):
+            t = d.forward_token(t)
+            steps.append(t)
+        assert steps == ref
+        assert d.tag_epoch() == 1 + 6 * one
+        assert d.engine() == ENGINE_PERSIST
+    finally:
+        d.set_relay(True)
+        d.set_engine(ENGINE_PERSIST)
