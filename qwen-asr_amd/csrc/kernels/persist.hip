@@ -98,6 +98,18 @@ __device__ __forceinline__ float4 px_ldf4(const void *base, unsigned off) {
 // it); this wave's LDS accesses are complete before it.
 __device__ __forceinline__ void px_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// This lane's index, produced where it is used: the compiler cannot hoist the
+// asm out of the layer loop, so offsets derived from it are recomputed in
+// place (two VALU ops) instead of being kept live across the loop.  Under
+// register pressure (1.7B) a kept offset was spilled, and its scratch reload
+// waits for every load the wave has in flight: the D-stage publish then
+// waited for the next layer's whole W_q slab.
+__device__ __forceinline__ int px_lane_here() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
 // Sync wave: wait until the n words at addr(i), i < n, carry `tag`, then
 // dst[i] = value.  PER words per lane in flight per pass.  False when the wait
 // passed a.wait_ticks (QK_PX_ERR_TIMEOUT raised) or another block raised an
@@ -156,11 +168,11 @@ struct PxSlab {
 
     // wave must be wave-uniform (an SGPR): every per-batch offset then folds
     // into the scalar base and a lane needs one 32-bit offset for all loads.
-    __device__ __forceinline__ void load(const uint16_t *W, int ld, int wave, int lane) {
-        unsigned lo = (unsigned)((lane / LW) * ld + (lane % LW) * 8) * 2u;
-        // recomputed at every call: otherwise the compiler keeps 64-bit
-        // per-lane slab addresses live across the layer loop and spills them
-        asm volatile("" : "+v"(lo));
+    __device__ __forceinline__ void load(const uint16_t *W, int ld, int wave, int /*lane*/) {
+        // recomputed at every call: otherwise the compiler keeps per-lane slab
+        // offsets live across the layer loop and spills them
+        const int ln = px_lane_here();
+        const unsigned lo = (unsigned)((ln / LW) * ld + (ln % LW) * 8) * 2u;
 #pragma unroll
         for (int b = 0; b < BPW; b++) {
             const uint16_t *wb = W + (long)((wave * WB + b) * RPI) * ld;
@@ -902,9 +914,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 // which stays in L2, and skipped).  1.7B (fewer registers per
                 // wave): one batch at a time.
                 if (!DEEP) {
-                    for (int pb = sp.s0 + gid + NG * AB; pb < sp.cend; pb += NG * AB) {
+                    const int ln = px_lane_here(), lgl = ln & 15, lgid = wave * 4 + (ln >> 4);
+                    for (int pb = sp.s0 + lgid + NG * AB; pb < sp.cend; pb += NG * AB) {
                         PxKv<AB> kv;
-                        kv.load(kcl, vcl, gl, pb, NG, sp.cend);
+                        kv.load(kcl, vcl, lgl, pb, NG, sp.cend);
                         bool in[AB];
 #pragma unroll
                         for (int j = 0; j < AB; j++) in[j] = pb + NG * j < sp.cend;
@@ -991,9 +1004,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 mark(6);
                 if ((lane & 31) == 0) {
                     u64 *dst = a.xo + (par * WG + g) * H + SO * r;
+                    const int ln = px_lane_here();
 #pragma unroll
                     for (int i = 0; i < SO / 2 / NCW; i++) {
-                        unsigned ro = (unsigned)SlabO::row(wave, i, lane);
+                        unsigned ro = (unsigned)SlabO::row(wave, i, ln);
                         asm volatile("" : "+v"(ro));   // no per-lane address kept across the loop
                         px_put_global(dst + ro, y[i], T + 2u);
                     }
@@ -1059,9 +1073,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 mark(9);
                 if ((lane & 15) == 0) {
                     u64 *dst = a.xd + (par * WG + g) * H + SO * r;
+                    const int ln = px_lane_here();
 #pragma unroll
                     for (int i = 0; i < SO / 4 / NCW; i++) {
-                        unsigned ro = (unsigned)SlabD::row(wave, i, lane);
+                        unsigned ro = (unsigned)SlabD::row(wave, i, ln);
                         asm volatile("" : "+v"(ro));   // no per-lane address kept across the loop
                         px_put_global(dst + ro, y[i], T + 5u);
                     }
