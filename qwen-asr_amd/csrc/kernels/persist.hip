@@ -1061,10 +1061,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
 
             // ---- D: this block's rows of W_down over the group's columns (:467-468) ----
             px_sync();
-            if (!DEEP) {
-                wd.load(Wd(l), I, wave, lane);
-                wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
-            }
+            if (!DEEP) wd.load(Wd(l), I, wave, lane);
             px_sync();
             if (S.abort_) return;
             {
@@ -1082,6 +1079,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                     }
                 }
             }
+            // 1.7B: the next W_q is issued once the down partials are out, so the
+            // D-stage hand-over queues behind W_down only (C3 1002.8 -> 1007.2 tok/s;
+            // the x-update hand-over before Q then waits behind W_q instead)
+            if (!DEEP) wq.load(Wq(l + 1 < L ? l + 1 : 0), H, wave, lane);
             {   // the next layer's operands (after the last layer: layer 0 of the next step)
                 const int ln = l + 1 < L ? l + 1 : 0;
                 const PxSplit sn(l + 1 < L ? pos : pos + 1, r);
