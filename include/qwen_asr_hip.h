@@ -158,8 +158,11 @@ int qwen_hip_decoder_read_logits(qwen_hip_decoder *dec, float *out);
  * where supported: 16 query / 8 kv heads, the 0.6B or 1.7B shape, 256 CUs in
  * 8 XCDs).  set_engine(2) returns QWEN_HIP_EINVAL where it is not supported.
  * Every wait inside the persistent kernel is bounded (set_wait_limit, default
- * 1 s of the device wall clock); a run that times out or finds its grid not
- * laid out one block per CU raises an error bit, and all its blocks leave.
+ * 1 s of the device wall clock; the launch check-in, where every block of the
+ * grid must have started, by 20 ms or the limit if shorter, so a grid that
+ * shares the device with other work gives up early); a run that times out or
+ * finds its grid not laid out one block per CU raises an error bit, and all
+ * its blocks leave.
  * With fallback on (set_fallback, the default) the decoder then reports on
  * stderr, counts the event (fallbacks), switches to engine 0 and redoes the
  * steps there; with fallback off the call returns QWEN_HIP_EDEVICE (forward:

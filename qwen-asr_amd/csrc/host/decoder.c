@@ -769,6 +769,17 @@ static int log_reserve(qwen_hip_decoder *d, int n) {
     return 0;
 }
 
+/* Bound of the launch check-in: QK_PX_CHECKIN_S, or the wait limit if that is
+ * shorter.  The blocks of an idle device all start within microseconds; a grid
+ * that is not fully resident by then shares the device with other work (its
+ * missing blocks could wait behind it indefinitely), so the launch gives up
+ * early instead of holding the CUs it has for the whole wait limit. */
+#define QK_PX_CHECKIN_S 0.02
+static unsigned long long checkin_ticks(const qwen_hip_decoder *d) {
+    const unsigned long long c = (unsigned long long)(QK_PX_CHECKIN_S * d->px_ticks_per_s);
+    return c < d->px_wait_ticks ? c : d->px_wait_ticks;
+}
+
 /* the relay kernel (rl_decode): two teams of CUs take the layers in turn */
 static int rl_launch(qwen_hip_decoder *d, int first_tok, int n) {
     const qwen_hip_config *c = &d->cfg;
@@ -781,7 +792,8 @@ static int rl_launch(qwen_hip_decoder *d, int first_tok, int n) {
         .cap = d->kv_cap, .rope_cos = d->rope_cos, .rope_sin = d->rope_sin, .layers = c->layers, .vocab = c->vocab,
         .eps = c->rms_eps, .scale = d->scale, .xq = d->rq, .xa = d->ra, .xm = d->rm, .xo = d->ro, .xla = d->rla,
         .xh = d->rh, .xd = d->rd, .xs = d->rs, .xlb = d->rlb, .xc = d->rc, .xv = d->rv, .cnt = d->px_ctl,
-        .err = d->px_ctl + 16, .epoch = d->px_epoch, .wait_ticks = d->px_wait_ticks, .pos0 = d->kv_len, .n_steps = n,
+        .err = d->px_ctl + 16, .epoch = d->px_epoch, .wait_ticks = d->px_wait_ticks, .checkin_ticks = checkin_ticks(d),
+        .pos0 = d->kv_len, .n_steps = n,
         .first_tok = first_tok, .x_in = d->x, .log = d->d_log, .tok_out = d->d_tok, .pos_out = d->d_pos,
         .hidden_out = d->hidden, .logits = d->keep_logits ? d->logits : NULL,
         .trace = d->px_trace_step >= 0 && d->px_trace_step < n ? d->px_trace : NULL, .trace_step = d->px_trace_step};
@@ -802,7 +814,7 @@ static int sp_launch(qwen_hip_decoder *d, int first_tok, int n) {
         .layers = c->layers, .vocab = c->vocab, .eps = c->rms_eps, .scale = d->scale,
         .xq = d->xq, .xa = d->xa, .xm = d->xm, .xo = d->xo, .xla = d->xla, .xh = d->xh, .xd = d->xd, .xlb = d->xlb,
         .xc = d->xc, .xv = d->xv, .cnt = d->px_ctl, .err = d->px_ctl + 16, .epoch = d->px_epoch,
-        .wait_ticks = d->px_wait_ticks,
+        .wait_ticks = d->px_wait_ticks, .checkin_ticks = checkin_ticks(d),
         .pos0 = d->kv_len, .n_steps = n, .first_tok = first_tok, .x_in = d->x, .log = d->d_log,
         .tok_out = d->d_tok, .pos_out = d->d_pos, .hidden_out = d->hidden,
         .logits = d->keep_logits ? d->logits : NULL,

@@ -114,8 +114,8 @@ __device__ __forceinline__ int px_lane_here() {
 // dst[i] = value.  PER words per lane in flight per pass.  False when the wait
 // passed a.wait_ticks (QK_PX_ERR_TIMEOUT raised) or another block raised an
 // error.  The clock is read while the pass's loads are in flight, so the
-// bound costs no extra round trip.
-template <int PER, typename Addr>
+// bound costs no extra round trip.  CHECKIN: the bound is a.checkin_ticks.
+template <int PER, bool CHECKIN = false, typename Addr>
 __device__ bool px_poll(const qk_persist_args &a, Addr addr, int n, unsigned tag, float *dst, int lane,
                         float *ssq = nullptr) {
     const u64 t0 = wall_clock64();
@@ -143,7 +143,7 @@ __device__ bool px_poll(const qk_persist_args &a, Addr addr, int n, unsigned tag
                 }
                 break;
             }
-            if (now - t0 > a.wait_ticks) {
+            if (now - t0 > (CHECKIN ? a.checkin_ticks : a.wait_ticks)) {
                 if (lane == 0) px_raise(a.err, QK_PX_ERR_TIMEOUT);
                 return false;
             }
@@ -525,7 +525,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
     {
         float *dst = S.cand;   // scratch
         auto addr = [&](int i) { return a.xv + i; };
-        bool ok = px_poll<4>(a, addr, QK_PX_BLOCKS, a.epoch, dst, lane);
+        bool ok = px_poll<4, true>(a, addr, QK_PX_BLOCKS, a.epoch, dst, lane);
         if (ok) {
             bool good = true;
             for (int i = lane; i < QK_PX_BLOCKS; i += 64) good = good && (__float_as_uint(dst[i]) & 1u);

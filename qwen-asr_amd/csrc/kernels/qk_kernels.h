@@ -181,6 +181,8 @@ typedef struct {
     unsigned *err;             /* QK_PX_ERR_* bits, zeroed before every launch */
     unsigned epoch;            /* first tag of this launch (>= 1) */
     unsigned long long wait_ticks; /* bound of every wait, in ticks of the device wall clock */
+    unsigned long long checkin_ticks; /* bound of the launch check-in wait (<= wait_ticks): every
+                                         block of the grid must have started within it */
     /* the steps */
     int pos0, n_steps;
     int first_tok;             /* >= 0: step 0 input is emb[first_tok] */
@@ -267,6 +269,7 @@ typedef struct {
     unsigned *err;             /* QK_PX_ERR_* bits, zeroed before every launch */
     unsigned epoch;            /* first tag of this launch (>= 1) */
     unsigned long long wait_ticks;
+    unsigned long long checkin_ticks; /* bound of the launch check-in wait (<= wait_ticks) */
     int pos0, n_steps;
     int first_tok;             /* >= 0: step 0 input is emb[first_tok] */
     const float *x_in;         /* first_tok < 0: step 0 input row [1024] */

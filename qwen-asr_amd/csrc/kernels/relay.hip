@@ -105,8 +105,8 @@ __device__ __forceinline__ void rl_wait_vm() { __builtin_amdgcn_s_waitcnt(0x0f70
 // raised an error.  The clock is read while the pass's loads are in flight.
 // The lane index is opaque to the optimiser, so no per-lane address of a poll
 // is hoisted out of the layer loop (that would hold ~2 VGPRs per word for the
-// whole kernel).
-template <int PER, typename Idx, typename Put>
+// whole kernel).  CHECKIN: the bound is a.checkin_ticks.
+template <int PER, bool CHECKIN = false, typename Idx, typename Put>
 __device__ __forceinline__ bool rl_poll(const qk_relay_args &a, const u64 *base, Idx idx, int i0, int i1, unsigned tag,
                                         Put put, int lane) {
     if (i1 <= i0) return true;
@@ -138,7 +138,7 @@ __device__ __forceinline__ bool rl_poll(const qk_relay_args &a, const u64 *base,
             }
             return true;
         }
-        if (now - t0 > a.wait_ticks) {
+        if (now - t0 > (CHECKIN ? a.checkin_ticks : a.wait_ticks)) {
             if (lane == 0) rl_raise(a.err, QK_PX_ERR_TIMEOUT);
             return false;
         }
@@ -533,7 +533,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
     rl_sync();
     {
         bool good = true;
-        const bool ok = rl_poll<1>(
+        const bool ok = rl_poll<1, true>(
             a, a.xv, [&](int i) { return (64 * wave + i) * QK_RL_LINE; }, 0, 64, a.epoch,
             [&](int, float v) { good = good && (__float_as_uint(v) & 1u); }, lane);
         if (!ok) S.abort_ = 1;

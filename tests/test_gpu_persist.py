@@ -478,3 +478,41 @@ def test_tag_space_restart(qa, dec06, relay):
     finally:
         d.set_relay(True)
         d.set_engine(ENGINE_PERSIST)
+
+
+def test_generate_beside_busy_stream(qa, dec06):
+    """A persistent launch queued while another stream keeps the CUs busy
+    (64 fp32 4096 x 4096 products): its blocks become resident as the other
+    kernels' blocks retire (measured: no fallback, ~5 ms), and a grid that
+    could not would give up at the launch check-in, bounded by 20 ms rather
+    than the 1 s wait limit.  Either way the call returns well within a
+    second with the right tokens."""
+    import time
+    import torch
+    d, rows = dec06
+    try:
+        d.set_engine(ENGINE_PERSIST)
+        d.set_kv_len(0)
+        d.prefill(rows[:-1])
+        base = d.kv_len()
+        first = d.forward(rows[-1])
+        ref = list(d.generate(first, 8))
+        n0 = d.fallbacks()
+        a = torch.randn(4096, 4096, device="cuda")
+        side = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            for _ in range(64):
+                a = torch.matmul(a, a) * 1e-3
+        d.set_kv_len(base + 1)
+        t0 = time.perf_counter()
+        got = list(d.generate(first, 8))
+        dt = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        print(f"generate beside a busy stream: {dt * 1e3:.1f} ms, fallbacks {d.fallbacks() - n0}, "
+              f"engine {d.engine()}")
+        assert got == ref
+        assert dt < 0.9, dt
+        assert torch.isfinite(a).all()
+    finally:
+        d.set_engine(ENGINE_PERSIST)
