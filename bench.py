@@ -79,7 +79,7 @@ def pmc_pass(counter, workload, timeout=150, extra=None):
         return None
     out = tempfile.mkdtemp(prefix="qk_pmc_")
     cmd = [exe, "--pmc", counter, "-d", out, "-o", "run", "--output-format", "csv", "--",
-           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--no-c3", "--no-stages",
+           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--no-extra", "--no-stages",
            "--steps", str(PMC_STEPS),
            "--warmup", "2", "--calib-copy-mb", "256", "--workload", workload] + list(extra or [])
     env = dict(os.environ, TMPDIR="/tmp")
@@ -664,6 +664,89 @@ def run_c3_decode(qa, K=C3_LINE_STEPS, W=8):
             "tokens_head": [int(first)] + [int(t) for t in toks[:7]]}
 
 
+C4_LINE_STEPS = 64
+
+
+def run_c4_decode(qa, K=C4_LINE_STEPS, W=8, reps=3):
+    """The 0.6B long-context decode carried in the default (C1) line: the C4
+    shape (prefill 8191 audio rows, forward the last row), then K timed greedy
+    steps from position 8192 in one persistent launch (the split kernel: the
+    relay kernel covers launches below position 1024); HIP events on the
+    decoder's stream.  The prefill time is the median of `reps` timed passes
+    after an untimed one.  No CPU leg and no counter passes (those are in
+    --workload c4)."""
+    import numpy as np
+    import torch
+    wl = WORKLOADS["c4"]
+    cfg = qa.preset(wl["model_b"])
+    n_rows = wl["n_audio"] + wl["n_ids"]
+    d = qa.Decoder(cfg, 0, n_rows + K + W + 64)
+    d.set_fallback(False)
+    t0 = time.time()
+    d.load_synthetic(0, 0.02, 0.0)
+    rows, _, _ = qa.prompt_rows(cfg, wl["n_audio"], wl["n_ids"])
+    d.prefill(rows[:-1])
+    times = []
+    for _ in range(reps):
+        d.set_kv_len(0)
+        torch.cuda.synchronize()
+        tp0 = time.perf_counter()
+        d.prefill(rows[:-1])
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - tp0)
+    prefill_s = sorted(times)[len(times) // 2]
+    first = d.forward(rows[-1])
+    base = d.kv_len()
+    d.generate(first, W)
+    d.set_kv_len(base)
+    stream = torch.cuda.ExternalStream(d.stream())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    tw0 = time.perf_counter()
+    toks = d.generate(first, K)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - tw0
+    gpu_ms = e0.elapsed_time(e1)
+    step_bytes = [d.step_bytes(base + i) for i in range(K)]
+    achieved = float(np.mean(step_bytes)) / (gpu_ms * 1e-3 / K) / 1e9
+    kernel = d.last_kernel() if d.engine() == 2 else 0
+    d.close()
+    log(f"[gpu] c4 in the line: prefill {n_rows - 1} rows {prefill_s * 1e3:.2f} ms; decode {K} steps "
+        f"{K / wall:.1f} tok/s ({gpu_ms * 1e3 / K:.1f} us/step, {achieved / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s); "
+        f"setup {time.time() - t0:.1f}s")
+    return {"workload": "C4 Qwen3-ASR-0.6B long context: prefill 8191 audio rows, forward, then greedy decode",
+            "steps": K, "decode_positions": [base, base + K - 1], "value": round(K / wall, 3), "unit": "tok/s",
+            "step_us": round(gpu_ms * 1e3 / K, 3),
+            "prefill_ms": round(prefill_s * 1e3, 3), "prefill_tok_s": round((n_rows - 1) / prefill_s, 2),
+            "prefill": prefill_rates(cfg, n_rows - 1, prefill_s),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         **launch_fields(2 if kernel else 0, K, step_bytes, gpu_ms, kernel)},
+            "tokens_head": [int(first)] + [int(t) for t in toks[:7]]}
+
+
+def run_c5_line(qa):
+    """The C5 streaming pattern carried in the default (C1) line: 2 warm-up
+    chunks, then C5_CHUNKS timed chunks (run_streaming; each chunk's wall time
+    includes its rollback, prefill, forward and greedy loop)."""
+    cfg = qa.preset(WORKLOADS["c5"]["model_b"])
+    d = qa.Decoder(cfg, 0, C5_CAP + 64)
+    d.set_fallback(False)
+    d.load_synthetic(0, 0.02, 0.0)
+    run_streaming(qa, d, cfg, 2)
+    toks, times = run_streaming(qa, d, cfg, C5_CHUNKS)
+    d.close()
+    total = sum(times)
+    log(f"[gpu] c5 in the line: {C5_CHUNKS} chunks, {total / C5_CHUNKS * 1e3:.3f} ms per chunk "
+        f"(max {max(times) * 1e3:.3f})")
+    return {"workload": WORKLOADS["c5"]["desc"], "chunks": C5_CHUNKS,
+            "value": round(C5_CHUNKS * C5_STEPS / total, 3), "unit": "generated tok/s",
+            "chunk_ms": {"mean": round(total / C5_CHUNKS * 1e3, 4), "max": round(max(times) * 1e3, 4)},
+            "tokens_head": [int(t) for t in toks[0][:8]]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -676,7 +759,8 @@ def main():
     ap.add_argument("--kernel", choices=("auto", "split", "relay"), default="auto",
                     help="persistent kernel: relay where available and the positions fit (default), or force one")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-c3", action="store_true", help="default (C1) line: skip the 1.7B decode block")
+    ap.add_argument("--no-extra", "--no-c3", dest="no_extra", action="store_true",
+                    help="default (C1) line: skip the C3 (1.7B decode), C4 (long context) and C5 (streaming) blocks")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc child runs")
     ap.add_argument("--c2-trace-reps", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--no-stages", action="store_true",
@@ -869,7 +953,10 @@ def main():
         cpu = cpu_baseline(wl, rows, first, threads, args.cpu_steps)
 
     d.close()
-    c3 = run_c3_decode(qa) if args.workload == "c1" and not args.no_c3 else None
+    extra = args.workload == "c1" and not args.no_extra
+    c3 = run_c3_decode(qa) if extra else None
+    c4 = run_c4_decode(qa) if extra else None
+    c5 = run_c5_line(qa) if extra else None
 
     out = {
         "metric": "decode tok/s at batch 1 (0.6B, 1.7B) + % of peak HBM GB/s; prefill tok/s",
@@ -897,6 +984,10 @@ def main():
             ("relay_stage_us" if kernel == qa.KERNEL_RELAY else "split_stage_us") + ")")
     if c3:
         out["c3_decode"] = c3
+    if c4:
+        out["c4_long_context"] = c4
+    if c5:
+        out["c5_streaming"] = c5
     print(json.dumps(out), flush=True)
 
 
