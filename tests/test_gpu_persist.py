@@ -509,10 +509,14 @@ def test_generate_beside_busy_stream(qa, dec06):
         got = list(d.generate(first, 8))
         dt = time.perf_counter() - t0
         torch.cuda.synchronize()
-        print(f"generate beside a busy stream: {dt * 1e3:.1f} ms, fallbacks {d.fallbacks() - n0}, "
-              f"engine {d.engine()}")
-        assert got == ref
+        fell = d.fallbacks() - n0
+        print(f"generate beside a busy stream: {dt * 1e3:.1f} ms, fallbacks {fell}, engine {d.engine()}")
         assert dt < 0.9, dt
         assert torch.isfinite(a).all()
+        if fell:   # redone by the graph engine: its tokens (equal to the persistent ones but for near-ties)
+            d.set_engine(ENGINE_GRAPH)
+            d.set_kv_len(base + 1)
+            ref = list(d.generate(first, 8))
+        assert got == ref
     finally:
         d.set_engine(ENGINE_PERSIST)
