@@ -431,6 +431,7 @@ __device__ __forceinline__ void rl_load_layer(const qk_relay_args &a, RlShared &
 // w gathers elements [256 w, 256 w + 256), the norm-weight range its own
 // load-phase DMA filled.  Order of the sum: x + (P_0 + ... + P_7), as x += o
 // in qwen_asr_decoder.c:458, :468.
+template <bool SYNC = true>
 __device__ __forceinline__ bool rl_residual(const qk_relay_args &a, RlShared &S, const u64 *part, unsigned tp,
                                             const u64 *bsrc, unsigned tb, u64 *xl, unsigned tx, const float *w, int q,
                                             int wave, int lane, u64 *tr1, u64 *tr2) {
@@ -474,6 +475,12 @@ __device__ __forceinline__ bool rl_residual(const qk_relay_args &a, RlShared &S,
     ss = wave_sum(ss);
     if (lane == 0) S.ssq[wave] = ss;
     if (!ok) S.abort_ = 1;
+    if constexpr (!SYNC) {
+        // the caller's next product reads only this wave's own range; its
+        // barrier after the product publishes S.ssq and S.abort_
+        if (tr2) *tr2 = wall_clock64();
+        return ok;
+    }
     rl_sync();
     if (S.abort_) return false;
     if (tr2) *tr2 = wall_clock64();
@@ -606,34 +613,36 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                 mark(RL_TM * l + 2);
             } else {
                 const unsigned tp = rl_tag(a, s, l - 1, 6);
-                const bool ok = rl_residual(a, S, a.xd + ((1 - t) * WG) * RL_H, tp, a.xs + ((1 - t) * WG + g) * RL_H, tp,
-                                            a.xlb + (t * WG + g) * RL_H, T(7), S.nin, q, wave, lane,
-                                            tracing ? trb + RL_TM * l + 1 : nullptr, tracing ? trb + RL_TM * l + 2 : nullptr);
-                if (!ok) return;
+                rl_residual<false>(a, S, a.xd + ((1 - t) * WG) * RL_H, tp, a.xs + ((1 - t) * WG + g) * RL_H, tp,
+                                   a.xlb + (t * WG + g) * RL_H, T(7), S.nin, q, wave, lane,
+                                   tracing ? trb + RL_TM * l + 1 : nullptr, tracing ? trb + RL_TM * l + 2 : nullptr);
                 rl_wait_vm();
             }
             mark(RL_TM * l + 3);
 
             // ---- Q: 32 rows of the group's Q|K|V (qwen_linear_nobias_bf16_qkv, qwen_asr_kernels.c:434-460) ----
             {
-                // wave w: row tile w & 1, k tiles [16 (w >> 1), + 16) on two accumulators
+                // wave w: row tiles 0, 1 over k tiles [8 w, 8 w + 8): the range of x
+                // this wave gathered itself, so no barrier between gather and product
                 f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
-                const int kt0 = 16 * (wave >> 1);
-                bf16x8 af[16];
+                bf16x8 af[8];
 #pragma unroll
-                for (int j = 0; j < 16; j++) af[j] = rl_afrag(S.xp, kt0 + j, lane);
+                for (int j = 0; j < 8; j++) af[j] = rl_afrag(S.xp, 8 * wave + j, lane);
                 __builtin_amdgcn_sched_barrier(0);   // every fragment read in flight before the products
 #pragma unroll
-                for (int j = 0; j < 16; j += 2) {
+                for (int j = 0; j < 8; j++) {
                     c0 = rl_mfma(af[j], w.q[j], c0);
-                    c1 = rl_mfma(af[j + 1], w.q[j + 1], c1);
+                    c1 = rl_mfma(af[j], w.q[8 + j], c1);
                 }
-                if (lane < 16) S.red[wave][lane] = rl_rowsum(c0) + rl_rowsum(c1);
+                if (lane < 16) {
+                    S.red[wave][lane] = rl_rowsum(c0);
+                    S.red[wave][16 + lane] = rl_rowsum(c1);
+                }
             }
             rl_sync();
+            if (S.abort_) return;
             if (wave == 0 && lane < 32) {
-                const int rt = lane >> 4, n = lane & 15;
-                const float y = (S.red[rt][n] + S.red[rt + 2][n]) * rl_rinv(a, S);
+                const float y = (((S.red[0][lane] + S.red[1][lane]) + S.red[2][lane]) + S.red[3][lane]) * rl_rinv(a, S);
                 rl_put_local(a.xq + (t * WG + g) * 512 + qrow + lane, y, T(0));
             }
             mark(RL_TM * l + 4);
@@ -812,10 +821,9 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
 
             // ---- F: x' = x + O; rms_norm; 48 gate|up rows + SwiGLU (qwen_asr_decoder.c:458-466) ----
             {
-                const bool ok = rl_residual(a, S, a.xo + (t * WG) * RL_H, T(3), nullptr, 0u, a.xla + (t * WG + g) * RL_H,
-                                            T(4), S.npost, q, wave, lane, tracing ? trb + RL_TM * l + 13 : nullptr,
-                                            tracing ? trb + RL_TM * l + 14 : nullptr);
-                if (!ok) return;
+                rl_residual<false>(a, S, a.xo + (t * WG) * RL_H, T(3), nullptr, 0u, a.xla + (t * WG + g) * RL_H, T(4),
+                                   S.npost, q, wave, lane, tracing ? trb + RL_TM * l + 13 : nullptr,
+                                   tracing ? trb + RL_TM * l + 14 : nullptr);
             }
             mark(RL_TM * l + 15);
             {
@@ -836,6 +844,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                 }
             }
             rl_sync();
+            if (S.abort_) return;
             mark(RL_TM * l + 16);
             if (wave == 0 && lane < 48) {
                 const float y = (((S.red[0][lane] + S.red[1][lane]) + S.red[2][lane]) + S.red[3][lane]) * rl_rinv(a, S);
@@ -1056,12 +1065,12 @@ __global__ __launch_bounds__(256) void rl_pack(uint4 *dst, const uint16_t *wqkv,
     const int g = (int)(t / QK_RL_TEAM);
     const int rl = lane & 15, kl = 8 * (lane >> 4);
     const uint16_t *src;
-    if (i < 16) {           // Q: row tile w & 1, k tile 16 (w >> 1) + i
+    if (i < 16) {           // Q: row tile i >> 3, k tile 8 w + (i & 7)
         // group row 32 q: queries of heads 2g, 2g+1 (stacked rows 256 g ..), k (2048 + 128 g ..), v (3072 + 128 g ..)
         const int gr = 32 * q;
         const int row = gr < 256 ? 256 * g + gr : (gr < 384 ? 2048 + 128 * g + (gr - 256) : 3072 + 128 * g + (gr - 384));
-        const int kt = 16 * (w >> 1) + i;
-        src = wqkv + (long)(row + 16 * (w & 1) + rl) * RL_H + 32 * kt + kl;
+        const int kt = 8 * w + (i & 7);
+        src = wqkv + (long)(row + 16 * (i >> 3) + rl) * RL_H + 32 * kt + kl;
     } else if (i < 24) {    // O: rows 64 q + 16 w, columns 256 g + 32 kt
         const int kt = i - 16;
         src = wo + (long)(RL_SO * q + 16 * w + rl) * 2048 + 256 * g + 32 * kt + kl;
