@@ -909,12 +909,14 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                     lmw[j][c] = ld_stream16(a.emb + (long)min(row, lm1 - 1) * RL_H + c * 512 + lane * 8);
             }
             const unsigned tp = rl_tag(a, s, L - 1, 6);
-            const bool ok = rl_residual(a, S, a.xd + (tl * WG) * RL_H, tp, a.xs + (tl * WG + g) * RL_H, tp,
-                                        a.xlb + (team * WG + g) * RL_H, rl_tag(a, s, L, 7), nullptr, q, wave, lane,
-                                        tracing ? trb + RL_TM * L + 1 : nullptr, tracing ? trb + RL_TM * L + 2 : nullptr);
-            if (!ok) return;
+            // one barrier publishes the gathered residual, the sums of squares
+            // and every wave's final-norm weight DMA
+            rl_residual<false>(a, S, a.xd + (tl * WG) * RL_H, tp, a.xs + (tl * WG + g) * RL_H, tp,
+                               a.xlb + (team * WG + g) * RL_H, rl_tag(a, s, L, 7), nullptr, q, wave, lane,
+                               tracing ? trb + RL_TM * L + 1 : nullptr, tracing ? trb + RL_TM * L + 2 : nullptr);
             rl_wait_vm();
             rl_sync();
+            if (S.abort_) return;
             rl_norm(a, S, S.fnw, nullptr, S.xn, wave, lane);
             rl_sync();
             if (g == 0 && r == 0 && a.hidden_out)
