@@ -221,11 +221,12 @@ int qwen_hip_decoder_read_trace(qwen_hip_decoder *dec, uint64_t *out, size_t n);
  *
  * Relay trace layout (read_trace returns 704 words per block): for layer l
  * of the block's team (team 0 even layers, team 1 odd), words 24*l + {0 input
- * wait entered, 1 cross-XCD half of the input residual in, 2 input residual
- * gathered, 4 Q stored, 5 q|k|v gathered, 6 attention entered, 7 fold done,
- * 8 split partials stored, 9 merge slices in, 10 merged dims stored,
- * 11 merged attention gathered, 12 O stored, 13 cross-XCD half of the
- * post-attention residual in, 14 post-attention residual gathered, 16 gate|up
+ * wait entered, 1 cross-XCD half of the input residual in, 2 wave 0's
+ * quarter of the input residual gathered, 4 Q stored, 5 q|k|v gathered,
+ * 6 attention entered, 7 fold done, 8 split partials stored, 9 merge slices
+ * in, 10 merged dims stored, 11 merged attention gathered, 12 O stored,
+ * 13 cross-XCD half of the post-attention residual in, 14 wave 0's quarter
+ * of the post-attention residual gathered, 16 gate|up
  * products reduced, 17 SwiGLU stored, 18 SwiGLU outputs gathered, 19 down
  * stored, 20 next layer's loads issued} (3 and 15 repeat 2 and 14); then
  * 24*layers + {0 LM entered, 1 final residual cross half in, 2 gathered,

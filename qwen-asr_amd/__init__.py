@@ -588,7 +588,7 @@ class Stream:
 # layout): name, first stamp, last stamp.  Each is the median over the blocks of
 # the team that computes the layer.
 RELAY_STAGES = (
-    ("input: residual gathered, planes written", 1, 3),
+    ("input: wave 0's quarter of the residual gathered, planes written", 1, 3),
     ("Q product stored", 3, 4),
     ("hop Q -> attention (512 words)", 4, 5),
     ("attention: q/k norm + RoPE + fold", 5, 7),
@@ -598,7 +598,7 @@ RELAY_STAGES = (
     ("hop merged dims -> every block (256 words)", 10, 11),
     ("O product stored", 11, 12),
     ("hop O partials: cross-XCD half in", 12, 13),
-    ("post-attention residual gathered, planes written", 13, 15),
+    ("post-attention: wave 0's quarter gathered, planes written", 13, 15),
     ("gate|up products reduced", 15, 16),
     ("SwiGLU stored", 16, 17),
     ("hop SwiGLU -> down (384 words)", 17, 18),

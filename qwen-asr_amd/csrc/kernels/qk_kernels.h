@@ -281,11 +281,11 @@ typedef struct {
 
 /* Trace points per block (100 MHz wall clock), written by wave 0 for the
  * block's own layers l at 24*l + {0: input wait entered, 1: cross-XCD half of
- * the input residual in, 2: input residual gathered (planes of x*w written),
+ * the input residual in, 2: wave 0's quarter of the input residual gathered (planes of x*w written; the product's barrier follows),
  * 3: = 2, 4: Q stored, 5: q|k|v gathered, 6: attention entered, 7: fold done,
  * 8: split partials stored, 9: merge slices in, 10: merged dims stored,
  * 11: merged output gathered, 12: O stored, 13: cross-XCD half of the
- * post-attention residual in, 14: post-attention residual gathered, 15: = 14,
+ * post-attention residual in, 14: wave 0's quarter of the post-attention residual gathered, 15: = 14,
  * 16: gate|up products reduced, 17: SwiGLU stored, 18: SwiGLU outputs
  * gathered, 19: down stored, 20: next layer's loads issued}; and at
  * 24*layers + {0: LM entered, 1: final residual cross half in, 2: final
