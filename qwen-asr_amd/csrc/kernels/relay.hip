@@ -376,7 +376,7 @@ struct RlShared {
         };
         float red[RL_NW][48];       // per-wave product partials
     };
-    float part[QK_RL_TEAM * 18];    // (m, l, o[16]) of every split for this block's merge dims
+    float pw[RL_NW][6 * QK_RL_TEAM];  // per wave: (m, l, o[4]) of every split for the wave's 4 merge dims
     float cand[2 * 256];            // LM-head candidates
     float ssq[RL_NW];
     float wv[RL_NW];
@@ -758,37 +758,36 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
 
             // ---- M: rank q merges dims [16 q, 16 q + 16) of the group's 256 over every split ----
             {
-                const int h = q >> 3, d0 = 16 * (q & 7);
+                // wave w merges dims d0 .. d0 + 3 and polls just their words: no barrier
+                const int h = q >> 3, d0 = 16 * (q & 7) + 4 * wave;
                 const u64 *src = a.xa + ((t * WG + g) * QK_RL_TEAM) * (long)QK_RL_PART + h * 130;
-                // word 18 i + k: split i's m (k 0), l (k 1), o[d0 + k - 2] (k 2..17)
-                const int nw = 18 * sp.nsplit;
+                // word 6 i + k: split i's m (k 0), l (k 1), o[d0 + k - 2] (k 2..5)
+                const int nw = 6 * sp.nsplit;
                 const bool ok = rl_poll<2>(
                     a, src,
                     [&](int i) {
-                        const int si = i / 18, k = i - 18 * si;
+                        const int si = i / 6, k = i - 6 * si;
                         return si * QK_RL_PART + (k < 2 ? k : d0 + k);
                     },
-                    128 * wave, min(nw, 128 * wave + 128), T(1), [&](int i, float v) { S.part[i] = v; }, lane);
+                    0, nw, T(1), [&](int i, float v) { S.pw[wave][i] = v; }, lane);
                 if (!ok) S.abort_ = 1;
-                rl_sync();
-                if (S.abort_) return;
                 mark(RL_TM * l + 9);
                 {
                     // 16 dims x 16 splits on the block's 256 lanes: lane (4 wave + lane / 16, lane % 16) holds
                     // split lane % 16 of dim d0 + 4 wave + lane / 16; max, sum and weighted sum over the 16-lane
                     // row (the online merge of qwen_causal_attention_heads' running max and sum,
                     // qwen_asr_kernels.c:1073-1094, taken over the splits at once)
-                    const int dl = 4 * wave + (lane >> 4), si = lane & 15;
+                    const int dl = lane >> 4, si = lane & 15;
                     const bool in = si < sp.nsplit;
-                    const float mv = in ? S.part[si * 18] : -INFINITY;
-                    const float lv = in ? S.part[si * 18 + 1] : 0.0f;
-                    const float ov = in ? S.part[si * 18 + 2 + dl] : 0.0f;
+                    const float mv = in ? S.pw[wave][si * 6] : -INFINITY;
+                    const float lv = in ? S.pw[wave][si * 6 + 1] : 0.0f;
+                    const float ov = in ? S.pw[wave][si * 6 + 2 + dl] : 0.0f;
                     const float M = group_max<16>(mv);
                     const float e = (mv == -INFINITY) ? 0.0f : __expf(mv - M);
                     const float Lh = group_sum<16>(lv * e);
                     const float acc = group_sum<16>(ov * e);
                     // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
-                    if (si == 0) rl_put_local(a.xm + (t * WG + g) * 256 + h * 128 + d0 + dl, acc * (1.0f / Lh), T(2));
+                    if (si == 0 && ok) rl_put_local(a.xm + (t * WG + g) * 256 + h * 128 + d0 + dl, acc * (1.0f / Lh), T(2));
                 }
                 mark(RL_TM * l + 10);
                 const bool ok2 = rl_poll<1>(
