@@ -194,7 +194,9 @@ unsigned qwen_hip_decoder_tag_epoch(const qwen_hip_decoder *dec);
  * 2 attention entered, 3 its input ready, 4 O entered, 5 ready, 6 MLP entered,
  * 7 ready, 8 down entered, 9 ready}, then 10*layers + {0 LM head entered,
  * 1 ready, 2 token reduction entered, 3 token ready}; "entered" means the
- * block's compute of the previous stage is done.  Compute-side stamps of
+ * block's compute of the previous stage is done (for the 1.7B shape, the
+ * attention and down entries are where the sync wave starts polling, while
+ * the previous dot may still run).  Compute-side stamps of
  * layer l sit at 320 + 10*l + {0 QKV dot done, 1 its stores and the next
  * prefetches issued, 2 q/k norm done, 3 attention fold done, 4 split partial
  * stored, 5 splits merged, 6 O dot done, 7 O stores and prefetches issued,

@@ -367,6 +367,13 @@ struct PxShared {
     static constexpr int SO = H / QK_PX_LOC;    // O / down rows per block
     static constexpr int HG = I / QK_PX_XCD;    // SwiGLU outputs per XCD group
     static constexpr int NG = NCW * 4;          // 16-lane attention groups
+    // 1.7B: the sync wave starts the q|k|v and SwiGLU polls without the
+    // stage-entry barrier (those polls fill S.qkv / S.hs, which the compute
+    // waves' dot still running then does not read): C3 1005 -> 1015 tok/s.
+    // 0.6B keeps it (2128 -> 2121 without), and both keep the Q and F entries,
+    // which also place the slab loads against the x-update polls (C3 1001
+    // with those removed too)
+    static constexpr bool EARLY_POLL = NCW != 4;
     float xs[H];                                // residual (kept identical in every block)
     float xn[H];                                // normed input of Q / F / LM head
     float nw[H];                                // norm weight of the pending RMSNorm (sync wave)
@@ -517,6 +524,7 @@ __device__ __forceinline__ void px_load_norm(const float *p, float *dst, int lan
 template <int H, int I, int NCW>
 __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, int lane) {
     constexpr int HG = PxShared<H, I, NCW>::HG;
+    constexpr bool EARLY_POLL = PxShared<H, I, NCW>::EARLY_POLL;
     const int L = a.layers, b = blockIdx.x;
     const long WG = (long)QK_PX_XCD;
 
@@ -587,7 +595,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             if (S.abort_) return;
 
             // ---- A: the group's q|q|k|v ----
-            px_sync();
+            if (!EARLY_POLL) px_sync();
             mark(10 * l + 2);
             {
                 const u64 *src = a.xq + (par * WG + g) * 512;
@@ -626,7 +634,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
             if (S.abort_) return;
 
             // ---- D: the group's SwiGLU outputs ----
-            px_sync();
+            if (!EARLY_POLL) px_sync();
             mark(10 * l + 8);
             {
                 const u64 *src = a.xh + (par * WG + g) * HG;
@@ -847,7 +855,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             mark(1);
 
             // ---- A: q/k norm + RoPE + K/V append + attention split (qwen_asr_decoder.c:439-455) ----
-            px_sync();
+            if (!PxShared<H, I, NCW>::EARLY_POLL) px_sync();
             px_sync();
             if (S.abort_) return;
             if (wave < 3) {
@@ -1060,7 +1068,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
             }
 
             // ---- D: this block's rows of W_down over the group's columns (:467-468) ----
-            px_sync();
+            if (!PxShared<H, I, NCW>::EARLY_POLL) px_sync();
             if (!DEEP) wd.load(Wd(l), I, wave, lane);
             px_sync();
             if (S.abort_) return;
