@@ -370,7 +370,7 @@ struct PxShared {
     // 1.7B: the sync wave starts the q|k|v and SwiGLU polls without the
     // stage-entry barrier (those polls fill S.qkv / S.hs, which the compute
     // waves' dot still running then does not read): C3 1005 -> 1015 tok/s.
-    // 0.6B keeps it (2128 -> 2121 without), and both keep the Q and F entries,
+    // 0.6B keeps it (2128 -> 2121 without, C4 1157 -> 1148), and both keep the Q and F entries,
     // which also place the slab loads against the x-update polls (C3 1001
     // with those removed too)
     static constexpr bool EARLY_POLL = NCW != 4;
