@@ -231,7 +231,7 @@ int qk_persist_launch(const qk_persist_args *a, int hidden, int inter, hipStream
 #define QK_RL_TILES 60                     /* weight tiles per wave per layer */
 #define QK_RL_TILE_BYTES 1024
 #define QK_RL_KVP 64                       /* cached positions per split (held in LDS) */
-#define QK_RL_MIN_CHUNK 32                 /* positions per split, at least */
+#define QK_RL_MIN_CHUNK 16                 /* positions per split, at least */
 #define QK_RL_MAX_SEQ (QK_RL_TEAM * QK_RL_KVP) /* the kernel attends over at most this many keys */
 #define QK_RL_TPL 8                        /* exchange tags per layer */
 #define QK_RL_PART 260                     /* words per split: 2 heads x (m, l, o[128]) */
