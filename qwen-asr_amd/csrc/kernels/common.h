@@ -53,19 +53,29 @@ __device__ __forceinline__ uint4 ld_stream16(const uint16_t *p) {
 // v_permlane32_swap exchange rows.  dpp<CTRL>(v): lane i reads lane f(i):
 //   0xB1 quad_perm [1,0,3,2] (xor 1)      0x4E quad_perm [2,3,0,1] (xor 2)
 //   0x104 row_shl:4 (i+4)   0x114 row_shr:4 (i-4)   0x128 row_ror:8 (xor 8)
-//   0x124 row_ror:4
+//   0x124 row_ror:4   0x140 row_mirror (15 - i)   0x141 row_half_mirror (7 - i
+//   within each 8 lanes)
 // ---------------------------------------------------------------------------
 template <int CTRL, int BANKS = 0xF>
 __device__ __forceinline__ float dpp_mov(float old, float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, 0xF, BANKS, false));
 }
 
+// v of lane f(i) for a CTRL under which every lane reads a lane of its own
+// row (quad_perm, row_ror, row_mirror, row_half_mirror).  With old 0 and
+// bound_ctrl the compiler folds the move into the VALU op that uses it
+// (one v_add_f32_dpp instead of a copy, a v_mov_b32_dpp and a v_add_f32).
+template <int CTRL>
+__device__ __forceinline__ float dpp_read(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
 // value of lane (i ^ M) for M in {1, 2, 4, 8}
 template <int M>
 __device__ __forceinline__ float xor_lane(float v) {
-    if (M == 1) return dpp_mov<0xB1>(v, v);
-    if (M == 2) return dpp_mov<0x4E>(v, v);
-    if (M == 8) return dpp_mov<0x128>(v, v);
+    if (M == 1) return dpp_read<0xB1>(v);
+    if (M == 2) return dpp_read<0x4E>(v);
+    if (M == 8) return dpp_read<0x128>(v);
     // M == 4: lanes with bit 2 clear read i+4 (banks 0, 2), the others i-4 (banks 1, 3)
     float t = dpp_mov<0x104, 0x5>(v, v);
     return dpp_mov<0x114, 0xA>(t, v);
@@ -86,13 +96,17 @@ __device__ __forceinline__ void swap16(float &a, float &b) {
 }
 
 // Sum over each aligned group of G lanes (G a power of two <= 64); every lane
-// of the group receives the group's sum.
+// of the group receives the group's sum, the same bits in every lane.  The
+// xor 4 and xor 8 steps read through the mirrors: after the xor 1, 2 steps
+// every quad is uniform, so lane 7 - i of the 8 holds the value of lane i ^ 4;
+// after the xor 4 step every 8 lanes are, so lane 15 - i holds that of i ^ 8.
+// Each step is one DPP add.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
     if (G >= 2) v += xor_lane<1>(v);
     if (G >= 4) v += xor_lane<2>(v);
-    if (G >= 8) v += xor_lane<4>(v);
-    if (G >= 16) v += xor_lane<8>(v);
+    if (G >= 8) v += dpp_read<0x141>(v);
+    if (G >= 16) v += dpp_read<0x140>(v);
     if (G >= 32) { float a = v, b = v; swap16(a, b); v = a + b; }
     if (G >= 64) { float a = v, b = v; swap32(a, b); v = a + b; }
     return v;
@@ -100,12 +114,13 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
+// Maximum over each aligned group of G lanes, steps as group_sum's.
 template <int G>
 __device__ __forceinline__ float group_max(float v) {
     if (G >= 2) v = fmaxf(v, xor_lane<1>(v));
     if (G >= 4) v = fmaxf(v, xor_lane<2>(v));
-    if (G >= 8) v = fmaxf(v, xor_lane<4>(v));
-    if (G >= 16) v = fmaxf(v, xor_lane<8>(v));
+    if (G >= 8) v = fmaxf(v, dpp_read<0x141>(v));
+    if (G >= 16) v = fmaxf(v, dpp_read<0x140>(v));
     if (G >= 32) { float a = v, b = v; swap16(a, b); v = fmaxf(a, b); }
     if (G >= 64) { float a = v, b = v; swap32(a, b); v = fmaxf(a, b); }
     return v;
