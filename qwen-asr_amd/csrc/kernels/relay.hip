@@ -59,7 +59,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 #define RL_NW QK_RL_WAVES
 #define RL_HG (RL_I / RL_XCD)       // 384 SwiGLU outputs per XCD
 #define RL_SO (RL_H / QK_RL_TEAM)   // 64 O / down rows per block
-#define RL_NG 16                    // 16-lane attention groups (waves 0-3)
+#define RL_NG 8                     // 32-lane attention groups (two per wave)
 #define RL_TM 24                    // trace stamps per layer
 static_assert(QK_RL_TRACE <= QK_PX_TRACE, "the two persistent kernels share one trace buffer");
 
@@ -267,72 +267,65 @@ __device__ __forceinline__ void rl_plane2(RlPlanes<K> &P, int i, float v0, float
 // ---------------------------------------------------------------------------
 // attention helpers
 // ---------------------------------------------------------------------------
-// online-softmax fold of one key/value position into both query heads
+// online-softmax fold of one key/value position into the lane's query head
 // (qwen_causal_attention_heads, qwen_asr_kernels.c:1073-1089)
-__device__ __forceinline__ void rl_fold1(const float (&q)[2][8], float4 k0, float4 k1, float4 v0, float4 v1, float scale,
-                                         float (&m)[2], float (&l)[2], float (&o)[2][8]) {
+__device__ __forceinline__ void rl_fold1(const float (&q)[8], float4 k0, float4 k1, float4 v0, float4 v1, float scale,
+                                         float &m, float &l, float (&o)[8]) {
     const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
     const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float d = 0.0f;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        float d = 0.0f;
+    for (int j = 0; j < 8; j++) d = fmaf(q[j], kv[j], d);
+    d = group_sum<16>(d);
+    const float sc = d * scale;
+    const float mn = fmaxf(m, sc);
+    const float corr = __expf(m - mn), pw = __expf(sc - mn);
+    l = fmaf(l, corr, pw);
 #pragma unroll
-        for (int j = 0; j < 8; j++) d = fmaf(q[h][j], kv[j], d);
-        d = group_sum<16>(d);
-        const float sc = d * scale;
-        const float mn = fmaxf(m[h], sc);
-        const float corr = __expf(m[h] - mn), pw = __expf(sc - mn);
-        l[h] = fmaf(l[h], corr, pw);
-#pragma unroll
-        for (int j = 0; j < 8; j++) o[h][j] = fmaf(o[h][j], corr, pw * vv[j]);
-        m[h] = mn;
-    }
+    for (int j = 0; j < 8; j++) o[j] = fmaf(o[j], corr, pw * vv[j]);
+    m = mn;
 }
 
 // NB positions at once: independent scores, one max / rescale per batch.
 template <int NB>
-__device__ __forceinline__ void rl_fold_n(const float (&q)[2][8], const float4 (&k)[NB][2], const float4 (&v)[NB][2],
-                                          const bool (&in)[NB], float scale, float (&m)[2], float (&l)[2],
-                                          float (&o)[2][8]) {
+__device__ __forceinline__ void rl_fold_n(const float (&q)[8], const float4 (&k)[NB][2], const float4 (&v)[NB][2],
+                                          const bool (&in)[NB], float scale, float &m, float &l, float (&o)[8]) {
+    float sc[NB];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        float sc[NB];
+    for (int i = 0; i < NB; i++) {
+        const float kv[8] = {k[i][0].x, k[i][0].y, k[i][0].z, k[i][0].w, k[i][1].x, k[i][1].y, k[i][1].z, k[i][1].w};
+        float d = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NB; i++) {
-            const float kv[8] = {k[i][0].x, k[i][0].y, k[i][0].z, k[i][0].w, k[i][1].x, k[i][1].y, k[i][1].z, k[i][1].w};
-            float d = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) d = fmaf(q[h][j], kv[j], d);
-            sc[i] = d;
-        }
-#pragma unroll
-        for (int i = 0; i < NB; i++) sc[i] = group_sum<16>(sc[i]);
-        float mn = m[h];
-#pragma unroll
-        for (int i = 0; i < NB; i++) {
-            sc[i] = in[i] ? sc[i] * scale : -INFINITY;
-            mn = fmaxf(mn, sc[i]);
-        }
-        const float corr = (mn == m[h]) ? 1.0f : __expf(m[h] - mn);
-        float p[NB], ps = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NB; i++) {
-            p[i] = in[i] ? __expf(sc[i] - mn) : 0.0f;
-            ps += p[i];
-        }
-        l[h] = fmaf(l[h], corr, ps);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            float acc = o[h][j] * corr;
-#pragma unroll
-            for (int i = 0; i < NB; i++) {
-                const float vj = j < 4 ? (&v[i][0].x)[j] : (&v[i][1].x)[j - 4];
-                acc = fmaf(p[i], vj, acc);
-            }
-            o[h][j] = acc;
-        }
-        m[h] = mn;
+        for (int j = 0; j < 8; j++) d = fmaf(q[j], kv[j], d);
+        sc[i] = d;
     }
+#pragma unroll
+    for (int i = 0; i < NB; i++) sc[i] = group_sum<16>(sc[i]);
+    float mn = m;
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        sc[i] = in[i] ? sc[i] * scale : -INFINITY;
+        mn = fmaxf(mn, sc[i]);
+    }
+    const float corr = (mn == m) ? 1.0f : __expf(m - mn);
+    float p[NB], ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        p[i] = in[i] ? __expf(sc[i] - mn) : 0.0f;
+        ps += p[i];
+    }
+    l = fmaf(l, corr, ps);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float acc = o[j] * corr;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const float vj = j < 4 ? (&v[i][0].x)[j] : (&v[i][1].x)[j - 4];
+            acc = fmaf(p[i], vj, acc);
+        }
+        o[j] = acc;
+    }
+    m = mn;
 }
 
 // The split of positions [0, pos] team rank q works on; cached positions
@@ -663,40 +656,40 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
             mark(RL_TM * l + 6);
             // causal attention of the group's two query heads over this block's
             // positions (qwen_causal_attention_heads, qwen_asr_kernels.c:1050-1097):
-            // 16-lane group gid folds positions s0 + gid + 16 j from LDS; lane c
-            // of the group owns dims 4c .. 4c+3 and 64+4c .. 64+4c+3, so a group's
-            // 16-byte reads of one K or V row cover 256 contiguous bytes
-            // Every group normalises and rotates the two query heads itself (no
-            // stage of its own): rms_norm_per_head (qwen_asr_kernels.c:811-873) +
-            // apply_rope_neox (:1182-1247); the RoPE pair (d, d + 64) sits in one lane.
+            // 32-lane group gid (two per wave) folds positions s0 + gid + 8 j from
+            // LDS; its lane row (lane / 16) & 1 holds query head 2g + that bit, and
+            // lane c of the row owns dims 4c .. 4c+3 and 64+4c .. 64+4c+3, so a
+            // row's 16-byte reads of one K or V row cover 256 contiguous bytes (the
+            // group's two rows read the same bytes).  Every row normalises and
+            // rotates its query head itself (no stage of its own):
+            // rms_norm_per_head (qwen_asr_kernels.c:811-873) + apply_rope_neox
+            // (:1182-1247); the RoPE pair (d, d + 64) sits in one lane.
             if (sp.active) {
-                const int gid = wave * 4 + (lane >> 4), gl = lane & 15, d0 = 4 * gl, d1 = 64 + 4 * gl;
+                const int hq = (lane >> 4) & 1, gid = wave * 2 + (lane >> 5), gl = lane & 15, d0 = 4 * gl,
+                          d1 = 64 + 4 * gl;
                 const float4 c4 = *reinterpret_cast<const float4 *>(&S.rope[d0]);
                 const float4 s4 = *reinterpret_cast<const float4 *>(&S.rope[128 + d0]);
-                float qv[2][8];
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    float4 lo = *reinterpret_cast<const float4 *>(&S.qkv[h * 128 + d0]);
-                    float4 hi = *reinterpret_cast<const float4 *>(&S.qkv[h * 128 + d1]);
+                float qv[8];
+                {
+                    float4 lo = *reinterpret_cast<const float4 *>(&S.qkv[hq * 128 + d0]);
+                    float4 hi = *reinterpret_cast<const float4 *>(&S.qkv[hq * 128 + d1]);
                     norm_rope_row16(lo, hi, *reinterpret_cast<const float4 *>(&S.nqk[d0]),
                                     *reinterpret_cast<const float4 *>(&S.nqk[d1]), c4, s4, a.eps);
-                    qv[h][0] = lo.x; qv[h][1] = lo.y; qv[h][2] = lo.z; qv[h][3] = lo.w;
-                    qv[h][4] = hi.x; qv[h][5] = hi.y; qv[h][6] = hi.z; qv[h][7] = hi.w;
+                    qv[0] = lo.x; qv[1] = lo.y; qv[2] = lo.z; qv[3] = lo.w;
+                    qv[4] = hi.x; qv[5] = hi.y; qv[6] = hi.z; qv[7] = hi.w;
                 }
-                float m[2] = {-INFINITY, -INFINITY}, ls[2] = {0.f, 0.f}, o[2][8];
+                float m = -INFINITY, ls = 0.f, o[8];
 #pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int j = 0; j < 8; j++) o[h][j] = 0.f;
+                for (int j = 0; j < 8; j++) o[j] = 0.f;
                 const int nc = sp.cend - sp.s0;
 #pragma unroll
-                for (int half = 0; half < 2; half++) {
-                    if (half == 1 && nc <= 2 * RL_NG) break;   // block-uniform: no position of the second half
+                for (int b = 0; b < 4; b++) {
+                    if (b > 0 && nc <= 2 * RL_NG * b) break;   // block-uniform: no position from here on
                     float4 kk[2][2], vv[2][2];
                     bool in[2];
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
-                        const int jj = gid + RL_NG * (2 * half + j);
+                        const int jj = gid + RL_NG * (2 * b + j);
                         in[j] = jj < nc;
                         const float *row = kv[in[j] ? jj : 0];
                         kk[j][0] = *reinterpret_cast<const float4 *>(row + d0);
@@ -713,21 +706,20 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                                     *reinterpret_cast<const float4 *>(&S.nqk[128 + d1]), c4, s4, a.eps);
                     const float4 v0 = *reinterpret_cast<const float4 *>(&S.qkv[384 + d0]);
                     const float4 v1 = *reinterpret_cast<const float4 *>(&S.qkv[384 + d1]);
-                    *reinterpret_cast<float4 *>(kcl + (long)pos * 128 + d0) = k0;
-                    *reinterpret_cast<float4 *>(kcl + (long)pos * 128 + d1) = k1;
-                    *reinterpret_cast<float4 *>(vcl + (long)pos * 128 + d0) = v0;
-                    *reinterpret_cast<float4 *>(vcl + (long)pos * 128 + d1) = v1;
+                    if (hq == 0) {
+                        *reinterpret_cast<float4 *>(kcl + (long)pos * 128 + d0) = k0;
+                        *reinterpret_cast<float4 *>(kcl + (long)pos * 128 + d1) = k1;
+                        *reinterpret_cast<float4 *>(vcl + (long)pos * 128 + d0) = v0;
+                        *reinterpret_cast<float4 *>(vcl + (long)pos * 128 + d1) = v1;
+                    }
                     rl_fold1(qv, k0, k1, v0, v1, a.scale, m, ls, o);
                 }
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    if (gl == 0) {
-                        S.sm_m[gid][h] = m[h];
-                        S.sm_l[gid][h] = ls[h];
-                    }
-                    *reinterpret_cast<float4 *>(&S.sm_o[gid][h][d0]) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-                    *reinterpret_cast<float4 *>(&S.sm_o[gid][h][d1]) = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+                if (gl == 0) {
+                    S.sm_m[gid][hq] = m;
+                    S.sm_l[gid][hq] = ls;
                 }
+                *reinterpret_cast<float4 *>(&S.sm_o[gid][hq][d0]) = make_float4(o[0], o[1], o[2], o[3]);
+                *reinterpret_cast<float4 *>(&S.sm_o[gid][hq][d1]) = make_float4(o[4], o[5], o[6], o[7]);
             }
             rl_sync();
             mark(RL_TM * l + 7);
