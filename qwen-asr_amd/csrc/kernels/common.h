@@ -188,10 +188,21 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) 
     return v > bv || (v == bv && i < bi);
 }
 
-// SiLU(g) * u as the reference writes it (qwen_asr_kernels.c:930-931).
+// SiLU(g) * u as the reference writes it (qwen_asr_kernels.c:930-931), the
+// division as a product with the hardware reciprocal (v_rcp_f32, within
+// 1 ulp; the reference's -ffast-math build, Makefile:5, does not divide
+// exactly either).  g -> -inf: 1 / inf = 0, the reference's -0 as well.
 __device__ __forceinline__ float swiglu1(float g, float u) {
-    return (g / (1.0f + expf(-g))) * u;
+    return (g * __builtin_amdgcn_rcpf(1.0f + expf(-g))) * u;
 }
+
+// 1 / sqrt(x) of the RMS norms (qwen_asr_kernels.c:783, :846): the hardware
+// reciprocal square root (v_rsq_f32, within 1 ulp) instead of a correctly
+// rounded square root and division (about 24 dependent instructions on the
+// norm's critical path).  The reference's build (-ffast-math, Makefile:5)
+// computes 1.0f / sqrtf(x) with an approximate reciprocal square root too.
+// x >= eps > 0 here, never denormal.
+__device__ __forceinline__ float rsqrt_norm(float x) { return __builtin_amdgcn_rsqf(x); }
 
 
 // ---------------------------------------------------------------------------
@@ -252,7 +263,7 @@ __device__ __forceinline__ void norm_rope_row16(float4 &lo, float4 &hi, float4 w
     ss = fmaf(lo.w, lo.w, ss);
     ss = fmaf(hi.w, hi.w, ss);
     ss = group_sum<16>(ss);
-    const float rinv = 1.0f / sqrtf(ss / 128.0f + eps);
+    const float rinv = rsqrt_norm(ss / 128.0f + eps);
     const float a0 = (lo.x * wl.x) * rinv, a1 = (lo.y * wl.y) * rinv, a2 = (lo.z * wl.z) * rinv,
                 a3 = (lo.w * wl.w) * rinv;
     const float b0 = (hi.x * wh.x) * rinv, b1 = (hi.y * wh.y) * rinv, b2 = (hi.z * wh.z) * rinv,
@@ -287,7 +298,7 @@ __device__ __forceinline__ float4 sum_splits4(const float *p, int n, long stride
 __device__ __forceinline__ void norm_rope_pair(float &x1, float &x2, const float *nw, float eps, float c, float sn,
                                                int lane) {
     float ss = wave_sum(fmaf(x1, x1, x2 * x2));
-    const float rinv = 1.0f / sqrtf(ss / 128.0f + eps);
+    const float rinv = rsqrt_norm(ss / 128.0f + eps);
     const float a = (x1 * nw[lane]) * rinv, b = (x2 * nw[lane + 64]) * rinv;
     x1 = fmaf(a, c, -(b * sn));
     x2 = fmaf(b, c, a * sn);

@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(qk_gemv_args a, int iters_arg
 #pragma unroll
             for (int j = 0; j < 8; j++) ss = fmaf(xr[c][j], xr[c][j], ss);
         ss = wave_sum(ss);
-        const float rinv = 1.0f / sqrtf(ss / (float)K + a.eps);
+        const float rinv = rsqrt_norm(ss / (float)K + a.eps);
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const int col = c * 512 + lane * 8;

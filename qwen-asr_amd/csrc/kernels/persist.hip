@@ -454,7 +454,7 @@ __device__ void px_rmsnorm(const qk_persist_args &a, PxShared<H, I, NCW> &S, con
         }
     }
     ss = wave_sum(ss);
-    const float rinv = 1.0f / sqrtf(ss / (float)H + a.eps);
+    const float rinv = rsqrt_norm(ss / (float)H + a.eps);
 #pragma unroll
     for (int j = 0; j < H / 64; j++) S.xn[j * 64 + lane] = (S.xs[j * 64 + lane] * w[j * 64 + lane]) * rinv;
 }
@@ -863,7 +863,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 float x1 = src[lane], x2 = src[lane + 64];
                 // rms_norm_per_head (qwen_asr_kernels.c:811-873) + apply_rope_neox (:1182-1247)
                 const float ss = wave_sum(fmaf(x1, x1, x2 * x2));
-                const float rinv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+                const float rinv = rsqrt_norm(ss / 128.0f + a.eps);
                 const float p1 = (x1 * nw1) * rinv, p2 = (x2 * nw2) * rinv;
                 x1 = fmaf(p1, rc, -(p2 * rs));
                 x2 = fmaf(p2, rc, p1 * rs);

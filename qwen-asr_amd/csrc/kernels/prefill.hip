@@ -69,7 +69,7 @@ __global__ __launch_bounds__(RN_THREADS) void rmsnorm_split(float *x, const floa
     float rinv = 1.0f;
     if (w) {
         ss = block_sum<RN_THREADS / 64>(ss, red);
-        rinv = 1.0f / sqrtf(ss / (float)D + eps);
+        rinv = rsqrt_norm(ss / (float)D + eps);
     }
     if (!hi) return;
     uint16_t *h = hi + (size_t)blockIdx.x * D, *l = lo + (size_t)blockIdx.x * D;
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(256) void rmsnorm_split_rows(float *x, const float 
             ss = fmaf(v[j].w, v[j].w, ss);
         }
         ss = wave_sum(ss);
-        rinv = 1.0f / sqrtf(ss / (float)D + eps);
+        rinv = rsqrt_norm(ss / (float)D + eps);
     }
     if (!hi) return;
     uint2 *h = reinterpret_cast<uint2 *>(hi + (size_t)row * D) + lane;
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(RN_THREADS) void rmsnorm_split_reg(float *x, const 
     float rinv = 1.0f;
     if (w) {
         ss = block_sum<RN_THREADS / 64>(ss, red);
-        rinv = 1.0f / sqrtf(ss / (float)D + eps);
+        rinv = rsqrt_norm(ss / (float)D + eps);
     }
     if (!hi) return;
     uint16_t *h = hi + (size_t)blockIdx.x * D, *l = lo + (size_t)blockIdx.x * D;
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(256) void rmsnorm_split_vec(float *x, const float *
             ss = fmaf(v[e].w, v[e].w, ss);
         }
         ss = block_sum<4>(ss, red);
-        rinv = 1.0f / sqrtf(ss / (float)D + eps);
+        rinv = rsqrt_norm(ss / (float)D + eps);
     }
     if (!hi) return;
     uint2 *h = reinterpret_cast<uint2 *>(hi + (size_t)blockIdx.x * D) + threadIdx.x;
@@ -984,7 +984,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(float *out, const float *
     float ss = 0.0f;
     for (int i = threadIdx.x; i < D; i += 256) ss = fmaf(xr[i], xr[i], ss);
     ss = block_sum256(ss, red);      // its trailing barrier orders all reads before in-place writes
-    const float rinv = 1.0f / sqrtf(ss / (float)D + eps);
+    const float rinv = rsqrt_norm(ss / (float)D + eps);
     for (int i = threadIdx.x; i < D; i += 256) orow[i] = (xr[i] * w[i]) * rinv;
 }
 
@@ -999,7 +999,7 @@ __global__ __launch_bounds__(64) void rms_norm_head_kernel(float *x, const float
     float ss = 0.0f;
     for (int i = threadIdx.x; i < hd; i += 64) ss = fmaf(v[i], v[i], ss);
     ss = wave_sum(ss);
-    const float rinv = 1.0f / sqrtf(ss / (float)hd + eps);
+    const float rinv = rsqrt_norm(ss / (float)hd + eps);
     for (int i = threadIdx.x; i < hd; i += 64) v[i] = (v[i] * w[i]) * rinv;
 }
 

@@ -487,7 +487,7 @@ __device__ __forceinline__ float rl_rinv(const qk_relay_args &a, const RlShared 
     float ss = S.ssq[0];
 #pragma unroll
     for (int i = 1; i < RL_NW; i++) ss += S.ssq[i];
-    return 1.0f / sqrtf(ss / (float)RL_H + a.eps);
+    return rsqrt_norm(ss / (float)RL_H + a.eps);
 }
 
 // rms_norm(S.xs) * w (qwen_rms_norm, qwen_asr_kernels.c:750-809) from the
@@ -498,7 +498,7 @@ __device__ __forceinline__ void rl_norm(const qk_relay_args &a, RlShared &S, con
     float ss = S.ssq[0];
 #pragma unroll
     for (int i = 1; i < RL_NW; i++) ss += S.ssq[i];
-    const float rinv = 1.0f / sqrtf(ss / (float)RL_H + a.eps);
+    const float rinv = rsqrt_norm(ss / (float)RL_H + a.eps);
     const int i = 256 * wave + 4 * lane;
     const float4 x = *reinterpret_cast<const float4 *>(&S.xs[i]);
     const float4 wv = *reinterpret_cast<const float4 *>(&w[i]);
