@@ -231,8 +231,9 @@ __device__ __forceinline__ bf16x8 rl_afrag(const RlPlanes<K> &P, int kt, int lan
 // The 16 rows of one tile's product in lanes 0..15: hi + mid + lo terms.
 __device__ __forceinline__ float rl_rowsum(f32x4 c) { return (c[0] + c[1]) + c[2]; }
 
-// v = hi + mid + lo exactly: hi and mid truncated to bf16, lo rounded (at most
-// 8 significant bits remain, so it is exact).
+// v = hi + mid + lo exactly: hi and mid truncated to bf16; lo, the rest, has
+// at most 8 significant bits (v's 24 less the 8 of hi and of mid), so its
+// bf16 truncation is exact too (v in the normal range).
 __device__ __forceinline__ void rl_split3(float v, unsigned &h, unsigned &m, unsigned &l) {
     const unsigned hb = __float_as_uint(v) & 0xffff0000u;
     const float r1 = v - __uint_as_float(hb);
@@ -240,7 +241,7 @@ __device__ __forceinline__ void rl_split3(float v, unsigned &h, unsigned &m, uns
     const float r2 = r1 - __uint_as_float(mb);
     h = hb >> 16;
     m = mb >> 16;
-    l = f32_to_bf16_rne(r2);
+    l = __float_as_uint(r2) >> 16;
 }
 
 // planes P at element i of value v
@@ -731,8 +732,10 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                 float Lh = 0.0f, acc = 0.0f;
 #pragma unroll
                 for (int i = 0; i < RL_NG; i++) {
-                    const float mi = S.sm_m[i][h];
-                    const float e = (mi == -INFINITY) ? 0.0f : __expf(mi - M);
+                    // M is finite (every group of a split below the last folds a
+                    // position, and group 0 of the last split folds pos), so a
+                    // group without positions (m = -inf) gets exp(-inf) = 0
+                    const float e = __expf(S.sm_m[i][h] - M);
                     Lh = fmaf(S.sm_l[i][h], e, Lh);
                     acc = fmaf(S.sm_o[i][h][d], e, acc);
                 }
@@ -775,11 +778,12 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                     const float lv = in ? S.pw[wave][si * 6 + 1] : 0.0f;
                     const float ov = in ? S.pw[wave][si * 6 + 2 + dl] : 0.0f;
                     const float M = group_max<16>(mv);
-                    const float e = (mv == -INFINITY) ? 0.0f : __expf(mv - M);
+                    const float e = __expf(mv - M);   // M finite: split 0 is always in
                     const float Lh = group_sum<16>(lv * e);
                     const float acc = group_sum<16>(ov * e);
                     // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
-                    if (si == 0 && ok) rl_put_local(a.xm + (t * WG + g) * 256 + h * 128 + d0 + dl, acc * (1.0f / Lh), T(2));
+                    if (si == 0 && ok)
+                        rl_put_local(a.xm + (t * WG + g) * 256 + h * 128 + d0 + dl, acc * __builtin_amdgcn_rcpf(Lh), T(2));
                 }
                 mark(RL_TM * l + 10);
                 const bool ok2 = rl_poll<1>(
