@@ -592,7 +592,7 @@ RELAY_STAGES = (
     ("Q product stored", 3, 4),
     ("hop Q -> attention (512 words)", 4, 5),
     ("attention: q/k norm + RoPE + fold", 5, 7),
-    ("attention: merge of 16 groups, partials stored", 7, 8),
+    ("attention: merge of 8 groups, partials stored", 7, 8),
     ("hop split partials -> merge slices", 8, 9),
     ("merge over the splits, stored", 9, 10),
     ("hop merged dims -> every block (256 words)", 10, 11),
