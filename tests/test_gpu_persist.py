@@ -229,6 +229,45 @@ def test_relay_vs_split_teacher_forced_06b(qa, dec06):
     first_divergence(ts, tr, ls)
 
 
+def test_relay_split_boundaries(qa, dec06):
+    """The relay kernel against the split kernel on teacher-forced steps
+    across the relay's split layout changes: short contexts (fewer than 16
+    splits, fold groups without positions, a last split that holds only the
+    new position: positions 16, 32, ...), 241 keys (every block of a team
+    folds from here), 256 -> 257 and 512 -> 513 keys (16 -> 17 and 32 -> 33
+    positions per split: a second LDS batch of the fold)."""
+    d, rows = dec06
+    d.set_engine(ENGINE_PERSIST)
+    d.set_fallback(False)
+    try:
+        d.set_kv_len(0)
+        d.prefill(rows[:2])
+        d.generate(d.forward(rows[2]), 530)   # K/V of positions 0..532 in the cache
+        rng = np.random.default_rng(11)
+        for p0, n in ((505, 12), (236, 24), (3, 36)):   # set_kv_len only rolls back: highest window first
+            teach = [int(t) for t in rng.integers(0, 151643, n)]
+            res = {}
+            for relay in (False, True):
+                d.set_relay(relay)
+                d.set_kv_len(p0)
+                d.set_keep_logits(True)
+                toks, logits = [], []
+                for t in teach:
+                    toks.append(d.forward_token(t))
+                    logits.append(d.read_logits())
+                d.set_keep_logits(False)
+                assert d.last_kernel() == (qa.KERNEL_RELAY if relay else qa.KERNEL_SPLIT)
+                res[relay] = (np.array(toks), np.array(logits))
+            err = float(np.abs(res[True][1] - res[False][1]).max())
+            print(f"positions {p0}..{p0 + n - 1}: relay vs split max |dlogit| {err:.2e}")
+            assert err < AGREE, (p0, err)
+            first_divergence(res[False][0], res[True][0], res[False][1])
+        assert d.fallbacks() == 0
+    finally:
+        d.set_relay(True)
+        d.set_fallback(True)
+
+
 @pytest.mark.parametrize("relay", [False, True])
 def test_generate_equals_single_steps_both_kernels(qa, dec06, relay):
     """one launch of n steps == n launches of one step, bit for bit, on each
