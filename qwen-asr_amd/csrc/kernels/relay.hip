@@ -64,6 +64,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 static_assert(QK_RL_TRACE <= QK_PX_TRACE, "the two persistent kernels share one trace buffer");
 
 static_assert(QK_RL_TEAM == 16 && RL_NW == 4 && QK_RL_TILES == 60, "layout constants");
+static_assert(4 * 2 * RL_NG == QK_RL_KVP, "the fold's 4 batches of 2 positions per group cover a split's LDS rows");
 static_assert(QK_RL_KVP * QK_RL_TEAM >= QK_RL_MAX_SEQ && QK_RL_MAX_SEQ == QWEN_HIP_RELAY_MAX_POS, "split capacity");
 
 // ---------------------------------------------------------------------------
