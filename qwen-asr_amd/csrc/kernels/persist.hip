@@ -491,22 +491,26 @@ __device__ bool px_merge_splits(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 lv[j] = in ? pp[1] : 0.0f;
                 ov[j] = in ? pp[2 + lane] : 0.0f;
             }
+            // Mc is finite from the first chunk on (split 0 always folds a
+            // position), so exp(-inf - Mc) = 0 covers M = -inf at the start
+            // and the splits past nsplit
             float Mc = M;
 #pragma unroll
             for (int j = 0; j < 8; j++) Mc = fmaxf(Mc, mv[j]);
-            const float sc = (M == -INFINITY) ? 0.0f : __expf(M - Mc);
+            const float sc = __expf(M - Mc);
             Lh *= sc;
             acc *= sc;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float e = (mv[j] == -INFINITY) ? 0.0f : __expf(mv[j] - Mc);
+                const float e = __expf(mv[j] - Mc);
                 Lh = fmaf(lv[j], e, Lh);
                 acc = fmaf(ov[j], e, acc);
             }
             M = Mc;
         }
-        // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094)
-        px_put_local(xm + h * 128 + d0 + lane, acc * (1.0f / Lh), T + 7u);
+        // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094); a
+        // hardware reciprocal here
+        px_put_local(xm + h * 128 + d0 + lane, acc * __builtin_amdgcn_rcpf(Lh), T + 7u);
     }
     auto whole = [&](int i) { return xm + i; };
     return px_poll<4>(a, whole, 256, T + 7u, S.att, lane);
@@ -968,8 +972,10 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                 float Lh = 0.0f, acc = 0.0f;
 #pragma unroll
                 for (int i = 0; i < NG; i++) {
-                    const float mi = S.sm_m[i][h];
-                    const float e = (mi == -INFINITY) ? 0.0f : __expf(mi - M);
+                    // M is finite (every group of a split below the last folds
+                    // positions, group 0 of the last one folds pos): a group
+                    // without positions (m = -inf) gets exp(-inf) = 0
+                    const float e = __expf(S.sm_m[i][h] - M);
                     Lh = fmaf(S.sm_l[i][h], e, Lh);
                     acc = fmaf(S.sm_o[i][h][d], e, acc);
                 }
