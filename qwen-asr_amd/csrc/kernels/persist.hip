@@ -455,8 +455,16 @@ __device__ void px_rmsnorm(const qk_persist_args &a, PxShared<H, I, NCW> &S, con
     }
     ss = wave_sum(ss);
     const float rinv = rsqrt_norm(ss / (float)H + a.eps);
+    // elementwise, so any lane may take any element: four consecutive ones
+    // per 16-byte access
 #pragma unroll
-    for (int j = 0; j < H / 64; j++) S.xn[j * 64 + lane] = (S.xs[j * 64 + lane] * w[j * 64 + lane]) * rinv;
+    for (int j = 0; j < H / 256; j++) {
+        const int i = 256 * j + 4 * lane;
+        const float4 x = *reinterpret_cast<const float4 *>(&S.xs[i]);
+        const float4 wv = *reinterpret_cast<const float4 *>(&w[i]);
+        *reinterpret_cast<float4 *>(&S.xn[i]) =
+            make_float4((x.x * wv.x) * rinv, (x.y * wv.y) * rinv, (x.z * wv.z) * rinv, (x.w * wv.w) * rinv);
+    }
 }
 
 // Stage O's input, in two hand-overs: block r of the group merges 8 of the
