@@ -128,6 +128,7 @@ __device__ __forceinline__ float group_max(float v) {
 
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
+
 // p[0] + p[stride] + ... + p[(n - 1) stride], 1 <= n <= N, added left to
 // right as a plain loop would; the n loads are issued together, so summing n
 // split-K partials costs one memory latency instead of n.
@@ -186,6 +187,39 @@ __device__ __forceinline__ float xor_sum16_32(float v) {
 // (qwen_asr_kernels.c:534-541).
 __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
+}
+
+// The (value, index) that wins under argmax_better among the 64 lanes, in
+// every lane, with no LDS round trip: the xor 1 / 2 partners by quad_perm,
+// the xor 4 / 8 partners through the mirrors (each quad, then each 8 lanes,
+// hold one winner by then), the xor 16 / 32 partners by the permlane swaps
+// (both swap results are offered: one is the lane's own pair).  argmax_better
+// is a total order, so the step order does not change the winner.
+__device__ __forceinline__ void wave_argmax(float &bv, int &bi) {
+    auto take = [&](float ov, float oi) {
+        if (argmax_better(ov, __float_as_int(oi), bv, bi)) {
+            bv = ov;
+            bi = __float_as_int(oi);
+        }
+    };
+    take(xor_lane<1>(bv), xor_lane<1>(__int_as_float(bi)));
+    take(xor_lane<2>(bv), xor_lane<2>(__int_as_float(bi)));
+    take(dpp_read<0x141>(bv), dpp_read<0x141>(__int_as_float(bi)));
+    take(dpp_read<0x140>(bv), dpp_read<0x140>(__int_as_float(bi)));
+    {
+        float v0 = bv, v1 = bv, i0 = __int_as_float(bi), i1 = __int_as_float(bi);
+        swap16(v0, v1);
+        swap16(i0, i1);
+        take(v0, i0);
+        take(v1, i1);
+    }
+    {
+        float v0 = bv, v1 = bv, i0 = __int_as_float(bi), i1 = __int_as_float(bi);
+        swap32(v0, v1);
+        swap32(i0, i1);
+        take(v0, i0);
+        take(v1, i1);
+    }
 }
 
 // SiLU(g) * u as the reference writes it (qwen_asr_kernels.c:930-931), the

@@ -696,12 +696,7 @@ __device__ void px_sync_role(const qk_persist_args &a, PxShared<H, I, NCW> &S, i
                     const int ix = __float_as_int(S.cand[QK_PX_BLOCKS + i]);
                     if (argmax_better(v, ix, bv, bi)) { bv = v; bi = ix; }
                 }
-#pragma unroll
-                for (int m = 32; m >= 1; m >>= 1) {
-                    const float ov = __shfl_xor(bv, m, 64);
-                    const int oi = __shfl_xor(bi, m, 64);
-                    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-                }
+                wave_argmax(bv, bi);
                 // nothing above the reference's -1e30 floor: it returns its start row
                 const int tok = bi == 0x7fffffff ? 0 : bi;
                 if (lane == 0) {
@@ -1166,12 +1161,7 @@ __device__ void px_compute_role(const qk_persist_args &a, PxShared<H, I, NCW> &S
                         for (int c = 0; c < SEGH; c++) lmw[j][c] = nx[j][c];
                 }
             }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                const float ov = __shfl_xor(bv, m, 64);
-                const int oi = __shfl_xor(bi, m, 64);
-                if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-            }
+            wave_argmax(bv, bi);
             if (lane == 0) { S.wv[wave] = bv; S.wi[wave] = bi; }
         }
         px_sync();

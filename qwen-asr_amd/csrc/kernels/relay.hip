@@ -845,7 +845,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
             if (wave == 0 && lane < 48) {
                 const float y = (((S.red[0][lane] + S.red[1][lane]) + S.red[2][lane]) + S.red[3][lane]) * rl_rinv(a, S);
                 // rows 2i (gate), 2i+1 (up) sit in adjacent lanes (qwen_swiglu_multiply, qwen_asr_kernels.c:930-931)
-                const float up = __shfl_xor(y, 1, 64);
+                const float up = xor_lane<1>(y);
                 if ((lane & 1) == 0)
                     rl_put_local(a.xh + (t * WG + g) * RL_HG + 24 * q + (lane >> 1), swiglu1(y, up), T(5));
             }
@@ -962,15 +962,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                         for (int c = 0; c < 2; c++) lmw[j][c] = nx[j][c];
                 }
             }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                const float ov = __shfl_xor(bv, m, 64);
-                const int oi = __shfl_xor(bi, m, 64);
-                if (argmax_better(ov, oi, bv, bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
+            wave_argmax(bv, bi);
             if (lane == 0) {
                 S.wv[wave] = bv;
                 S.wi[wave] = bi;
@@ -1016,15 +1008,7 @@ __global__ __launch_bounds__(RL_NW * 64, 1) void rl_decode(qk_relay_args a) {
                         bi = ix;
                     }
                 }
-#pragma unroll
-                for (int m = 32; m >= 1; m >>= 1) {
-                    const float ov = __shfl_xor(bv, m, 64);
-                    const int oi = __shfl_xor(bi, m, 64);
-                    if (argmax_better(ov, oi, bv, bi)) {
-                        bv = ov;
-                        bi = oi;
-                    }
-                }
+                wave_argmax(bv, bi);
                 // nothing above the reference's -1e30 floor: it returns its start row
                 const int tok = bi == 0x7fffffff ? 0 : bi;
                 if (lane == 0) {

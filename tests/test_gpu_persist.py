@@ -559,3 +559,50 @@ def test_generate_beside_busy_stream(qa, dec06):
         assert got == ref
     finally:
         d.set_engine(ENGINE_PERSIST)
+
+
+def test_lm_head_exact_ties(qa, gpu):
+    """Exact logit ties resolve to the lowest vocabulary row on every engine,
+    as the reference's strict `>` scan and in-order combine do
+    (qwen_asr_kernels_avx.c:223-226, qwen_asr_kernels.c:534-541).  Rows whose
+    only nonzero weight is 64 at the largest element k of the final normed
+    row all score exactly 64 * xn[k] (every other product adds an exact
+    zero), far above the rest.  The tied rows sit in one 4-row group, in
+    neighbouring groups, and in far-apart groups of different blocks."""
+    cfg = qa.preset(0)
+    cfg.layers = 2
+    d = qa.Decoder(cfg, 0, 128)
+    d.set_fallback(False)
+    d.load_synthetic(5, 0.02, 0.0)
+    base_emb = qa.synth_bf16(cfg.vocab * cfg.hidden, 5, qa.SYNTH_EMBED).reshape(cfg.vocab, cfg.hidden)
+    ones = np.ones(cfg.hidden, np.float32)
+    d.load_embeddings(base_emb, ones)
+    rows, _, _ = qa.prompt_rows(cfg, 30, 4, seed=5, emb=base_emb)
+    d.set_engine(ENGINE_GRAPH)
+    d.prefill(rows[:-1])
+    base = d.kv_len()
+    d.set_keep_logits(True)
+    d.forward(rows[-1])
+    xn = d.read_hidden()
+    k = int(np.argmax(xn))
+    assert xn[k] > 0.5
+    try:
+        for tied in ((151930, 7), (1031, 1027), (40002, 40001), (150000, 70000, 99999)):
+            emb = base_emb.copy()
+            for r in tied:
+                emb[r] = 0
+                emb[r, k] = 0x4280          # bf16 64.0
+            d.load_embeddings(emb, ones)
+            for engine, relay in ((ENGINE_GRAPH, True), (ENGINE_PERSIST, True), (ENGINE_PERSIST, False)):
+                d.set_engine(engine)
+                d.set_relay(relay)
+                d.set_kv_len(base)
+                t = d.forward(rows[-1])
+                lg = d.read_logits()
+                assert lg[tied[0]] == lg[tied[1]], (tied, engine, relay)
+                assert t == min(tied), (tied, engine, relay, t)
+                if engine == ENGINE_PERSIST:
+                    assert d.last_kernel() == (qa.KERNEL_RELAY if relay else qa.KERNEL_SPLIT)
+    finally:
+        d.set_relay(True)
+        d.close()
