@@ -487,38 +487,55 @@ __device__ bool px_merge_splits(const qk_persist_args &a, PxShared<H, I, NCW> &S
     };
     if (!px_poll<QK_PX_MAX_SPLIT * 10 / 64>(a, part, 10 * sp.nsplit, T + 1u, S.part, lane)) return false;
     u64 *xm = a.xm + (par * WG + g) * 256;
-    if (lane < 8) {
+    {
+        // lane (8 sg + dl) folds splits sg, sg + 8, ... of dim d0 + dl; then
+        // the 8 split groups of a dim combine (xor 8 by DPP, xor 16 / 32 by the
+        // permlane swaps).  M is finite from split 0 on, so exp(-inf - M) = 0
+        // covers the lanes and splits without positions.
+        const int dl = lane & 7, sg = lane >> 3;
         float M = -INFINITY, Lh = 0.0f, acc = 0.0f;
-        for (int c0 = 0; c0 < sp.nsplit; c0 += 8) {
-            float mv[8], lv[8], ov[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const bool in = c0 + j < sp.nsplit;
-                const float *pp = S.part + (in ? c0 + j : 0) * 10;
-                mv[j] = in ? pp[0] : -INFINITY;
-                lv[j] = in ? pp[1] : 0.0f;
-                ov[j] = in ? pp[2 + lane] : 0.0f;
-            }
-            // Mc is finite from the first chunk on (split 0 always folds a
-            // position), so exp(-inf - Mc) = 0 covers M = -inf at the start
-            // and the splits past nsplit
-            float Mc = M;
-#pragma unroll
-            for (int j = 0; j < 8; j++) Mc = fmaxf(Mc, mv[j]);
-            const float sc = __expf(M - Mc);
-            Lh *= sc;
-            acc *= sc;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float e = __expf(mv[j] - Mc);
-                Lh = fmaf(lv[j], e, Lh);
-                acc = fmaf(ov[j], e, acc);
-            }
-            M = Mc;
+        for (int i = sg; i < sp.nsplit; i += 8) {
+            const float *pp = S.part + i * 10;
+            const float mv = pp[0], lv = pp[1], ov = pp[2 + dl];
+            const float Mn = fmaxf(M, mv);
+            const float sc = __expf(M - Mn), e = __expf(mv - Mn);
+            Lh = fmaf(lv, e, Lh * sc);
+            acc = fmaf(ov, e, acc * sc);
+            M = Mn;
+        }
+        float Ma = fmaxf(M, xor_lane<8>(M));
+        {
+            float x = Ma, y = Ma;
+            swap16(x, y);
+            Ma = fmaxf(x, y);
+            x = Ma;
+            y = Ma;
+            swap32(x, y);
+            Ma = fmaxf(x, y);
+        }
+        const float sc = __expf(M - Ma);
+        Lh *= sc;
+        acc *= sc;
+        Lh += xor_lane<8>(Lh);
+        acc += xor_lane<8>(acc);
+        {
+            float x = Lh, y = Lh, u = acc, v = acc;
+            swap16(x, y);
+            swap16(u, v);
+            Lh = x + y;
+            acc = u + v;
+            x = Lh;
+            y = Lh;
+            u = acc;
+            v = acc;
+            swap32(x, y);
+            swap32(u, v);
+            Lh = x + y;
+            acc = u + v;
         }
         // the reference scales by 1/sum (qwen_asr_kernels.c:1091-1094); a
         // hardware reciprocal here
-        px_put_local(xm + h * 128 + d0 + lane, acc * __builtin_amdgcn_rcpf(Lh), T + 7u);
+        if (lane < 8) px_put_local(xm + h * 128 + d0 + lane, acc * __builtin_amdgcn_rcpf(Lh), T + 7u);
     }
     auto whole = [&](int i) { return xm + i; };
     return px_poll<4>(a, whole, 256, T + 7u, S.att, lane);
