@@ -153,6 +153,49 @@ __device__ bool px_poll(const qk_persist_args &a, Addr addr, int n, unsigned tag
     return true;
 }
 
+// SO rows (64 or 32) of 8 split-K partials each, the partial of XCD j at
+// p + j * stride, polled like px_poll and summed in XCD order in registers.
+// SO = 64: lane = row, 8 loads.  SO = 32: lane l polls XCDs 2 k + l / 32 of
+// row l % 32 and one permlane32 swap hands each pair (even, odd) to both
+// lanes of the row.  The row's sum lands in o of lane row (and row + 32).
+template <int SO>
+__device__ bool px_poll_rows(const qk_persist_args &a, const u64 *p, long stride, unsigned tag, int lane, float &o) {
+    static_assert(SO == 64 || SO == 32, "one or two lanes per row");
+    constexpr int NL = SO == 64 ? 8 : 4;
+    const u64 *q = SO == 64 ? p + lane : p + (lane >> 5) * stride + (lane & 31);
+    const long js = SO == 64 ? stride : 2 * stride;
+    const u64 t0 = wall_clock64();
+    for (unsigned spin = 1;; spin++) {
+        u64 w[NL];
+#pragma unroll
+        for (int j = 0; j < NL; j++) w[j] = px_get(q + j * js);
+        const u64 now = wall_clock64();
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < NL; j++) ok = ok && ((unsigned)(w[j] >> 32) == tag);
+        if (__all(ok)) {
+            if constexpr (SO == 64) {
+                o = __uint_as_float((unsigned)w[0]);
+#pragma unroll
+                for (int j = 1; j < 8; j++) o += __uint_as_float((unsigned)w[j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float ev = __uint_as_float((unsigned)w[j]), od = ev;
+                    swap32(ev, od);   // ev: XCD 2 j's partial, od: XCD 2 j + 1's, in both lanes of the row
+                    o = j == 0 ? ev + od : (o + ev) + od;
+                }
+            }
+            return true;
+        }
+        if (now - t0 > a.wait_ticks) {
+            if (lane == 0) px_raise(a.err, QK_PX_ERR_TIMEOUT);
+            return false;
+        }
+        if ((spin & 15u) == 0u && px_aborted(a.err)) return false;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // A slab of bf16 weight rows held in registers by the compute waves.  Lanes
 // form groups of LW; a group covers 8*LW consecutive columns per 16-byte load
@@ -421,14 +464,22 @@ __device__ bool px_x_update(const qk_persist_args &a, PxShared<H, I, NCW> &S, co
     constexpr int SO = PxShared<H, I, NCW>::SO;
     const int r = S.r;
     // this block's slice of the 8 split-K partials
-    auto slice = [&](int i) { return yp + (long)(i / SO) * H + SO * r + (i % SO); };
-    if (!px_poll<8 * SO / 64>(a, slice, 8 * SO, ty, S.ysum, lane)) return false;
-    if (tr_hop) *tr_hop = wall_clock64();
-    if (lane < SO) {
-        float o = S.ysum[lane];
+    if constexpr (SO == 64 || SO == 32) {
+        // summed in registers, XCD order
+        float o;
+        if (!px_poll_rows<SO>(a, yp + SO * r, H, ty, lane, o)) return false;
+        if (tr_hop) *tr_hop = wall_clock64();
+        if (lane < SO) px_put_local(xl + SO * r + lane, S.xs[SO * r + lane] + o, tx);   // x += o (qwen_asr_decoder.c:458, :468)
+    } else {
+        auto slice = [&](int i) { return yp + (long)(i / SO) * H + SO * r + (i % SO); };
+        if (!px_poll<8 * SO / 64>(a, slice, 8 * SO, ty, S.ysum, lane)) return false;
+        if (tr_hop) *tr_hop = wall_clock64();
+        if (lane < SO) {
+            float o = S.ysum[lane];
 #pragma unroll
-        for (int gg = 1; gg < QK_PX_XCD; gg++) o += S.ysum[gg * SO + lane];
-        px_put_local(xl + SO * r + lane, S.xs[SO * r + lane] + o, tx);   // x += o (qwen_asr_decoder.c:458, :468)
+            for (int gg = 1; gg < QK_PX_XCD; gg++) o += S.ysum[gg * SO + lane];
+            px_put_local(xl + SO * r + lane, S.xs[SO * r + lane] + o, tx);   // x += o (qwen_asr_decoder.c:458, :468)
+        }
     }
     // the XCD's whole new residual
     auto whole = [&](int i) { return xl + i; };
